@@ -1,0 +1,362 @@
+"""Benchmark of the fused layer kernels on one MI355X.
+
+Headline (the JSON line's `value`): the attention pre-block -- per-head q/k
+RMSNorm fused with IMROPE -- on config 2 of the benchmark definition:
+q [2048, 24, 256], k [2048, 4, 256] fp32, rotary 64 with sections
+[11,11,10,0], theta 1e7, positions 0..2047.  One step = one launch of
+bh_qk_norm_rope over the whole batch.  `value` = algorithmic HBM bytes per
+step / measured time, in GB/s.
+
+The line also carries, for every kernel family of the hot path, the achieved
+GB/s, fraction of the 8 TB/s HBM peak and rows/s ("kernels"), the roofline of
+the dominant kernel and a CPU baseline: the C restatement of the reference
+(oracle/) timed on this host, one core, on a bounded sample.
+
+Inputs are synthetic (config distributions), already resident in HBM when the
+timed region starts.  Buffer sets rotate so each config's working set exceeds
+the 256 MB Infinity Cache (MALL); otherwise repeated launches would be served
+from it and overstate HBM bandwidth.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+PKG_DIR = REPO / "ternary-bonsai-inference_amd"
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 600 * 2**20  # > 2x the 256 MB MALL
+
+
+def _load(name: str, path: Path):
+    if name in sys.modules:
+        return sys.modules[name]
+    is_pkg = path.name == "__init__.py"
+    spec = importlib.util.spec_from_file_location(
+        name, path, submodule_search_locations=[str(path.parent)] if is_pkg else None)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def n_sets(bytes_per_set: int, max_sets: int = 32) -> int:
+    return max(1, min(max_sets, -(-ROTATE_BYTES // max(1, bytes_per_set))))
+
+
+def time_launches(launch, n_rot: int, steps: int, warmup: int, stream) -> float:
+    """Average ms per launch, HIP events on the launch stream."""
+    import torch
+    for i in range(warmup):
+        launch(i % n_rot)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        launch(i % n_rot)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+# ---------------------------------------------------------------------------
+# workloads: each returns (launch(i), n_rot, algorithmic bytes, rows, info)
+# ---------------------------------------------------------------------------
+
+def wl_qk_norm_rope(bh, synth, dev, stream, n_tok=2048):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    nq, nk, hd = 24, 4, 256
+    bytes_per = (n_tok * nq * hd * 4 + n_tok * nk * hd * 4) * 2 + 2 * hd * 4
+    sets = []
+    for _ in range(n_sets(bytes_per)):
+        q = torch.randn((n_tok, nq, hd), device=dev, generator=g)
+        k = torch.randn((n_tok, nk, hd), device=dev, generator=g)
+        sets.append((q, torch.empty_like(q), k, torch.empty_like(k)))
+    wq = 1 + 0.1 * torch.randn(hd, device=dev, generator=g)
+    wk = 1 + 0.1 * torch.randn(hd, device=dev, generator=g)
+    pos = torch.from_numpy(synth.positions(n_tok)).to(dev)
+    args = [bh.make_qk_args(q, qo, k, ko, wq, wk, pos, n_tok, nq, nk) for q, qo, k, ko in sets]
+    sh = stream.cuda_stream
+    lib = bh.lib()
+    import ctypes
+    refs = [ctypes.byref(a) for a in args]
+
+    def launch(i):
+        st = lib.bh_qk_norm_rope(refs[i], sh)
+        if st:
+            bh.check(st)
+    keep = (sets, wq, wk, pos, args)
+    return launch, len(sets), bytes_per, n_tok, keep
+
+
+def wl_rms_rows(bh, synth, dev, stream, rows=512, row_len=5120):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    bytes_per = rows * row_len * 4 * 2 + row_len * 4
+    sets = [(torch.randn((rows, row_len), device=dev, generator=g),
+             torch.empty((rows, row_len), device=dev)) for _ in range(n_sets(bytes_per))]
+    w = 1 + 0.1 * torch.randn(row_len, device=dev, generator=g)
+    lib, sh = bh.lib(), stream.cuda_stream
+    n = rows * row_len
+
+    def launch(i):
+        x, y = sets[i]
+        st = lib.bh_rms_norm_rows(x.data_ptr(), n, w.data_ptr(), row_len, row_len, 1e-6,
+                                  y.data_ptr(), sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, rows, (sets, w)
+
+
+def wl_gdn_prep(bh, synth, dev, stream, n_tok=4096):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    C, H = 6144, 48
+    bytes_per = (n_tok * C * 4 * 2 + n_tok * H * 4 * 2 + 2 * H * 4 + n_tok * H * 4 * 2
+                 + n_tok * C * 4 * 3)
+    A = -torch.exp(2 * torch.rand(H, device=dev, generator=g))
+    bias = 0.5 * torch.randn(H, device=dev, generator=g)
+    sets = []
+    for _ in range(n_sets(bytes_per)):
+        conv = torch.randn((n_tok, C), device=dev, generator=g)
+        z = torch.randn((n_tok, C), device=dev, generator=g)
+        y = torch.randn((n_tok, C), device=dev, generator=g)
+        dt = torch.randn((n_tok, H), device=dev, generator=g)
+        beta = torch.randn((n_tok, H), device=dev, generator=g)
+        outs = [torch.empty_like(conv), torch.empty_like(z), torch.empty_like(dt),
+                torch.empty_like(beta)]
+        sets.append((conv, z, y, dt, beta, outs))
+    args = [bh.make_gdn_args(conv=c, conv_out=o[0], z=z, y=y, gated_out=o[1], alpha_raw=dt,
+                             dt_bias=bias, ssm_a=A, beta_raw=b, gate_out=o[2], beta_out=o[3],
+                             n_tok=n_tok, conv_dim=C, l2_dim=C, head_dim=128, inner_dim=C,
+                             n_v_head=H, gate_mode=bh.BH_SIGMOID_MUL, eps=1e-6)
+            for c, z, y, dt, b, o in sets]
+    import ctypes
+    refs = [ctypes.byref(a) for a in args]
+    lib, sh = bh.lib(), stream.cuda_stream
+
+    def launch(i):
+        st = lib.bh_gdn_prep_fused(refs[i], sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, n_tok, (sets, A, bias, args)
+
+
+def wl_softmax(bh, synth, dev, stream, rows, row_len, inv_t, causal=False, spikes=False):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(3 if spikes else 4)
+    bytes_per = rows * row_len * 4 * 2
+    sets = []
+    for _ in range(n_sets(bytes_per)):
+        x = torch.randn((rows, row_len), device=dev, generator=g) * (3.0 if spikes else 2.0)
+        if spikes:
+            x += 10.0 * (torch.rand((rows, row_len), device=dev, generator=g) < 0.01)
+        if causal:
+            q = torch.arange(rows, device=dev) % row_len
+            x.masked_fill_(torch.arange(row_len, device=dev)[None, :] > q[:, None],
+                           float("-inf"))
+        sets.append((x, torch.empty_like(x)))
+    lib, sh = bh.lib(), stream.cuda_stream
+    n = rows * row_len
+
+    def launch(i):
+        x, y = sets[i]
+        st = lib.bh_softmax_rows(x.data_ptr(), n, row_len, inv_t, y.data_ptr(), sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, rows, sets
+
+
+def wl_gather_rms(bh, synth, dev, stream, n_tok=8192, vocab=248320, ne0=5120):
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    table = synth.torch_pq2_table(vocab, ne0, dev, generator=g)
+    w = 1 + 0.1 * torch.randn(ne0, device=dev, generator=g)
+    rb = table.shape[1]
+    bytes_per = n_tok * rb + n_tok * 4 + ne0 * 4 + 2 * n_tok * ne0 * 4
+    sets = []
+    for _ in range(n_sets(2 * n_tok * ne0 * 4)):
+        ids = torch.randint(0, vocab, (n_tok,), device=dev, generator=g, dtype=torch.int32)
+        sets.append((ids, torch.empty((n_tok, ne0), device=dev),
+                     torch.empty((n_tok, ne0), device=dev)))
+    lib, sh = bh.lib(), stream.cuda_stream
+
+    def launch(i):
+        ids, e, nrm = sets[i]
+        st = lib.bh_pq2_embed_gather_rms(table.data_ptr(), ne0, vocab, ids.data_ptr(), n_tok,
+                                         w.data_ptr(), ne0, 1e-6, e.data_ptr(), nrm.data_ptr(),
+                                         None, sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, n_tok, (table, w, sets)
+
+
+def measure(name, wl, steps, warmup, stream, extra=None):
+    import torch
+    launch, n_rot, nbytes, rows, keep = wl
+    ms = time_launches(launch, n_rot, steps, warmup, stream)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    rec = {"kernel": name, "ms": round(ms, 5), "GBps": round(gbs, 1),
+           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "rows": rows,
+           "rows_per_s": round(rows / (ms * 1e-3), 1), "rotating_sets": n_rot}
+    if extra:
+        rec.update(extra)
+    del keep
+    torch.cuda.empty_cache()
+    return rec
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (C restatement of the reference), 1 thread
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(bh, synth, oracle, seconds: float):
+    """Time oracle.qk_norm_rope (src/forward.rs:237-270 restated) on the same
+    config, repeating the 2048-token batch until `seconds` have passed."""
+    import numpy as np
+    n_tok, nq, nk, hd = 2048, 24, 4, 256
+    r = synth.Rng(1)
+    q = r.normal(n_tok * nq * hd).reshape(n_tok, nq, hd)
+    k = r.normal(n_tok * nk * hd).reshape(n_tok, nk, hd)
+    wq, wk = r.normal(hd, 1.0, 0.1), r.normal(hd, 1.0, 0.1)
+    pos = synth.positions(n_tok)
+    nbytes = (q.nbytes + k.nbytes) * 2 + 2 * hd * 4
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.qk_norm_rope(q, k, wq, wk, pos, nq, nk, hd, 64, bh.SECTIONS, 1e7, 1e-6)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(nbytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"oracle qk_norm_rope on the full config-2 batch (2048 tokens x 28 heads),"
+                      f" {reps} repetitions in {el:.1f} s, 1 thread",
+            "rows_per_s": round(n_tok * reps / el, 1)}
+
+
+def load_traffic():
+    """HBM bytes per launch of the headline kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs, if they have been recorded."""
+    p = REPO / "profiles" / "traffic_qk_norm_rope.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the headline kernel (profiling runs)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="length of the CPU-baseline sample (0 disables)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(every kernel is row-independent: multi-GPU runs would shard rows with no "
+              "exchange)", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    bh = _load("bonsai_amd", PKG_DIR / "__init__.py")
+    synth = _load("bonsai_amd_synth", PKG_DIR / "synth.py")
+    dev = torch.device("cuda:0")
+    bh.lib()  # fail loudly if the HIP library is missing
+    stream = torch.cuda.Stream(device=dev)
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * 2**20 // 4
+        a = torch.randn(n, device=dev)
+        b = torch.empty_like(a)
+        with torch.cuda.stream(stream):
+            for _ in range(args.steps):
+                torch.mul(a, 1.0, out=b)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes_each_way": n * 4, "launches": args.steps}))
+        return 0
+
+    with torch.cuda.stream(stream):
+        head = measure("qk_norm_rope", wl_qk_norm_rope(bh, synth, dev, stream), args.steps,
+                       args.warmup, stream)
+        kernels = [head]
+        if not args.headline_only:
+            ksteps = max(10, args.steps // 4)
+            kernels += [
+                measure("rms_norm_rows T=512", wl_rms_rows(bh, synth, dev, stream, 512),
+                        ksteps, args.warmup, stream),
+                measure("rms_norm_rows T=2048", wl_rms_rows(bh, synth, dev, stream, 2048),
+                        ksteps, args.warmup, stream),
+                measure("rms_norm_rows T=8192", wl_rms_rows(bh, synth, dev, stream, 8192),
+                        ksteps, args.warmup, stream),
+                measure("gdn_prep_fused T=4096", wl_gdn_prep(bh, synth, dev, stream), ksteps,
+                        args.warmup, stream),
+                measure("softmax vocab [64,248320] temp 0.7",
+                        wl_softmax(bh, synth, dev, stream, 64, 248320,
+                                   float(1 / __import__("numpy").float32(0.7)), spikes=True),
+                        ksteps, args.warmup, stream),
+                measure("softmax causal [24*2048,2048]",
+                        wl_softmax(bh, synth, dev, stream, 24 * 2048, 2048, 1.0, causal=True),
+                        ksteps, args.warmup, stream),
+                measure("pq2_gather_rms T=8192", wl_gather_rms(bh, synth, dev, stream), ksteps,
+                        args.warmup, stream),
+            ]
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        oracle = _load("bonsai_oracle", REPO / "oracle" / "oracle.py")
+        cpu = cpu_baseline(bh, synth, oracle, args.cpu_seconds)
+
+    ms = head["ms"]
+    line = {
+        "metric": "achieved HBM GB/s (% of 8 TB/s) per fused kernel; rows/s at T=2048",
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (config distributions, torch RNG on device)",
+        "config": {"workload": "config 2: attention pre-block, q/k RMSNorm + IMROPE, "
+                               "q [2048,24,256] k [2048,4,256] fp32, n_rot 64, sections "
+                               "[11,11,10,0], theta 1e7, pos 0..2047",
+                   "tokens": 2048, "head_rows": 2048 * 28},
+        "rows_per_s": head["rows_per_s"],
+        "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(head["GBps"] / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic()},
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,265 @@
+/*
+ * bonsai_hip.h -- C ABI of the MI355X (gfx950) fused layer kernels of
+ * ternary-bonsai-inference.
+ *
+ * The reference engine is Rust; its hot-path kernels are free functions over
+ * f32 slices in src/kernels.rs and src/rope.rs.  Every entry point below
+ * replaces one of those functions (or one composition site of them in
+ * src/forward.rs) and cites it.  The ABI is plain C: pointers, sizes, scalars
+ * and an opaque stream handle, so a Rust `extern "C"` block binds it directly.
+ *
+ * Two families:
+ *   bh_*       device entry points.  Every pointer is DEVICE memory owned by
+ *              the caller; work is enqueued on `stream` (a hipStream_t, NULL =
+ *              the default stream) and the call returns without synchronising.
+ *   bh_host_*  host-slice mirrors with the exact Rust signatures: host
+ *              pointers in and out, the call copies to the GPU, runs the
+ *              device kernel and copies back before returning.
+ *
+ * Status codes: 0 on success, otherwise one of BH_ERR_*.  The message the
+ * Rust code would put in Err(String) is available from bh_last_error()
+ * (thread-local, valid until the next bh_* call on the same thread).
+ *
+ * Numerics follow the reference CPU path: f32 storage, f64 accumulation where
+ * the Rust accumulates in f64 (l2_norm_rows, softmax_rows), libm-accurate
+ * expf/logf/sinf/cosf, no FMA contraction.  The PQ2_0 decode is bit-exact.
+ *
+ * Threading: every device entry point is re-entrant per stream, except
+ * bh_softmax_rows on rows too wide for one workgroup, which uses a per-device
+ * scratch buffer and must not run concurrently with itself on one device.
+ */
+#ifndef BONSAI_HIP_H
+#define BONSAI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BH_OK 0
+#define BH_ERR_SHAPE (-1) /* the Rust Err(String) shape checks            */
+#define BH_ERR_RANGE (-2) /* token id >= n_rows (src/weights.rs:337-341)    */
+#define BH_ERR_HIP (-3)   /* HIP runtime failure (launch, copy, malloc)     */
+#define BH_ERR_ARG (-4)   /* NULL pointer, unknown mode, unsupported layout */
+
+/* Opaque stream handle: a hipStream_t.  NULL selects the default stream. */
+typedef void *bh_stream;
+
+/* Message of the last failing call on this thread ("" after a success). */
+const char *bh_last_error(void);
+/* Library identification string (version, target architecture). */
+const char *bh_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Normalisation (src/kernels.rs:58-145)
+ * ------------------------------------------------------------------------- */
+
+/* kernels::rms_norm (src/kernels.rs:59-75) and rms_norm_inplace (:80-93):
+ * out = x * (1/sqrt(mean(x^2) + eps)) * w over one vector of n.  out may
+ * equal x (in place).  n == 0 is a no-op. */
+int bh_rms_norm(const float *x, const float *w, size_t n, float eps, float *out,
+                bh_stream stream);
+
+/* kernels::rms_norm_rows (src/kernels.rs:97-122): RMSNorm of each of the
+ * x_len/row_len consecutive rows with the shared weight w[row_len].
+ * BH_ERR_SHAPE when w_len != row_len or x_len % row_len != 0. */
+int bh_rms_norm_rows(const float *x, size_t x_len, const float *w, size_t w_len,
+                     size_t row_len, float eps, float *out, bh_stream stream);
+
+/* Residual add + RMSNorm, the composition at src/forward.rs:708-713
+ * (cur[i] += attn_out[i]; ffn_in = rms_norm(cur, post_w, eps)), per row:
+ * sum_out = x + residual; out = rms_norm_rows(sum_out, w, row_len, eps).
+ * sum_out may alias x (the in-place `cur +=` of the reference). */
+int bh_add_rms_norm_rows(const float *x, const float *residual, size_t x_len,
+                         const float *w, size_t w_len, size_t row_len, float eps,
+                         float *sum_out, float *out, bh_stream stream);
+
+/* kernels::l2_norm_rows (src/kernels.rs:126-145): per row, f64 sum of x^2,
+ * scale = 1 / max(sqrt((f32)sum), eps), out = x * scale. */
+int bh_l2_norm_rows(const float *x, size_t x_len, size_t row_len, float eps,
+                    float *out, bh_stream stream);
+
+/* SiLU then L2 rows: the conv output path of src/forward.rs:524 (silu) and
+ * :539-540 (l2_norm_rows) fused: out = l2_norm_rows(silu(x), row_len, eps). */
+int bh_silu_l2_norm_rows(const float *x, size_t x_len, size_t row_len, float eps,
+                         float *out, bh_stream stream);
+
+/* ---------------------------------------------------------------------------
+ * Activations (src/kernels.rs:148-171; shaders/elem.comp modes 0-4)
+ * ------------------------------------------------------------------------- */
+
+#define BH_SILU 0        /* kernels::silu     x / (1 + exp(-x))               */
+#define BH_SIGMOID 1     /* kernels::sigmoid  1 / (1 + exp(-x))               */
+#define BH_SOFTPLUS 2    /* kernels::softplus x > 20 ? x : ln(1 + exp(x))     */
+#define BH_SILU_MUL 3    /* b * silu(a): FFN gate-up (src/forward.rs:574),
+                            GDN output gate (src/forward.rs:549-551)          */
+#define BH_SIGMOID_MUL 4 /* b * sigmoid(a): attention gate
+                            (src/forward.rs:379-382)                         */
+
+/* kernels::map_inplace(x, f) (src/kernels.rs:167-171) for modes 0-2 (b is
+ * ignored and may be NULL), and the fused gated products for modes 3-4.
+ * out may alias a or b. */
+int bh_unary(int mode, const float *a, const float *b, size_t n, float *out,
+             bh_stream stream);
+
+/* GDN gate prep (src/forward.rs:497-507), n_tok x n_head:
+ *   beta_out = sigmoid(beta_raw)
+ *   gate_out = softplus(alpha_raw + dt_bias[h]) * ssm_a[h]
+ * dt_bias and ssm_a have n_head entries.  Either output may be NULL (then
+ * its inputs are not read). */
+int bh_gdn_gate_prep(const float *alpha_raw, const float *dt_bias,
+                     const float *ssm_a, const float *beta_raw, size_t n_tok,
+                     size_t n_head, float *gate_out, float *beta_out,
+                     bh_stream stream);
+
+/* All of the recurrent layer's small ops for n_tok tokens in ONE launch
+ * (src/forward.rs:497-507, 524, 539-540, 549-551 / :379-382):
+ *   conv_out[t]  = silu(conv[t]); its first l2_dim channels are then
+ *                  l2-normalised per head_dim group (q and k heads);
+ *   gated_out[t] = y[t] * silu(z[t])    (gate_mode BH_SILU_MUL, GDN) or
+ *                  y[t] * sigmoid(z[t]) (gate_mode BH_SIGMOID_MUL, attention);
+ *   gate_out[t]  = softplus(alpha_raw[t] + dt_bias) * ssm_a;
+ *   beta_out[t]  = sigmoid(beta_raw[t]).
+ * Each group is skipped when its output pointer is NULL. */
+typedef struct bh_gdn_prep_args {
+  const float *conv;  /* [n_tok][conv_dim]                          */
+  float *conv_out;    /* [n_tok][conv_dim], may alias conv          */
+  const float *z;     /* [n_tok][inner_dim] gate pre-activation     */
+  const float *y;     /* [n_tok][inner_dim] gated tensor            */
+  float *gated_out;   /* [n_tok][inner_dim], may alias y or z       */
+  const float *alpha_raw; /* [n_tok][n_v_head]                      */
+  const float *dt_bias;   /* [n_v_head]                             */
+  const float *ssm_a;     /* [n_v_head]                             */
+  const float *beta_raw;  /* [n_tok][n_v_head]                      */
+  float *gate_out;        /* [n_tok][n_v_head]                      */
+  float *beta_out;        /* [n_tok][n_v_head]                      */
+  size_t n_tok;
+  size_t conv_dim;  /* channels per token row of conv            */
+  size_t l2_dim;    /* leading channels that get the L2 norm     */
+  size_t head_dim;  /* L2 group width (128 in Ternary-Bonsai-27B) */
+  size_t inner_dim; /* width of z / y                            */
+  size_t n_v_head;  /* 48 in Ternary-Bonsai-27B                  */
+  int gate_mode;    /* BH_SILU_MUL or BH_SIGMOID_MUL             */
+  float eps;
+} bh_gdn_prep_args;
+
+int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream);
+
+/* ---------------------------------------------------------------------------
+ * Softmax (src/kernels.rs:175-202; temperature: src/sampler.rs:85, 110)
+ * ------------------------------------------------------------------------- */
+
+/* out = softmax_rows(x * inv_temp, row_len): per row, max in f32,
+ * e = expf(v - max), f64 sum, out = e * (1 / (f32)sum).  -inf entries give 0.
+ * inv_temp = 1.0f is the plain kernels::softmax_rows; the sampler passes
+ * 1.0f / temp.  BH_ERR_SHAPE when x_len % row_len != 0. */
+int bh_softmax_rows(const float *x, size_t x_len, size_t row_len,
+                    float inv_temp, float *out, bh_stream stream);
+
+/* ---------------------------------------------------------------------------
+ * Rotary embedding (src/rope.rs:9-70)
+ * ------------------------------------------------------------------------- */
+
+/* rope::rope_imrope over every head of n_tok tokens, in place:
+ * heads[t][h][0..head_dim), positions pos[t][0..4) = (p_t, p_h, p_w, p_e).
+ * theta_scale = powf(freq_base, -2/n_dims) is evaluated on the host with the
+ * C library, and theta for pair j is the chain p * theta_scale * ... (j
+ * multiplies in f32), as in the reference loop.  n_dims must be even and
+ * <= head_dim. */
+int bh_rope_imrope(float *heads, size_t n_tok, size_t n_head, size_t head_dim,
+                   const int32_t *pos, size_t n_dims, const int32_t sections[4],
+                   float freq_base, bh_stream stream);
+
+/* Attention pre-block, fused (src/forward.rs:237-270):
+ *   q_out = rope_imrope(rms_norm_rows(q, wq, head_dim, eps))
+ *   k_out = rope_imrope(rms_norm_rows(k, wk, head_dim, eps))
+ * q heads are read with stride q_head_stride floats: head_dim for a plain
+ * [n_tok][n_q_head][head_dim] tensor, 2*head_dim for the fused attn_q output
+ * whose rows are [q | gate] per head (src/forward.rs:237-241).  With
+ * gate_out != NULL (requires q_head_stride == 2*head_dim) the gate half is
+ * split out and passed through sigmoid (src/forward.rs:379):
+ * gate_out[t][h] = sigmoid(gate).  k may be NULL when n_k_head == 0. */
+typedef struct bh_qk_norm_rope_args {
+  const float *q;      /* [n_tok][n_q_head][q_head_stride]  */
+  float *q_out;        /* [n_tok][n_q_head][head_dim]       */
+  float *gate_out;     /* [n_tok][n_q_head][head_dim] or NULL */
+  const float *k;      /* [n_tok][n_k_head][head_dim]       */
+  float *k_out;        /* [n_tok][n_k_head][head_dim]       */
+  const float *wq;     /* [head_dim] attn_q_norm.weight     */
+  const float *wk;     /* [head_dim] attn_k_norm.weight     */
+  const int32_t *pos;  /* [n_tok][4] (p_t, p_h, p_w, p_e)   */
+  size_t n_tok, n_q_head, n_k_head, head_dim, q_head_stride, n_dims;
+  int32_t sections[4];
+  float freq_base;
+  float eps;
+} bh_qk_norm_rope_args;
+
+int bh_qk_norm_rope(const bh_qk_norm_rope_args *args, bh_stream stream);
+
+/* ---------------------------------------------------------------------------
+ * PQ2_0 ternary embedding rows (src/kernels.rs:204-229, src/gguf.rs:881-911)
+ * ------------------------------------------------------------------------- */
+
+/* kernels::pq2_row_bytes (src/kernels.rs:209-211): ceil(ne0/128) * 34. */
+size_t bh_pq2_row_bytes(size_t ne0);
+
+/* Batched Weights::row_f32 on a PQ2_0 tensor (src/weights.rs:333-349,
+ * src/prefill.rs:143-154): out[i] = decode_pq2_0_row(table row ids[i]),
+ * bit-exact.  table holds n_rows rows of bh_pq2_row_bytes(ne0) bytes.  An id
+ * >= n_rows yields a zero row and, when bad_id != NULL, its value is stored
+ * to *bad_id (device word; the caller presets it, e.g. to 0xFFFFFFFF, and
+ * reads it after the stream completes). */
+int bh_pq2_embed_gather(const uint8_t *table, size_t ne0, size_t n_rows,
+                        const uint32_t *ids, size_t n_ids, float *out,
+                        uint32_t *bad_id, bh_stream stream);
+
+/* Embedding gather fused with the first RMSNorm (src/forward.rs:691, 701-702):
+ * out_embed[i] = decode_pq2_0_row(row ids[i])      (bit-exact, the residual)
+ * out_norm[i]  = rms_norm(out_embed[i], w, eps)    (blk.0.attn_norm)
+ * BH_ERR_SHAPE when w_len != ne0. */
+int bh_pq2_embed_gather_rms(const uint8_t *table, size_t ne0, size_t n_rows,
+                            const uint32_t *ids, size_t n_ids, const float *w,
+                            size_t w_len, float eps, float *out_embed,
+                            float *out_norm, uint32_t *bad_id, bh_stream stream);
+
+/* ---------------------------------------------------------------------------
+ * Host-slice mirrors: the Rust signatures, host memory in and out.  Outputs
+ * are caller-allocated with the length the Rust function would return.
+ * ------------------------------------------------------------------------- */
+
+/* kernels::rms_norm (src/kernels.rs:59); w has n entries. */
+int bh_host_rms_norm(const float *x, size_t n, const float *w, float eps,
+                     float *out);
+/* kernels::rms_norm_rows (src/kernels.rs:97); out has x_len entries. */
+int bh_host_rms_norm_rows(const float *x, size_t x_len, const float *w,
+                          size_t w_len, size_t row_len, float eps, float *out);
+/* kernels::l2_norm_rows (src/kernels.rs:126). */
+int bh_host_l2_norm_rows(const float *x, size_t x_len, size_t row_len,
+                         float eps, float *out);
+/* kernels::map_inplace(x, silu|sigmoid|softplus) (src/kernels.rs:167). */
+int bh_host_map_inplace(float *x, size_t n, int mode);
+/* kernels::softmax_rows (src/kernels.rs:175). */
+int bh_host_softmax_rows(const float *x, size_t x_len, size_t row_len,
+                         float *out);
+/* rope::rope_imrope on one head (src/rope.rs:9), in place. */
+int bh_host_rope_imrope(float *head, size_t head_len, int64_t p_t, int64_t p_h,
+                        int64_t p_w, int64_t p_e, size_t n_dims,
+                        const int32_t sections[4], float freq_base);
+/* kernels::decode_pq2_0_row (src/kernels.rs:214); raw has raw_len bytes
+ * (>= bh_pq2_row_bytes(ne0)); out has ne0 entries. */
+int bh_host_decode_pq2_0_row(const uint8_t *raw, size_t raw_len, size_t ne0,
+                             float *out);
+/* prefill::batch_embed (src/prefill.rs:143) over a PQ2_0 payload of n_rows
+ * rows: out[k] = row_f32(tokens[k]); BH_ERR_RANGE on a token >= n_rows with
+ * the message of src/weights.rs:337-341. */
+int bh_host_batch_embed(const uint8_t *payload, size_t payload_len, size_t ne0,
+                        size_t n_rows, const uint32_t *tokens, size_t n_tok,
+                        float *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BONSAI_HIP_H */

@@ -1,0 +1,228 @@
+"""ctypes binding of oracle/liboracle.so (the C restatement in oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the checker the HIP library is compared against.
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it.
+
+Arrays are numpy; every function returns new arrays.  Each wraps the C
+function of the same name, which cites the reference source it restates.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "liboracle.so"
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_f = ctypes.c_float
+_i64 = ctypes.c_int64
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+_SIG = {
+    "or_half_to_f32": (_f, [ctypes.c_uint16]),
+    "or_f32_to_half": (ctypes.c_uint16, [_f]),
+    "or_half_to_f32_n": (None, [_vp, _sz, _vp]),
+    "or_f32_to_half_n": (None, [_vp, _sz, _vp]),
+    "or_silu": (_f, [_f]),
+    "or_softplus": (_f, [_f]),
+    "or_sigmoid": (_f, [_f]),
+    "or_unary": (None, [ctypes.c_int, _vp, _vp, _sz, _vp]),
+    "or_rms_norm": (None, [_vp, _sz, _vp, _f, _vp]),
+    "or_rms_norm_rows": (ctypes.c_int, [_vp, _sz, _vp, _sz, _sz, _f, _vp]),
+    "or_add_rms_norm_rows": (ctypes.c_int, [_vp, _vp, _sz, _vp, _sz, _sz, _f, _vp, _vp]),
+    "or_l2_norm_rows": (ctypes.c_int, [_vp, _sz, _sz, _f, _vp]),
+    "or_softmax_rows": (ctypes.c_int, [_vp, _sz, _sz, _f, _vp]),
+    "or_rope_imrope": (None, [_vp, _sz, _i64, _i64, _i64, _i64, _sz, _i32p, _f]),
+    "or_qk_norm_rope": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz,
+                                       _sz, _sz, _sz, _i32p, _f, _f]),
+    "or_pq2_row_bytes": (_sz, [_sz]),
+    "or_decode_pq2_0_row": (None, [_vp, _sz, _vp]),
+    "or_embed_gather": (ctypes.c_int, [_vp, _sz, _sz, _vp, _sz, _vp, _f, _vp, _vp, _vp]),
+    "or_gdn_gate_prep": (None, [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp]),
+    "or_silu_l2_part": (ctypes.c_int, [_vp, _sz, _sz, _sz, _sz, _f, _vp]),
+}
+
+_LIB = None
+
+
+class OracleShapeError(ValueError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(f"{LIB_PATH} missing: run `make -C oracle`")
+        h = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIG.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = h
+    return _LIB
+
+
+def _c(a, dtype=np.float32):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _sections(s):
+    return (ctypes.c_int32 * 4)(*s)
+
+
+def _st(code: int, what: str):
+    if code == -1:
+        raise OracleShapeError(what)
+    if code == -2:
+        raise IndexError(what)
+
+
+def half_to_f32(h) -> np.ndarray:
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().or_half_to_f32_n(_p(h), h.size, _p(out))
+    return out
+
+
+def f32_to_half(v) -> np.ndarray:
+    v = _c(v)
+    out = np.empty(v.shape, np.uint16)
+    lib().or_f32_to_half_n(_p(v), v.size, _p(out))
+    return out
+
+
+def silu(x: float) -> float:
+    return lib().or_silu(x)
+
+
+def softplus(x: float) -> float:
+    return lib().or_softplus(x)
+
+
+def sigmoid(x: float) -> float:
+    return lib().or_sigmoid(x)
+
+
+def unary(mode: int, a, b=None) -> np.ndarray:
+    a = _c(a)
+    b = None if b is None else _c(b)
+    out = np.empty_like(a)
+    lib().or_unary(mode, _p(a), _p(b), a.size, _p(out))
+    return out
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    x, w = _c(x), _c(w)
+    out = np.empty_like(x)
+    lib().or_rms_norm(_p(x), x.size, _p(w), eps, _p(out))
+    return out
+
+
+def rms_norm_rows(x, w, row_len: int, eps: float) -> np.ndarray:
+    x, w = _c(x), _c(w)
+    out = np.empty_like(x)
+    _st(lib().or_rms_norm_rows(_p(x), x.size, _p(w), w.size, row_len, eps, _p(out)),
+        "rms_norm_rows shape")
+    return out
+
+
+def add_rms_norm_rows(x, r, w, row_len: int, eps: float):
+    x, r, w = _c(x), _c(r), _c(w)
+    s = np.empty_like(x)
+    out = np.empty_like(x)
+    _st(lib().or_add_rms_norm_rows(_p(x), _p(r), x.size, _p(w), w.size, row_len, eps, _p(s),
+                                   _p(out)), "add_rms_norm_rows shape")
+    return s, out
+
+
+def l2_norm_rows(x, row_len: int, eps: float) -> np.ndarray:
+    x = _c(x)
+    out = np.empty_like(x)
+    _st(lib().or_l2_norm_rows(_p(x), x.size, row_len, eps, _p(out)), "l2_norm_rows shape")
+    return out
+
+
+def softmax_rows(x, row_len: int, inv_temp: float = 1.0) -> np.ndarray:
+    x = _c(x)
+    out = np.empty_like(x)
+    _st(lib().or_softmax_rows(_p(x), x.size, row_len, inv_temp, _p(out)), "softmax_rows shape")
+    return out
+
+
+def rope_imrope(head, p_t, p_h, p_w, p_e, n_dims, sections, freq_base) -> np.ndarray:
+    h = _c(head).copy()
+    lib().or_rope_imrope(_p(h), h.size, p_t, p_h, p_w, p_e, n_dims, _sections(sections),
+                         freq_base)
+    return h
+
+
+def qk_norm_rope(q, k, wq, wk, pos, n_q_head, n_k_head, head_dim, n_dims, sections,
+                 freq_base, eps, q_head_stride=None, want_gate=False):
+    q, wq, pos = _c(q), _c(wq), _c(pos, np.int32)
+    n_tok = pos.shape[0]
+    stride = head_dim if q_head_stride is None else q_head_stride
+    q_out = np.empty((n_tok, n_q_head, head_dim), np.float32)
+    gate = np.empty_like(q_out) if want_gate else None
+    if n_k_head:
+        k, wk = _c(k), _c(wk)
+        k_out = np.empty((n_tok, n_k_head, head_dim), np.float32)
+    else:
+        k = wk = k_out = None
+    _st(lib().or_qk_norm_rope(_p(q), _p(q_out), _p(gate), _p(k), _p(k_out), _p(wq), _p(wk),
+                              _p(pos), n_tok, n_q_head, n_k_head, head_dim, stride, n_dims,
+                              _sections(sections), freq_base, eps), "qk_norm_rope shape")
+    return q_out, k_out, gate
+
+
+def pq2_row_bytes(ne0: int) -> int:
+    return int(lib().or_pq2_row_bytes(ne0))
+
+
+def decode_pq2_0_row(raw, ne0: int) -> np.ndarray:
+    raw = _c(raw, np.uint8)
+    if raw.size < pq2_row_bytes(ne0):
+        raise OracleShapeError("raw row too short")
+    out = np.empty(ne0, np.float32)
+    lib().or_decode_pq2_0_row(_p(raw), ne0, _p(out))
+    return out
+
+
+def embed_gather(table, ne0: int, n_rows: int, tokens, w=None, eps: float = 1e-6):
+    table = _c(table, np.uint8)
+    tokens = _c(tokens, np.uint32)
+    out = np.empty((tokens.size, ne0), np.float32)
+    out_norm = np.empty_like(out) if w is not None else None
+    wv = _c(w) if w is not None else None
+    bad = np.zeros(1, np.uint32)
+    _st(lib().or_embed_gather(_p(table), ne0, n_rows, _p(tokens), tokens.size, _p(wv), eps,
+                              _p(out), _p(out_norm), _p(bad)),
+        f"row {int(bad[0])} out of range (n_rows {n_rows})")
+    return (out, out_norm) if w is not None else out
+
+
+def gdn_gate_prep(alpha_raw, dt_bias, ssm_a, beta_raw):
+    alpha_raw, dt_bias, ssm_a, beta_raw = map(_c, (alpha_raw, dt_bias, ssm_a, beta_raw))
+    n_tok, n_head = alpha_raw.shape
+    gate = np.empty_like(alpha_raw)
+    beta = np.empty_like(beta_raw)
+    lib().or_gdn_gate_prep(_p(alpha_raw), _p(dt_bias), _p(ssm_a), _p(beta_raw), n_tok, n_head,
+                           _p(gate), _p(beta))
+    return gate, beta
+
+
+def silu_l2_part(conv, l2_dim: int, head_dim: int, eps: float) -> np.ndarray:
+    conv = _c(conv)
+    n_tok, conv_dim = conv.shape
+    out = np.empty_like(conv)
+    _st(lib().or_silu_l2_part(_p(conv), n_tok, conv_dim, l2_dim, head_dim, eps, _p(out)),
+        "silu_l2_part shape")
+    return out

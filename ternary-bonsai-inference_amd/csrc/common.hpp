@@ -1,0 +1,142 @@
+// Shared host and device helpers of the bonsai HIP library (gfx950 only).
+//
+// Host side: status/last-error plumbing and launch checking.
+// Device side: wave64 / workgroup reductions for "row groups" of G lanes and
+// the scalar functions of the reference (src/kernels.rs:148-164,
+// src/gguf.rs:881-911) written so that the GPU result matches the x86 build
+// of the reference.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/bonsai_hip.h"
+
+namespace bh {
+
+// ---------------------------------------------------------------------------
+// Host: status plumbing
+// ---------------------------------------------------------------------------
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const std::string &msg);
+// Clears the last error and returns BH_OK.
+int ok();
+// Converts the result of a launch (hipGetLastError) into a status.
+int check_launch(const char *what);
+// Converts an arbitrary HIP call result into a status.
+int check_hip(hipError_t e, const char *what);
+
+inline hipStream_t as_stream(bh_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Smallest power of two >= v (v >= 1).
+inline int pow2ceil(size_t v) {
+  int p = 1;
+  while (static_cast<size_t>(p) < v) p <<= 1;
+  return p;
+}
+
+// Per-device scratch owned by the library (grown on demand, never shrunk).
+// Used only by the split-row softmax.  Returns nullptr on allocation failure
+// (the status is already recorded).
+void *device_scratch(size_t bytes);
+
+// ---------------------------------------------------------------------------
+// Device: reductions
+// ---------------------------------------------------------------------------
+
+struct SumOp {
+  template <class T> __device__ T operator()(T a, T b) const { return a + b; }
+};
+// max that ignores NaN in the candidate, like the reference's `if v > max`.
+struct MaxOp {
+  __device__ float operator()(float a, float b) const { return b > a ? b : a; }
+};
+
+// Reduce `v` over a group of G consecutive lanes (G a power of two <= 1024).
+// Groups of up to 64 lanes live in one wave and reduce with cross-lane
+// shuffles only; larger groups span G/64 waves of the block and combine the
+// per-wave values through `lds` (blockDim.x/64 entries), in wave order, so
+// every lane of the group gets the same bits.  Every thread of the block must
+// call this (it contains a barrier when G > 64).
+template <int G, class T, class Op>
+__device__ __forceinline__ T group_reduce(T v, Op op, T *lds) {
+  constexpr int W = G < 64 ? G : 64;
+#pragma unroll
+  for (int off = W / 2; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+  if constexpr (G > 64) {
+    constexpr int WPG = G / 64;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) lds[wave] = v;
+    __syncthreads();
+    const int first = (wave / WPG) * WPG;
+    T r = lds[first];
+#pragma unroll
+    for (int i = 1; i < WPG; ++i) r = op(r, lds[first + i]);
+    v = r;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Device: scalar functions of the reference
+// ---------------------------------------------------------------------------
+
+// kernels::silu (src/kernels.rs:148-150)
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+// kernels::sigmoid (src/kernels.rs:162-164)
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// kernels::softplus (src/kernels.rs:153-159): ln(1 + e^x), identity above 20
+__device__ __forceinline__ float softplus(float x) {
+  return x > 20.0f ? x : logf(1.0f + expf(x));
+}
+
+// gguf::half_to_f32 (src/gguf.rs:881-911) in integer arithmetic: exact for
+// every one of the 65536 patterns, NaN payloads kept (no quieting).
+__device__ __forceinline__ uint32_t half_bits_to_f32_bits(uint32_t h) {
+  const uint32_t sign = (h >> 15) & 1u;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  const uint32_t man = h & 0x3ffu;
+  if (exp == 0u) {
+    if (man == 0u) return sign << 31;
+    // subnormal: shift the mantissa up until bit 10 is set
+    const uint32_t nbits = 32u - __clz(man);  // 1..10
+    const uint32_t k = 11u - nbits;
+    const uint32_t e = 113u - k;
+    return (sign << 31) | (e << 23) | (((man << k) & 0x3ffu) << 13);
+  }
+  if (exp == 0x1fu) return (sign << 31) | 0x7f800000u | (man << 13);
+  return (sign << 31) | ((exp + 112u) << 23) | (man << 13);
+}
+
+// One PQ2_0 weight: (code - 1) * scale with the IEEE product an x86 SSE
+// multiply gives (src/kernels.rs:226).  The finite case is a single exact
+// multiply; the two non-finite scale cases are spelled out because the GPU
+// and SSE return different NaN bit patterns: a NaN scale comes back quieted
+// with its payload, and 0 * inf is SSE's default NaN 0xFFC00000.
+__device__ __forceinline__ float pq2_weight(uint32_t code, float scale, bool finite) {
+  const float v = static_cast<float>(static_cast<int>(code) - 1) * scale;
+  if (finite) return v;
+  const uint32_t sb = __float_as_uint(scale);
+  if ((sb & 0x7fffffu) != 0u) return __uint_as_float(sb | 0x00400000u);  // NaN
+  if (code == 1u) return __uint_as_float(0xffc00000u);                   // 0*inf
+  return v;                                                              // +-inf
+}
+
+}  // namespace bh
+
+// Launch helper: bounds-checked grid, returns a status from the enclosing fn.
+#define BH_LAUNCH(kernel, grid, block, shmem, stream, ...)                   \
+  do {                                                                       \
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(block), shmem, stream,       \
+                       __VA_ARGS__);                                         \
+    int _st = ::bh::check_launch(#kernel);                                   \
+    if (_st != BH_OK) return _st;                                            \
+  } while (0)

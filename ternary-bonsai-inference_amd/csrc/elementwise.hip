@@ -1,0 +1,350 @@
+// Activations and the gated-delta-net gate prep for gfx950.
+//
+//   bh_unary            kernels::map_inplace(silu|sigmoid|softplus)
+//                       (src/kernels.rs:148-171) and the gated products of
+//                       shaders/elem.comp modes 3/4 (src/forward.rs:574, 549-551, 379-382)
+//   bh_gdn_gate_prep    beta = sigmoid, gate = softplus(alpha + dt_bias) * ssm_a
+//                       (src/forward.rs:497-507)
+//   bh_gdn_prep_fused   every small op of a recurrent layer for a batch of
+//                       tokens, one launch (src/forward.rs:497-551)
+//
+// All of these are streaming, HBM-bound maps.  The elementwise kernel gives
+// every block a contiguous run of 4 x 256 float4 (16 KB per input), issued as
+// four independent 16-byte loads per lane before any math.  The fused gate
+// prep gives one block one token: the token's conv row (silu, then L2 per
+// head of head_dim lanes-groups reduced with shuffles in f64, as
+// src/kernels.rs:134-140), its z/y gate row and its n_v_head scalar gates,
+// so a recurrent layer's prep is a single pass over its inputs.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "common.hpp"
+
+namespace bh {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+template <int MODE>
+__device__ __forceinline__ float unary_op(float a, float b) {
+  if constexpr (MODE == BH_SILU) return silu(a);
+  if constexpr (MODE == BH_SIGMOID) return sigmoid(a);
+  if constexpr (MODE == BH_SOFTPLUS) return softplus(a);
+  // src/forward.rs:549-551 `normed[i] *= silu(z[i])` and :574 silu(g) * u;
+  // the product is commutative, so b * act(a) has the reference's bits.
+  if constexpr (MODE == BH_SILU_MUL) return b * silu(a);
+  if constexpr (MODE == BH_SIGMOID_MUL) return b * sigmoid(a);
+  return a;
+}
+
+template <int MODE>
+__device__ __forceinline__ float4 unary_op4(float4 a, float4 b) {
+  return make_float4(unary_op<MODE>(a.x, b.x), unary_op<MODE>(a.y, b.y),
+                     unary_op<MODE>(a.z, b.z), unary_op<MODE>(a.w, b.w));
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void unary_vec_kernel(const float *a, const float *b,
+                                                           float *out, size_t n) {
+  constexpr bool BIN = MODE == BH_SILU_MUL || MODE == BH_SIGMOID_MUL;
+  const size_t n4 = n >> 2;
+  const size_t base = static_cast<size_t>(blockIdx.x) * (kBlock * kUnroll) + threadIdx.x;
+  const float4 *a4 = reinterpret_cast<const float4 *>(a);
+  const float4 *b4 = reinterpret_cast<const float4 *>(b);
+  float4 *o4 = reinterpret_cast<float4 *>(out);
+  float4 va[kUnroll], vb[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const size_t i = base + u * kBlock;
+    va[u] = i < n4 ? a4[i] : make_float4(0, 0, 0, 0);
+    if constexpr (BIN) vb[u] = i < n4 ? b4[i] : make_float4(0, 0, 0, 0);
+    else vb[u] = va[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const size_t i = base + u * kBlock;
+    if (i < n4) o4[i] = unary_op4<MODE>(va[u], vb[u]);
+  }
+  // scalar tail (n % 4 elements), done by the first lanes of block 0
+  if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+    const size_t i = n4 * 4 + threadIdx.x;
+    out[i] = unary_op<MODE>(a[i], BIN ? b[i] : 0.0f);
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void unary_scalar_kernel(const float *a, const float *b,
+                                                              float *out, size_t n) {
+  constexpr bool BIN = MODE == BH_SILU_MUL || MODE == BH_SIGMOID_MUL;
+  const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < n) out[i] = unary_op<MODE>(a[i], BIN ? b[i] : 0.0f);
+}
+
+template <int MODE>
+int unary_launch(const float *a, const float *b, float *out, size_t n, hipStream_t st) {
+  constexpr bool BIN = MODE == BH_SILU_MUL || MODE == BH_SIGMOID_MUL;
+  const bool vec = aligned16(a) && aligned16(out) && (!BIN || aligned16(b));
+  if (vec) {
+    const size_t per_block = static_cast<size_t>(kBlock) * kUnroll;
+    size_t blocks = ((n >> 2) + per_block - 1) / per_block;
+    if (blocks == 0) blocks = 1;  // tail only
+    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "unary: n too large");
+    BH_LAUNCH((unary_vec_kernel<MODE>), static_cast<unsigned>(blocks), kBlock, 0, st, a, b, out,
+              n);
+  } else {
+    const size_t blocks = (n + kBlock - 1) / kBlock;
+    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "unary: n too large");
+    BH_LAUNCH((unary_scalar_kernel<MODE>), static_cast<unsigned>(blocks), kBlock, 0, st, a, b,
+              out, n);
+  }
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// GDN gate prep
+// ---------------------------------------------------------------------------
+
+struct GdnParams {
+  const float *conv;
+  float *conv_out;
+  const float *z;
+  const float *y;
+  float *gated_out;
+  const float *alpha_raw;
+  const float *dt_bias;
+  const float *ssm_a;
+  const float *beta_raw;
+  float *gate_out;
+  float *beta_out;
+  int conv_dim, l2_dim, head_dim, inner_dim, n_v_head;
+  int sigmoid_gate;  // 1: y * sigmoid(z), 0: y * silu(z)
+  float eps;
+};
+
+// src/forward.rs:501-507: beta = sigmoid(beta_raw); gate = softplus(alpha_raw
+// + dt_bias) * ssm_a, one (token, head) per call.
+__device__ __forceinline__ void small_gates(const GdnParams &a, size_t idx, int h) {
+  if (a.beta_out != nullptr) a.beta_out[idx] = sigmoid(a.beta_raw[idx]);
+  if (a.gate_out != nullptr) a.gate_out[idx] = softplus(a.alpha_raw[idx] + a.dt_bias[h]) * a.ssm_a[h];
+}
+
+__global__ __launch_bounds__(kBlock) void gdn_gate_prep_kernel(GdnParams a, size_t total) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < total) small_gates(a, i, static_cast<int>(i % a.n_v_head));
+}
+
+__device__ __forceinline__ float4 silu4(float4 v) {
+  return make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
+}
+
+// One block per token; G = head_dim / 4 lanes per L2 head.
+template <int G>
+__global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a) {
+  const size_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+
+  // (1) scalar gates of this token
+  for (int h = tid; h < a.n_v_head; h += kBlock) small_gates(a, t * a.n_v_head + h, h);
+
+  // (2) conv row: silu, then L2 per head over the first l2_dim channels
+  if (a.conv_out != nullptr) {
+    const int n4 = a.conv_dim >> 2;
+    const int l2_4 = a.l2_dim >> 2;
+    const float4 *c4 = reinterpret_cast<const float4 *>(a.conv) + t * n4;
+    float4 *o4 = reinterpret_cast<float4 *>(a.conv_out) + t * n4;
+    for (int base = 0; base < n4; base += kBlock * kUnroll) {  // uniform trip count
+      float4 v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * kBlock + tid;
+        v[u] = i < n4 ? c4[i] : make_float4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * kBlock + tid;
+        float4 s = silu4(v[u]);
+        double ss = static_cast<double>(s.x) * static_cast<double>(s.x);
+        ss += static_cast<double>(s.y) * static_cast<double>(s.y);
+        ss += static_cast<double>(s.z) * static_cast<double>(s.z);
+        ss += static_cast<double>(s.w) * static_cast<double>(s.w);
+#pragma unroll
+        for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (i < l2_4) {
+          const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
+          s = make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
+        }
+        if (i < n4) o4[i] = s;
+      }
+    }
+  }
+
+  // (3) output gate row: y * act(z)
+  if (a.gated_out != nullptr) {
+    const int n4 = a.inner_dim >> 2;
+    const float4 *z4 = reinterpret_cast<const float4 *>(a.z) + t * n4;
+    const float4 *y4 = reinterpret_cast<const float4 *>(a.y) + t * n4;
+    float4 *o4 = reinterpret_cast<float4 *>(a.gated_out) + t * n4;
+    for (int base = 0; base < n4; base += kBlock * kUnroll) {
+      float4 vz[kUnroll], vy[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * kBlock + tid;
+        vz[u] = i < n4 ? z4[i] : make_float4(0, 0, 0, 0);
+        vy[u] = i < n4 ? y4[i] : make_float4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int i = base + u * kBlock + tid;
+        if (i < n4) {
+          o4[i] = a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(vz[u], vy[u])
+                                 : unary_op4<BH_SILU_MUL>(vz[u], vy[u]);
+        }
+      }
+    }
+  }
+}
+
+// Looped version for layouts the fast kernel does not cover (odd widths,
+// unaligned pointers): one block per token, one L2 head at a time.
+__global__ __launch_bounds__(kBlock) void gdn_prep_loop_kernel(GdnParams a) {
+  __shared__ double lds[kBlock / 64];
+  const size_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+  for (int h = tid; h < a.n_v_head; h += kBlock) small_gates(a, t * a.n_v_head + h, h);
+  if (a.conv_out != nullptr) {
+    const float *c = a.conv + t * a.conv_dim;
+    float *o = a.conv_out + t * a.conv_dim;
+    const int n_heads = a.l2_dim / a.head_dim;
+    for (int hh = 0; hh < n_heads; ++hh) {
+      double ss = 0.0;
+      for (int d = tid; d < a.head_dim; d += kBlock) {
+        const float s = silu(c[hh * a.head_dim + d]);
+        ss += static_cast<double>(s) * static_cast<double>(s);
+      }
+      ss = group_reduce<kBlock>(ss, SumOp{}, lds);
+      const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
+      for (int d = tid; d < a.head_dim; d += kBlock)
+        o[hh * a.head_dim + d] = silu(c[hh * a.head_dim + d]) * scale;
+      __syncthreads();  // lds reuse by the next head
+    }
+    for (int i = a.l2_dim + tid; i < a.conv_dim; i += kBlock) o[i] = silu(c[i]);
+  }
+  if (a.gated_out != nullptr) {
+    const size_t off = t * a.inner_dim;
+    for (int i = tid; i < a.inner_dim; i += kBlock) {
+      const float z = a.z[off + i], y = a.y[off + i];
+      a.gated_out[off + i] = a.sigmoid_gate ? y * sigmoid(z) : y * silu(z);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace bh
+
+using namespace bh;
+
+extern "C" int bh_unary(int mode, const float *a, const float *b, size_t n, float *out,
+                        bh_stream stream) {
+  if (mode < BH_SILU || mode > BH_SIGMOID_MUL)
+    return fail(BH_ERR_ARG, "unary: unknown mode " + std::to_string(mode));
+  if (n == 0) return ok();
+  if (!a || !out || ((mode == BH_SILU_MUL || mode == BH_SIGMOID_MUL) && !b))
+    return fail(BH_ERR_ARG, "unary: null pointer");
+  hipStream_t st = as_stream(stream);
+  switch (mode) {
+    case BH_SILU: return unary_launch<BH_SILU>(a, b, out, n, st);
+    case BH_SIGMOID: return unary_launch<BH_SIGMOID>(a, b, out, n, st);
+    case BH_SOFTPLUS: return unary_launch<BH_SOFTPLUS>(a, b, out, n, st);
+    case BH_SILU_MUL: return unary_launch<BH_SILU_MUL>(a, b, out, n, st);
+    default: return unary_launch<BH_SIGMOID_MUL>(a, b, out, n, st);
+  }
+}
+
+extern "C" int bh_gdn_gate_prep(const float *alpha_raw, const float *dt_bias, const float *ssm_a,
+                                const float *beta_raw, size_t n_tok, size_t n_head,
+                                float *gate_out, float *beta_out, bh_stream stream) {
+  const size_t total = n_tok * n_head;
+  if (total == 0) return ok();
+  if ((gate_out && (!alpha_raw || !dt_bias || !ssm_a)) || (beta_out && !beta_raw))
+    return fail(BH_ERR_ARG, "gdn_gate_prep: null pointer");
+  if (n_head > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_gate_prep: n_head too large");
+  GdnParams p{};
+  p.alpha_raw = alpha_raw;
+  p.dt_bias = dt_bias;
+  p.ssm_a = ssm_a;
+  p.beta_raw = beta_raw;
+  p.gate_out = gate_out;
+  p.beta_out = beta_out;
+  p.n_v_head = static_cast<int>(n_head);
+  const size_t blocks = (total + kBlock - 1) / kBlock;
+  if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_gate_prep: too many elements");
+  BH_LAUNCH(gdn_gate_prep_kernel, static_cast<unsigned>(blocks), kBlock, 0, as_stream(stream), p,
+            total);
+  return ok();
+}
+
+extern "C" int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream) {
+  if (args == nullptr) return fail(BH_ERR_ARG, "gdn_prep_fused: null args");
+  const bh_gdn_prep_args &g = *args;
+  if (g.gate_mode != BH_SILU_MUL && g.gate_mode != BH_SIGMOID_MUL)
+    return fail(BH_ERR_ARG, "gdn_prep_fused: gate_mode must be BH_SILU_MUL or BH_SIGMOID_MUL");
+  if (g.conv_out != nullptr) {
+    if (g.head_dim == 0 || g.l2_dim % g.head_dim != 0 || g.l2_dim > g.conv_dim)
+      return fail(BH_ERR_SHAPE, "gdn_prep_fused: l2_dim " + std::to_string(g.l2_dim) +
+                                    " must be a multiple of head_dim " +
+                                    std::to_string(g.head_dim) + " and <= conv_dim " +
+                                    std::to_string(g.conv_dim));
+    if (!g.conv) return fail(BH_ERR_ARG, "gdn_prep_fused: null conv");
+  }
+  if (g.gated_out != nullptr && (!g.z || !g.y)) return fail(BH_ERR_ARG, "gdn_prep_fused: null z/y");
+  if ((g.gate_out && (!g.alpha_raw || !g.dt_bias || !g.ssm_a)) || (g.beta_out && !g.beta_raw))
+    return fail(BH_ERR_ARG, "gdn_prep_fused: null gate input");
+  if (g.conv_dim > 0x7fffffffu || g.inner_dim > 0x7fffffffu || g.n_v_head > 0x7fffffffu)
+    return fail(BH_ERR_SHAPE, "gdn_prep_fused: dimension exceeds 2^31-1");
+  if (g.n_tok == 0) return ok();
+  if (g.n_tok > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: n_tok too large");
+  GdnParams p{};
+  p.conv = g.conv;
+  p.conv_out = g.conv_out;
+  p.z = g.z;
+  p.y = g.y;
+  p.gated_out = g.gated_out;
+  p.alpha_raw = g.alpha_raw;
+  p.dt_bias = g.dt_bias;
+  p.ssm_a = g.ssm_a;
+  p.beta_raw = g.beta_raw;
+  p.gate_out = g.gate_out;
+  p.beta_out = g.beta_out;
+  p.conv_dim = static_cast<int>(g.conv_dim);
+  p.l2_dim = static_cast<int>(g.l2_dim);
+  p.head_dim = static_cast<int>(g.head_dim);
+  p.inner_dim = static_cast<int>(g.inner_dim);
+  p.n_v_head = (g.gate_out || g.beta_out) ? static_cast<int>(g.n_v_head) : 0;
+  p.sigmoid_gate = g.gate_mode == BH_SIGMOID_MUL ? 1 : 0;
+  p.eps = g.eps;
+  const unsigned grid = static_cast<unsigned>(g.n_tok);
+  hipStream_t st = as_stream(stream);
+  const size_t hq = g.head_dim / 4;
+  const bool conv_fast = g.conv_out == nullptr ||
+                         (g.conv_dim % 4 == 0 && g.head_dim % 4 == 0 && hq >= 1 && hq <= 64 &&
+                          (hq & (hq - 1)) == 0 && aligned16(g.conv) && aligned16(g.conv_out));
+  const bool gate_fast = g.gated_out == nullptr ||
+                         (g.inner_dim % 4 == 0 && aligned16(g.z) && aligned16(g.y) &&
+                          aligned16(g.gated_out));
+  if (conv_fast && gate_fast) {
+    switch (g.conv_out == nullptr ? 64 : hq) {
+      case 1: BH_LAUNCH(gdn_prep_fused_kernel<1>, grid, kBlock, 0, st, p); return ok();
+      case 2: BH_LAUNCH(gdn_prep_fused_kernel<2>, grid, kBlock, 0, st, p); return ok();
+      case 4: BH_LAUNCH(gdn_prep_fused_kernel<4>, grid, kBlock, 0, st, p); return ok();
+      case 8: BH_LAUNCH(gdn_prep_fused_kernel<8>, grid, kBlock, 0, st, p); return ok();
+      case 16: BH_LAUNCH(gdn_prep_fused_kernel<16>, grid, kBlock, 0, st, p); return ok();
+      case 32: BH_LAUNCH(gdn_prep_fused_kernel<32>, grid, kBlock, 0, st, p); return ok();
+      case 64: BH_LAUNCH(gdn_prep_fused_kernel<64>, grid, kBlock, 0, st, p); return ok();
+      default: break;
+    }
+  }
+  BH_LAUNCH(gdn_prep_loop_kernel, grid, kBlock, 0, st, p);
+  return ok();
+}

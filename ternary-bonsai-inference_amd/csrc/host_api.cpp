@@ -1,0 +1,237 @@
+// Host-slice mirrors of the reference signatures (bh_host_*).
+//
+// Each one takes the Rust function's arguments as host pointers + lengths,
+// checks them the way the Rust does (same error text), copies the inputs to
+// the current device, runs the device entry point on a private stream,
+// copies the result back and synchronises.  They exist so a Rust FFI module
+// can keep the exact shapes of src/kernels.rs / src/rope.rs / src/prefill.rs
+// while the arithmetic runs on the GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace bh {
+namespace {
+
+// Device buffer owned for the duration of one host call.
+class DevBuf {
+ public:
+  DevBuf() = default;
+  DevBuf(const DevBuf &) = delete;
+  DevBuf &operator=(const DevBuf &) = delete;
+  ~DevBuf() {
+    if (p_ != nullptr) (void)hipFree(p_);
+  }
+  int alloc(size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    return check_hip(hipMalloc(&p_, bytes), "hipMalloc");
+  }
+  template <class T>
+  T *as() const {
+    return static_cast<T *>(p_);
+  }
+
+ private:
+  void *p_ = nullptr;
+};
+
+class Stream {
+ public:
+  Stream() { err_ = check_hip(hipStreamCreate(&s_), "hipStreamCreate"); }
+  ~Stream() {
+    if (s_ != nullptr) (void)hipStreamDestroy(s_);
+  }
+  int status() const { return err_; }
+  hipStream_t get() const { return s_; }
+  bh_stream handle() const { return reinterpret_cast<bh_stream>(s_); }
+
+ private:
+  hipStream_t s_ = nullptr;
+  int err_ = BH_OK;
+};
+
+int upload(DevBuf &d, const void *src, size_t bytes, hipStream_t s) {
+  if (int e = d.alloc(bytes)) return e;
+  if (bytes == 0) return BH_OK;
+  return check_hip(hipMemcpyAsync(d.as<void>(), src, bytes, hipMemcpyHostToDevice, s),
+                   "hipMemcpyAsync H2D");
+}
+
+int download(void *dst, const DevBuf &d, size_t bytes, hipStream_t s) {
+  if (bytes != 0) {
+    if (int e = check_hip(hipMemcpyAsync(dst, d.as<void>(), bytes, hipMemcpyDeviceToHost, s),
+                          "hipMemcpyAsync D2H"))
+      return e;
+  }
+  return check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+}  // namespace
+}  // namespace bh
+
+using namespace bh;
+
+extern "C" int bh_host_rms_norm(const float *x, size_t n, const float *w, float eps, float *out) {
+  if (n == 0) return ok();
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dx, dw, dout;
+  if (int e = upload(dx, x, n * 4, s.get())) return e;
+  if (int e = upload(dw, w, n * 4, s.get())) return e;
+  if (int e = dout.alloc(n * 4)) return e;
+  if (int e = bh_rms_norm(dx.as<float>(), dw.as<float>(), n, eps, dout.as<float>(), s.handle()))
+    return e;
+  if (int e = download(out, dout, n * 4, s.get())) return e;
+  return ok();
+}
+
+extern "C" int bh_host_rms_norm_rows(const float *x, size_t x_len, const float *w, size_t w_len,
+                                     size_t row_len, float eps, float *out) {
+  // shape errors first, with the reference's messages (src/kernels.rs:98-108)
+  if (w_len != row_len)
+    return fail(BH_ERR_SHAPE, "rms_norm_rows: weight len " + std::to_string(w_len) +
+                                  " != row_len " + std::to_string(row_len));
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "rms_norm_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dx, dw, dout;
+  if (int e = upload(dx, x, x_len * 4, s.get())) return e;
+  if (int e = upload(dw, w, w_len * 4, s.get())) return e;
+  if (int e = dout.alloc(x_len * 4)) return e;
+  if (int e = bh_rms_norm_rows(dx.as<float>(), x_len, dw.as<float>(), w_len, row_len, eps,
+                               dout.as<float>(), s.handle()))
+    return e;
+  if (int e = download(out, dout, x_len * 4, s.get())) return e;
+  return ok();
+}
+
+extern "C" int bh_host_l2_norm_rows(const float *x, size_t x_len, size_t row_len, float eps,
+                                    float *out) {
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "l2_norm_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dx, dout;
+  if (int e = upload(dx, x, x_len * 4, s.get())) return e;
+  if (int e = dout.alloc(x_len * 4)) return e;
+  if (int e = bh_l2_norm_rows(dx.as<float>(), x_len, row_len, eps, dout.as<float>(), s.handle()))
+    return e;
+  if (int e = download(out, dout, x_len * 4, s.get())) return e;
+  return ok();
+}
+
+extern "C" int bh_host_map_inplace(float *x, size_t n, int mode) {
+  if (mode != BH_SILU && mode != BH_SIGMOID && mode != BH_SOFTPLUS)
+    return fail(BH_ERR_ARG, "map_inplace: mode must be silu, sigmoid or softplus");
+  if (n == 0) return ok();
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dx;
+  if (int e = upload(dx, x, n * 4, s.get())) return e;
+  if (int e = bh_unary(mode, dx.as<float>(), nullptr, n, dx.as<float>(), s.handle())) return e;
+  if (int e = download(x, dx, n * 4, s.get())) return e;
+  return ok();
+}
+
+extern "C" int bh_host_softmax_rows(const float *x, size_t x_len, size_t row_len, float *out) {
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "softmax_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dx, dout;
+  if (int e = upload(dx, x, x_len * 4, s.get())) return e;
+  if (int e = dout.alloc(x_len * 4)) return e;
+  if (int e = bh_softmax_rows(dx.as<float>(), x_len, row_len, 1.0f, dout.as<float>(), s.handle()))
+    return e;
+  if (int e = download(out, dout, x_len * 4, s.get())) return e;
+  return ok();
+}
+
+extern "C" int bh_host_rope_imrope(float *head, size_t head_len, int64_t p_t, int64_t p_h,
+                                   int64_t p_w, int64_t p_e, size_t n_dims,
+                                   const int32_t sections[4], float freq_base) {
+  // the reference debug-asserts n_dims <= head.len() and n_dims even (src/rope.rs:19-20)
+  if (n_dims % 2 != 0 || n_dims > head_len)
+    return fail(BH_ERR_SHAPE, "rope_imrope: n_dims " + std::to_string(n_dims) +
+                                  " must be even and <= head len " + std::to_string(head_len));
+  if (head_len == 0) return ok();
+  // positions travel as int32 on the device; `p as f32` of a position beyond
+  // the int32 range is not representable there
+  const int64_t ps[4] = {p_t, p_h, p_w, p_e};
+  int32_t pos[4];
+  for (int i = 0; i < 4; ++i) {
+    if (ps[i] < INT32_MIN || ps[i] > INT32_MAX)
+      return fail(BH_ERR_RANGE, "rope_imrope: position outside the int32 range");
+    pos[i] = static_cast<int32_t>(ps[i]);
+  }
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dh, dp;
+  if (int e = upload(dh, head, head_len * 4, s.get())) return e;
+  if (int e = upload(dp, pos, sizeof(pos), s.get())) return e;
+  if (int e = bh_rope_imrope(dh.as<float>(), 1, 1, head_len, dp.as<int32_t>(), n_dims, sections,
+                             freq_base, s.handle()))
+    return e;
+  if (int e = download(head, dh, head_len * 4, s.get())) return e;
+  return ok();
+}
+
+extern "C" int bh_host_decode_pq2_0_row(const uint8_t *raw, size_t raw_len, size_t ne0,
+                                        float *out) {
+  const size_t rb = bh_pq2_row_bytes(ne0);
+  if (raw_len < rb)
+    return fail(BH_ERR_SHAPE, "decode_pq2_0_row: raw len " + std::to_string(raw_len) +
+                                  " < row bytes " + std::to_string(rb));
+  if (ne0 == 0) return ok();
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf draw, did, dout;
+  const uint32_t id = 0;
+  if (int e = upload(draw, raw, rb, s.get())) return e;
+  if (int e = upload(did, &id, sizeof(id), s.get())) return e;
+  if (int e = dout.alloc(ne0 * 4)) return e;
+  if (int e = bh_pq2_embed_gather(draw.as<uint8_t>(), ne0, 1, did.as<uint32_t>(), 1,
+                                  dout.as<float>(), nullptr, s.handle()))
+    return e;
+  if (int e = download(out, dout, ne0 * 4, s.get())) return e;
+  return ok();
+}
+
+extern "C" int bh_host_batch_embed(const uint8_t *payload, size_t payload_len, size_t ne0,
+                                   size_t n_rows, const uint32_t *tokens, size_t n_tok,
+                                   float *out) {
+  const size_t rb = bh_pq2_row_bytes(ne0);
+  if (payload_len < rb * n_rows)
+    return fail(BH_ERR_SHAPE, "batch_embed: payload len " + std::to_string(payload_len) +
+                                  " < n_rows * row bytes " + std::to_string(rb * n_rows));
+  // Weights::row_f32 range check (src/weights.rs:337-341), first bad token wins
+  for (size_t k = 0; k < n_tok; ++k) {
+    if (tokens[k] >= n_rows)
+      return fail(BH_ERR_RANGE, "Weights: row_f32(token_embd.weight): row " +
+                                    std::to_string(tokens[k]) + " out of range (n_rows " +
+                                    std::to_string(n_rows) + ")");
+  }
+  if (n_tok == 0 || ne0 == 0) return ok();
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dtab, dids, dout;
+  if (int e = upload(dtab, payload, rb * n_rows, s.get())) return e;
+  if (int e = upload(dids, tokens, n_tok * 4, s.get())) return e;
+  if (int e = dout.alloc(n_tok * ne0 * 4)) return e;
+  if (int e = bh_pq2_embed_gather(dtab.as<uint8_t>(), ne0, n_rows, dids.as<uint32_t>(), n_tok,
+                                  dout.as<float>(), nullptr, s.handle()))
+    return e;
+  if (int e = download(out, dout, n_tok * ne0 * 4, s.get())) return e;
+  return ok();
+}

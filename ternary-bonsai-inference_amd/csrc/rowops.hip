@@ -1,0 +1,654 @@
+// Row-wise normalisation and softmax kernels for gfx950.
+//
+//   bh_rms_norm / bh_rms_norm_rows   kernels::rms_norm, rms_norm_rows
+//                                    (src/kernels.rs:59-122)
+//   bh_add_rms_norm_rows             residual add + RMSNorm (src/forward.rs:708-713)
+//   bh_l2_norm_rows                  kernels::l2_norm_rows (src/kernels.rs:126-145)
+//   bh_silu_l2_norm_rows             silu + l2_norm_rows (src/forward.rs:524, 539-540)
+//   bh_softmax_rows                  kernels::softmax_rows (src/kernels.rs:175-202)
+//                                    with the sampler temperature (src/sampler.rs:85,110)
+//
+// Design.  Every op here reads a row once from HBM and writes it once; the
+// arithmetic is < 1 flop/byte, so the roofline is HBM bandwidth and the
+// kernels are built around it:
+//   * a row is owned by a "group" of G lanes (G a power of two).  Rows of up
+//     to 256 floats are owned by part of one wave (128-float L2 heads: 32
+//     lanes, 256-float q/k heads: 64 lanes); rows of up to 2048 floats by one
+//     wave; longer rows (5120-float hidden rows) by G/64 waves of one block;
+//   * each lane holds VPT <= 8 float4 of its row in registers, loaded with
+//     16-byte coalesced loads (lane gl reads float4 gl, gl+G, ...), so the
+//     reduction and the scaled write-back need no second HBM pass;
+//   * row reductions run with cross-lane shuffles inside the wave and an LDS
+//     combine across waves, in a fixed order (deterministic output);
+//   * rows that do not fit this scheme (length not a multiple of 4, unaligned
+//     pointers, > 32768 floats) go to a block-per-row looped kernel; rows
+//     that are both long and few (the 248320-wide vocabulary softmax) are
+//     split over many blocks with an online (max, sum) first pass.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <string>
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace bh {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <int G>
+constexpr int block_of() {
+  return G > kBlock ? G : kBlock;
+}
+
+template <int N>
+using IC = std::integral_constant<int, N>;
+
+// Lanes-per-row G and float4-per-lane VPT for a row of row_len floats.
+struct RowGeom {
+  int G = 0;
+  int VPT = 0;
+};
+
+// Returns false when the register scheme does not apply (the caller then
+// uses the looped kernel).
+bool pick_geom(size_t row_len, RowGeom &g) {
+  if (row_len == 0 || (row_len & 3u) != 0) return false;
+  const size_t r4 = row_len / 4;
+  if (r4 <= 64) {
+    g.G = pow2ceil(r4);
+    g.VPT = 1;
+  } else if (r4 <= 512) {
+    g.G = 64;
+    g.VPT = static_cast<int>((r4 + 63) / 64);
+  } else if (r4 <= 8192) {
+    g.G = pow2ceil((r4 + 7) / 8);
+    g.VPT = static_cast<int>((r4 + g.G - 1) / g.G);
+    if (g.VPT < 4 || g.VPT > 8) return false;
+  } else {
+    return false;
+  }
+  return true;
+}
+
+// Calls f(IC<G>, IC<VPT>) for the instantiated geometries; returns -999 when
+// the geometry has no instantiation.
+template <class F>
+int with_geom(const RowGeom &g, F &&f) {
+#define BH_G_SMALL(GV) \
+  case GV:             \
+    return f(IC<GV>{}, IC<1>{});
+#define BH_G_BIG(GV)                      \
+  case GV:                                \
+    switch (g.VPT) {                      \
+      case 4: return f(IC<GV>{}, IC<4>{}); \
+      case 5: return f(IC<GV>{}, IC<5>{}); \
+      case 6: return f(IC<GV>{}, IC<6>{}); \
+      case 7: return f(IC<GV>{}, IC<7>{}); \
+      case 8: return f(IC<GV>{}, IC<8>{}); \
+      default: return -999;               \
+    }
+  switch (g.G) {
+    BH_G_SMALL(1)
+    BH_G_SMALL(2)
+    BH_G_SMALL(4)
+    BH_G_SMALL(8)
+    BH_G_SMALL(16)
+    BH_G_SMALL(32)
+    case 64:
+      switch (g.VPT) {
+        case 1: return f(IC<64>{}, IC<1>{});
+        case 2: return f(IC<64>{}, IC<2>{});
+        case 3: return f(IC<64>{}, IC<3>{});
+        case 4: return f(IC<64>{}, IC<4>{});
+        case 5: return f(IC<64>{}, IC<5>{});
+        case 6: return f(IC<64>{}, IC<6>{});
+        case 7: return f(IC<64>{}, IC<7>{});
+        case 8: return f(IC<64>{}, IC<8>{});
+        default: return -999;
+      }
+    BH_G_BIG(128)
+    BH_G_BIG(256)
+    BH_G_BIG(512)
+    BH_G_BIG(1024)
+    default:
+      return -999;
+  }
+#undef BH_G_SMALL
+#undef BH_G_BIG
+}
+
+__device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+// ---------------------------------------------------------------------------
+// RMSNorm rows (optionally with the residual add in front)
+// ---------------------------------------------------------------------------
+
+// out = (v * scale) * w, scale = 1 / sqrt(sum(v^2)/row_len + eps), with v = x
+// or v = x + r (ADD, also stored to sum_out).  Matches src/kernels.rs:112-120
+// operation for operation; only the order of the sum of squares differs
+// (lane partials + tree instead of one sequential loop).
+template <int G, int VPT, bool ADD>
+__global__ __launch_bounds__(block_of<G>()) void rms_rows_kernel(
+    const float *x, const float *__restrict__ r, const float *__restrict__ w,
+    float *sum_out, float *out, size_t rows, int row_len, float eps) {
+  constexpr int RPB = block_of<G>() / G;
+  __shared__ float lds[block_of<G>() / 64];
+  const int gl = threadIdx.x % G;
+  const size_t row = static_cast<size_t>(blockIdx.x) * RPB + threadIdx.x / G;
+  const bool live = row < rows;
+  const int r4 = row_len >> 2;
+  const size_t off = live ? row * r4 : 0;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x) + off;
+
+  float4 v[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = gl + i * G;
+    v[i] = (live && c < r4) ? x4[c] : f4_zero();
+  }
+  if constexpr (ADD) {
+    const float4 *r4p = reinterpret_cast<const float4 *>(r) + off;
+    float4 *s4 = reinterpret_cast<float4 *>(sum_out) + off;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int c = gl + i * G;
+      if (live && c < r4) {
+        const float4 a = r4p[c];
+        v[i].x += a.x;
+        v[i].y += a.y;
+        v[i].z += a.z;
+        v[i].w += a.w;
+        s4[c] = v[i];
+      }
+    }
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    ss += v[i].x * v[i].x;
+    ss += v[i].y * v[i].y;
+    ss += v[i].z * v[i].z;
+    ss += v[i].w * v[i].w;
+  }
+  ss = group_reduce<G>(ss, SumOp{}, lds);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(row_len) + eps);
+  const float4 *w4 = reinterpret_cast<const float4 *>(w);
+  float4 *o4 = reinterpret_cast<float4 *>(out) + off;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = gl + i * G;
+    if (live && c < r4) {
+      const float4 wv = w4[c];
+      float4 o;
+      o.x = (v[i].x * scale) * wv.x;
+      o.y = (v[i].y * scale) * wv.y;
+      o.z = (v[i].z * scale) * wv.z;
+      o.w = (v[i].w * scale) * wv.w;
+      o4[c] = o;
+    }
+  }
+}
+
+// Looped fallback: one block per row, any length / alignment.  Reads x twice.
+template <bool ADD>
+__global__ __launch_bounds__(kBlock) void rms_rows_loop_kernel(
+    const float *x, const float *__restrict__ r, const float *__restrict__ w,
+    float *sum_out, float *out, int row_len, float eps) {
+  __shared__ float lds[kBlock / 64];
+  const size_t off = static_cast<size_t>(blockIdx.x) * row_len;
+  float ss = 0.0f;
+  for (int c = threadIdx.x; c < row_len; c += kBlock) {
+    float v = x[off + c];
+    if constexpr (ADD) {
+      v += r[off + c];
+      sum_out[off + c] = v;
+    }
+    ss += v * v;
+  }
+  ss = group_reduce<kBlock>(ss, SumOp{}, lds);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(row_len) + eps);
+  for (int c = threadIdx.x; c < row_len; c += kBlock) {
+    // each thread re-reads exactly the elements it wrote, so sum_out == x is safe
+    const float v = ADD ? sum_out[off + c] : x[off + c];
+    out[off + c] = (v * scale) * w[c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// L2 rows (optionally SiLU first)
+// ---------------------------------------------------------------------------
+
+// out = v * (1 / max(sqrt((f32) sum_f64(v^2)), eps)), v = x or silu(x)
+// (src/kernels.rs:136-143; silu src/kernels.rs:148-150).
+template <int G, int VPT, bool SILU>
+__global__ __launch_bounds__(block_of<G>()) void l2_rows_kernel(
+    const float *x, float *out, size_t rows, int row_len, float eps) {
+  constexpr int RPB = block_of<G>() / G;
+  __shared__ double lds[block_of<G>() / 64];
+  const int gl = threadIdx.x % G;
+  const size_t row = static_cast<size_t>(blockIdx.x) * RPB + threadIdx.x / G;
+  const bool live = row < rows;
+  const int r4 = row_len >> 2;
+  const size_t off = live ? row * r4 : 0;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x) + off;
+
+  float4 v[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = gl + i * G;
+    v[i] = (live && c < r4) ? x4[c] : f4_zero();
+    if constexpr (SILU) {
+      v[i].x = silu(v[i].x);
+      v[i].y = silu(v[i].y);
+      v[i].z = silu(v[i].z);
+      v[i].w = silu(v[i].w);
+    }
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    ss += static_cast<double>(v[i].x) * static_cast<double>(v[i].x);
+    ss += static_cast<double>(v[i].y) * static_cast<double>(v[i].y);
+    ss += static_cast<double>(v[i].z) * static_cast<double>(v[i].z);
+    ss += static_cast<double>(v[i].w) * static_cast<double>(v[i].w);
+  }
+  ss = group_reduce<G>(ss, SumOp{}, lds);
+  const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), eps);
+  float4 *o4 = reinterpret_cast<float4 *>(out) + off;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = gl + i * G;
+    if (live && c < r4) {
+      o4[c] = make_float4(v[i].x * scale, v[i].y * scale, v[i].z * scale, v[i].w * scale);
+    }
+  }
+}
+
+template <bool SILU>
+__global__ __launch_bounds__(kBlock) void l2_rows_loop_kernel(const float *x, float *out,
+                                                              int row_len, float eps) {
+  __shared__ double lds[kBlock / 64];
+  const size_t off = static_cast<size_t>(blockIdx.x) * row_len;
+  double ss = 0.0;
+  for (int c = threadIdx.x; c < row_len; c += kBlock) {
+    float v = x[off + c];
+    if constexpr (SILU) v = silu(v);
+    ss += static_cast<double>(v) * static_cast<double>(v);
+  }
+  ss = group_reduce<kBlock>(ss, SumOp{}, lds);
+  const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), eps);
+  for (int c = threadIdx.x; c < row_len; c += kBlock) {
+    float v = x[off + c];
+    if constexpr (SILU) v = silu(v);
+    out[off + c] = v * scale;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Softmax rows
+// ---------------------------------------------------------------------------
+
+// y = x * inv_t; m = max(y) (NaN never becomes the max, as `if v > max`);
+// e = expf(y - m); s = sum_f64(e); out = e * (1 / (f32)s)
+// (src/kernels.rs:184-200).  -inf entries give expf(-inf) = 0.
+template <int G, int VPT>
+__global__ __launch_bounds__(block_of<G>()) void softmax_rows_kernel(
+    const float *x, float *out, size_t rows, int row_len, float inv_t) {
+  constexpr int RPB = block_of<G>() / G;
+  __shared__ float lds_m[block_of<G>() / 64];
+  __shared__ double lds_s[block_of<G>() / 64];
+  const int gl = threadIdx.x % G;
+  const size_t row = static_cast<size_t>(blockIdx.x) * RPB + threadIdx.x / G;
+  const bool live = row < rows;
+  const int r4 = row_len >> 2;
+  const size_t off = live ? row * r4 : 0;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x) + off;
+  const float ninf = -INFINITY;
+
+  float4 v[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = gl + i * G;
+    if (live && c < r4) {
+      v[i] = x4[c];
+      v[i].x *= inv_t;
+      v[i].y *= inv_t;
+      v[i].z *= inv_t;
+      v[i].w *= inv_t;
+    } else {
+      v[i] = make_float4(ninf, ninf, ninf, ninf);
+    }
+  }
+  float m = ninf;
+  const MaxOp mx;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    m = mx(m, v[i].x);
+    m = mx(m, v[i].y);
+    m = mx(m, v[i].z);
+    m = mx(m, v[i].w);
+  }
+  m = group_reduce<G>(m, mx, lds_m);
+  double s = 0.0;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = gl + i * G;
+    if (live && c < r4) {
+      v[i].x = expf(v[i].x - m);
+      v[i].y = expf(v[i].y - m);
+      v[i].z = expf(v[i].z - m);
+      v[i].w = expf(v[i].w - m);
+      s += static_cast<double>(v[i].x);
+      s += static_cast<double>(v[i].y);
+      s += static_cast<double>(v[i].z);
+      s += static_cast<double>(v[i].w);
+    }
+  }
+  s = group_reduce<G>(s, SumOp{}, lds_s);
+  const float inv = 1.0f / static_cast<float>(s);
+  float4 *o4 = reinterpret_cast<float4 *>(out) + off;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = gl + i * G;
+    if (live && c < r4) {
+      o4[c] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+    }
+  }
+}
+
+// Online (max, sum) state of a stream of y values: sum of expf(y - m) in f64
+// relative to the running max m.  -inf values contribute nothing; NaN
+// poisons the sum exactly as it poisons the reference's.
+struct MaxSum {
+  float m;
+  double s;
+};
+
+__device__ __forceinline__ void ms_push(MaxSum &a, float y) {
+  if (y > a.m) {
+    a.s = (a.m == -INFINITY) ? 0.0 : a.s * static_cast<double>(expf(a.m - y));
+    a.m = y;
+  }
+  if (y != -INFINITY) a.s += static_cast<double>(expf(y - a.m));
+}
+
+__device__ __forceinline__ MaxSum ms_merge(MaxSum a, MaxSum b) {
+  const float M = b.m > a.m ? b.m : a.m;
+  if (M == -INFINITY) return MaxSum{M, 0.0};
+  double s = 0.0;
+  if (a.m != -INFINITY) s += a.s * exp(static_cast<double>(a.m) - static_cast<double>(M));
+  if (b.m != -INFINITY) s += b.s * exp(static_cast<double>(b.m) - static_cast<double>(M));
+  return MaxSum{M, s};
+}
+
+// Split-row pass 1: block (c, r) reduces chunk c of row r to (max, sum).
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(
+    const float *x, size_t row_len, size_t chunk, float inv_t, float *part_m,
+    double *part_s) {
+  __shared__ float lm[kBlock / 64];
+  __shared__ double ls[kBlock / 64];
+  const size_t r = blockIdx.y;
+  const size_t c0 = blockIdx.x * chunk;
+  const size_t c1 = (c0 + chunk < row_len) ? c0 + chunk : row_len;
+  const float *xr = x + r * row_len;
+  MaxSum a{-INFINITY, 0.0};
+  if constexpr (VEC) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+    for (size_t c = c0 / 4 + threadIdx.x; c < c1 / 4; c += kBlock) {
+      const float4 v = x4[c];
+      ms_push(a, v.x * inv_t);
+      ms_push(a, v.y * inv_t);
+      ms_push(a, v.z * inv_t);
+      ms_push(a, v.w * inv_t);
+    }
+  } else {
+    for (size_t c = c0 + threadIdx.x; c < c1; c += kBlock) ms_push(a, xr[c] * inv_t);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    MaxSum b{__shfl_xor(a.m, off, 64), __shfl_xor(a.s, off, 64)};
+    a = ms_merge(a, b);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    lm[wave] = a.m;
+    ls[wave] = a.s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    MaxSum t{lm[0], ls[0]};
+    for (int i = 1; i < kBlock / 64; ++i) t = ms_merge(t, MaxSum{lm[i], ls[i]});
+    part_m[r * gridDim.x + blockIdx.x] = t.m;
+    part_s[r * gridDim.x + blockIdx.x] = t.s;
+  }
+}
+
+// Split-row pass 2: every block folds its row's chunk states in chunk order
+// (same bits in all blocks of the row), then writes expf(y - M) * inv.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(
+    const float *x, float *out, size_t row_len, size_t chunk, float inv_t,
+    const float *part_m, const double *part_s) {
+  const size_t r = blockIdx.y;
+  const int nch = gridDim.x;
+  MaxSum t{part_m[r * nch], part_s[r * nch]};
+  for (int i = 1; i < nch; ++i) t = ms_merge(t, MaxSum{part_m[r * nch + i], part_s[r * nch + i]});
+  const float M = t.m;
+  const float inv = 1.0f / static_cast<float>(t.s);
+  const size_t c0 = blockIdx.x * chunk;
+  const size_t c1 = (c0 + chunk < row_len) ? c0 + chunk : row_len;
+  const float *xr = x + r * row_len;
+  float *orow = out + r * row_len;
+  if constexpr (VEC) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+    float4 *o4 = reinterpret_cast<float4 *>(orow);
+    for (size_t c = c0 / 4 + threadIdx.x; c < c1 / 4; c += kBlock) {
+      const float4 v = x4[c];
+      o4[c] = make_float4(expf(v.x * inv_t - M) * inv, expf(v.y * inv_t - M) * inv,
+                          expf(v.z * inv_t - M) * inv, expf(v.w * inv_t - M) * inv);
+    }
+  } else {
+    for (size_t c = c0 + threadIdx.x; c < c1; c += kBlock)
+      orow[c] = expf(xr[c] * inv_t - M) * inv;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host dispatch
+// ---------------------------------------------------------------------------
+
+int grid_for(size_t rows, int rows_per_block, unsigned *grid) {
+  const size_t g = (rows + rows_per_block - 1) / rows_per_block;
+  if (g > 0x7fffffffu) return fail(BH_ERR_SHAPE, "row count exceeds the launch grid limit");
+  *grid = static_cast<unsigned>(g);
+  return BH_OK;
+}
+
+int rms_rows_impl(const float *x, const float *r, const float *w, float *sum_out,
+                  float *out, size_t rows, size_t row_len, float eps, hipStream_t st,
+                  bool add) {
+  if (rows == 0) return ok();
+  if (row_len > 0x7fffffffu) return fail(BH_ERR_SHAPE, "row_len exceeds 2^31-1");
+  RowGeom g;
+  const bool vec = pick_geom(row_len, g) && aligned16(x) && aligned16(w) && aligned16(out) &&
+                   (!add || (aligned16(r) && aligned16(sum_out)));
+  if (vec) {
+    int st_code = with_geom(g, [&](auto GC, auto VC) -> int {
+      constexpr int G_ = decltype(GC)::value;
+      constexpr int V_ = decltype(VC)::value;
+      unsigned grid;
+      if (int e = grid_for(rows, block_of<G_>() / G_, &grid)) return e;
+      if (add) {
+        BH_LAUNCH((rms_rows_kernel<G_, V_, true>), grid, block_of<G_>(), 0, st, x, r, w,
+                  sum_out, out, rows, static_cast<int>(row_len), eps);
+      } else {
+        BH_LAUNCH((rms_rows_kernel<G_, V_, false>), grid, block_of<G_>(), 0, st, x, r, w,
+                  sum_out, out, rows, static_cast<int>(row_len), eps);
+      }
+      return ok();
+    });
+    if (st_code != -999) return st_code;
+  }
+  unsigned grid;
+  if (int e = grid_for(rows, 1, &grid)) return e;
+  if (add) {
+    BH_LAUNCH((rms_rows_loop_kernel<true>), grid, kBlock, 0, st, x, r, w, sum_out, out,
+              static_cast<int>(row_len), eps);
+  } else {
+    BH_LAUNCH((rms_rows_loop_kernel<false>), grid, kBlock, 0, st, x, r, w, sum_out, out,
+              static_cast<int>(row_len), eps);
+  }
+  return ok();
+}
+
+template <bool SILU>
+int l2_rows_impl(const float *x, float *out, size_t rows, size_t row_len, float eps,
+                 hipStream_t st) {
+  if (rows == 0) return ok();
+  if (row_len > 0x7fffffffu) return fail(BH_ERR_SHAPE, "row_len exceeds 2^31-1");
+  RowGeom g;
+  if (pick_geom(row_len, g) && aligned16(x) && aligned16(out)) {
+    int st_code = with_geom(g, [&](auto GC, auto VC) -> int {
+      constexpr int G_ = decltype(GC)::value;
+      constexpr int V_ = decltype(VC)::value;
+      unsigned grid;
+      if (int e = grid_for(rows, block_of<G_>() / G_, &grid)) return e;
+      BH_LAUNCH((l2_rows_kernel<G_, V_, SILU>), grid, block_of<G_>(), 0, st, x, out, rows,
+                static_cast<int>(row_len), eps);
+      return ok();
+    });
+    if (st_code != -999) return st_code;
+  }
+  unsigned grid;
+  if (int e = grid_for(rows, 1, &grid)) return e;
+  BH_LAUNCH((l2_rows_loop_kernel<SILU>), grid, kBlock, 0, st, x, out, static_cast<int>(row_len),
+            eps);
+  return ok();
+}
+
+int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float inv_t,
+                  hipStream_t st) {
+  if (rows > 65535) return fail(BH_ERR_SHAPE, "softmax_rows: too many wide rows for one launch");
+  // about 2048 blocks over the chip, chunks of >= 4096 floats, multiple of 4
+  size_t nch = (2048 + rows - 1) / rows;
+  const size_t max_ch = (row_len + 4095) / 4096;
+  if (nch > max_ch) nch = max_ch;
+  if (nch < 1) nch = 1;
+  if (nch > 1024) nch = 1024;
+  size_t chunk = (row_len + nch - 1) / nch;
+  chunk = (chunk + 3) & ~static_cast<size_t>(3);
+  nch = (row_len + chunk - 1) / chunk;
+  const size_t nparts = rows * nch;
+  char *scratch = static_cast<char *>(device_scratch(nparts * (sizeof(double) + sizeof(float))));
+  if (scratch == nullptr) return BH_ERR_HIP;
+  double *part_s = reinterpret_cast<double *>(scratch);
+  float *part_m = reinterpret_cast<float *>(scratch + nparts * sizeof(double));
+  const dim3 grid(static_cast<unsigned>(nch), static_cast<unsigned>(rows));
+  const bool vec = (row_len % 4 == 0) && aligned16(x) && aligned16(out);
+  if (vec) {
+    BH_LAUNCH((softmax_split_stats_kernel<true>), grid, kBlock, 0, st, x, row_len, chunk, inv_t,
+              part_m, part_s);
+    BH_LAUNCH((softmax_split_write_kernel<true>), grid, kBlock, 0, st, x, out, row_len, chunk,
+              inv_t, part_m, part_s);
+  } else {
+    BH_LAUNCH((softmax_split_stats_kernel<false>), grid, kBlock, 0, st, x, row_len, chunk, inv_t,
+              part_m, part_s);
+    BH_LAUNCH((softmax_split_write_kernel<false>), grid, kBlock, 0, st, x, out, row_len, chunk,
+              inv_t, part_m, part_s);
+  }
+  return ok();
+}
+
+}  // namespace
+}  // namespace bh
+
+using namespace bh;
+
+extern "C" int bh_rms_norm(const float *x, const float *w, size_t n, float eps, float *out,
+                           bh_stream stream) {
+  if (n == 0) return ok();
+  if (!x || !w || !out) return fail(BH_ERR_ARG, "rms_norm: null pointer");
+  return rms_rows_impl(x, nullptr, w, nullptr, out, 1, n, eps, as_stream(stream), false);
+}
+
+extern "C" int bh_rms_norm_rows(const float *x, size_t x_len, const float *w, size_t w_len,
+                                size_t row_len, float eps, float *out, bh_stream stream) {
+  if (w_len != row_len)
+    return fail(BH_ERR_SHAPE, "rms_norm_rows: weight len " + std::to_string(w_len) +
+                                  " != row_len " + std::to_string(row_len));
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "rms_norm_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  if (!x || !w || !out) return fail(BH_ERR_ARG, "rms_norm_rows: null pointer");
+  return rms_rows_impl(x, nullptr, w, nullptr, out, x_len / row_len, row_len, eps,
+                       as_stream(stream), false);
+}
+
+extern "C" int bh_add_rms_norm_rows(const float *x, const float *residual, size_t x_len,
+                                    const float *w, size_t w_len, size_t row_len, float eps,
+                                    float *sum_out, float *out, bh_stream stream) {
+  if (w_len != row_len)
+    return fail(BH_ERR_SHAPE, "add_rms_norm_rows: weight len " + std::to_string(w_len) +
+                                  " != row_len " + std::to_string(row_len));
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "add_rms_norm_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  if (!x || !residual || !w || !sum_out || !out)
+    return fail(BH_ERR_ARG, "add_rms_norm_rows: null pointer");
+  return rms_rows_impl(x, residual, w, sum_out, out, x_len / row_len, row_len, eps,
+                       as_stream(stream), true);
+}
+
+extern "C" int bh_l2_norm_rows(const float *x, size_t x_len, size_t row_len, float eps,
+                               float *out, bh_stream stream) {
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "l2_norm_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  if (!x || !out) return fail(BH_ERR_ARG, "l2_norm_rows: null pointer");
+  return l2_rows_impl<false>(x, out, x_len / row_len, row_len, eps, as_stream(stream));
+}
+
+extern "C" int bh_silu_l2_norm_rows(const float *x, size_t x_len, size_t row_len, float eps,
+                                    float *out, bh_stream stream) {
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "silu_l2_norm_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  if (!x || !out) return fail(BH_ERR_ARG, "silu_l2_norm_rows: null pointer");
+  return l2_rows_impl<true>(x, out, x_len / row_len, row_len, eps, as_stream(stream));
+}
+
+extern "C" int bh_softmax_rows(const float *x, size_t x_len, size_t row_len, float inv_temp,
+                               float *out, bh_stream stream) {
+  if (row_len == 0 || x_len % row_len != 0)
+    return fail(BH_ERR_SHAPE, "softmax_rows: x len " + std::to_string(x_len) +
+                                  " not divisible by row_len " + std::to_string(row_len));
+  if (x_len == 0) return ok();
+  if (!x || !out) return fail(BH_ERR_ARG, "softmax_rows: null pointer");
+  const size_t rows = x_len / row_len;
+  hipStream_t st = as_stream(stream);
+  RowGeom g;
+  const bool fits = pick_geom(row_len, g) && aligned16(x) && aligned16(out);
+  const bool few_long_rows = rows < 1024 && row_len >= 16384;
+  if (fits && !few_long_rows) {
+    int st_code = with_geom(g, [&](auto GC, auto VC) -> int {
+      constexpr int G_ = decltype(GC)::value;
+      constexpr int V_ = decltype(VC)::value;
+      unsigned grid;
+      if (int e = grid_for(rows, block_of<G_>() / G_, &grid)) return e;
+      BH_LAUNCH((softmax_rows_kernel<G_, V_>), grid, block_of<G_>(), 0, st, x, out, rows,
+                static_cast<int>(row_len), inv_temp);
+      return ok();
+    });
+    if (st_code != -999) return st_code;
+  }
+  // The split path reads x again in pass 2; each element is read by the same
+  // thread just before it writes it, so out == x (in place) is safe there too.
+  return softmax_split(x, out, rows, row_len, inv_temp, st);
+}

@@ -1,0 +1,78 @@
+// Status plumbing, version string and the per-device scratch allocator.
+//
+// The reference reports shape errors as Err(String) (e.g. src/kernels.rs:98-109);
+// the C ABI returns a negative status and keeps the same message in a
+// thread-local string readable through bh_last_error().
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace bh {
+
+namespace {
+thread_local std::string g_last_error;
+
+struct Scratch {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_scratch_mu;
+std::vector<Scratch> g_scratch;  // indexed by device ordinal
+}  // namespace
+
+int fail(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return BH_OK;
+}
+
+int check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess) return BH_OK;
+  return fail(BH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int check_launch(const char *what) {
+  return check_hip(hipGetLastError(), what);
+}
+
+void *device_scratch(size_t bytes) {
+  int dev = 0;
+  if (check_hip(hipGetDevice(&dev), "hipGetDevice") != BH_OK) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch.size() <= static_cast<size_t>(dev)) g_scratch.resize(dev + 1);
+  Scratch &s = g_scratch[dev];
+  if (s.bytes >= bytes) return s.ptr;
+  // grow: the old buffer may still be read by queued work, so wait for the
+  // device before releasing it
+  if (s.ptr != nullptr) {
+    if (check_hip(hipDeviceSynchronize(), "scratch grow: hipDeviceSynchronize") != BH_OK)
+      return nullptr;
+    (void)hipFree(s.ptr);
+    s.ptr = nullptr;
+    s.bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  void *p = nullptr;
+  if (check_hip(hipMalloc(&p, want), "scratch hipMalloc") != BH_OK) return nullptr;
+  s.ptr = p;
+  s.bytes = want;
+  return p;
+}
+
+}  // namespace bh
+
+extern "C" const char *bh_last_error(void) { return bh::g_last_error.c_str(); }
+
+extern "C" const char *bh_version(void) {
+  return "bonsai-hip 0.1.0 (gfx950)";
+}
+
+extern "C" size_t bh_pq2_row_bytes(size_t ne0) { return (ne0 + 127) / 128 * 34; }

@@ -1,0 +1,151 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects bad shapes with the reference's error text
+before it touches the device (src/kernels.rs:97-109, 126-131, 175-180;
+src/weights.rs:337-341)."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+
+def test_library_exports_every_header_symbol(bh):
+    lib = bh.lib()
+    names = bh.header_symbols()
+    assert len(names) == 24
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding declares a signature for each of them
+    assert sorted(bh._SIGNATURES) == names
+
+
+def test_version_and_row_bytes(bh):
+    assert b"gfx950" in bh.lib().bh_version()
+    assert bh.pq2_row_bytes(5120) == 1360
+    assert bh.pq2_row_bytes(128) == 34
+    assert bh.pq2_row_bytes(129) == 68
+    assert bh.pq2_row_bytes(0) == 0
+
+
+def test_rms_norm_rows_shape_errors(bh):
+    lib = bh.lib()
+    st = lib.bh_rms_norm_rows(None, 8, None, 2, 4, 1e-6, None, None)
+    assert st == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "rms_norm_rows: weight len 2 != row_len 4"
+    st = lib.bh_rms_norm_rows(None, 8, None, 3, 3, 1e-6, None, None)
+    assert st == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "rms_norm_rows: x len 8 not divisible by row_len 3"
+    # row_len 0 is an error, not a division by zero
+    assert lib.bh_rms_norm_rows(None, 8, None, 0, 0, 1e-6, None, None) == bh.BH_ERR_SHAPE
+    # empty input is fine and touches nothing
+    assert lib.bh_rms_norm_rows(None, 0, None, 4, 4, 1e-6, None, None) == bh.BH_OK
+    assert bh.last_error() == ""
+
+
+def test_host_mirror_shape_errors_match(bh):
+    lib = bh.lib()
+    x = (ctypes.c_float * 8)()
+    w = (ctypes.c_float * 2)()
+    assert lib.bh_host_rms_norm_rows(x, 8, w, 2, 4, 1e-6, x) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "rms_norm_rows: weight len 2 != row_len 4"
+    assert lib.bh_host_l2_norm_rows(x, 8, 3, 1e-12, x) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "l2_norm_rows: x len 8 not divisible by row_len 3"
+    assert lib.bh_host_softmax_rows(x, 8, 3, x) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "softmax_rows: x len 8 not divisible by row_len 3"
+    assert lib.bh_host_map_inplace(x, 8, 7) == bh.BH_ERR_ARG
+
+
+def test_other_shape_errors(bh):
+    lib = bh.lib()
+    assert lib.bh_l2_norm_rows(None, 10, 4, 1e-6, None, None) == bh.BH_ERR_SHAPE
+    assert lib.bh_silu_l2_norm_rows(None, 10, 4, 1e-6, None, None) == bh.BH_ERR_SHAPE
+    assert lib.bh_softmax_rows(None, 10, 4, 1.0, None, None) == bh.BH_ERR_SHAPE
+    assert lib.bh_add_rms_norm_rows(None, None, 8, None, 3, 4, 1e-6, None, None,
+                                    None) == bh.BH_ERR_SHAPE
+    assert lib.bh_unary(9, None, None, 4, None, None) == bh.BH_ERR_ARG
+    assert bh.last_error().startswith("unary: unknown mode")
+    assert lib.bh_unary(bh.BH_SILU_MUL, None, None, 4, None, None) == bh.BH_ERR_ARG
+    assert lib.bh_pq2_embed_gather_rms(None, 5120, 10, None, 4, None, 5000, 1e-6, None, None,
+                                       None, None) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_embed_gather_rms: weight len 5000 != ne0 5120"
+    assert lib.bh_qk_norm_rope(None, None) == bh.BH_ERR_ARG
+
+
+def test_rope_argument_errors(bh):
+    lib = bh.lib()
+    sec = (ctypes.c_int32 * 4)(11, 11, 10, 0)
+    head = (ctypes.c_float * 8)()
+    assert lib.bh_host_rope_imrope(head, 8, 0, 0, 0, 0, 3, sec, 1e7) == bh.BH_ERR_SHAPE
+    assert lib.bh_host_rope_imrope(head, 8, 0, 0, 0, 0, 10, sec, 1e7) == bh.BH_ERR_SHAPE
+    zero = (ctypes.c_int32 * 4)(0, 0, 0, 0)
+    assert lib.bh_rope_imrope(None, 1, 1, 8, None, 4, zero, 1e7, None) == bh.BH_ERR_ARG
+    args = bh.make_qk_args(None, None, None, None, None, None, None, 1, 1, 0, head_dim=256,
+                           q_head_stride=256)
+    args.gate_out = 16  # any non-NULL value: rejected before use
+    assert lib.bh_qk_norm_rope(ctypes.byref(args), None) == bh.BH_ERR_SHAPE
+    assert "gate_out needs q_head_stride" in bh.last_error()
+
+
+def test_gdn_prep_argument_errors(bh):
+    lib = bh.lib()
+    a = bh.make_gdn_args(conv=None, conv_out=None, n_tok=1, conv_dim=512, l2_dim=200,
+                         head_dim=128)
+    a.conv_out = 16
+    assert lib.bh_gdn_prep_fused(ctypes.byref(a), None) == bh.BH_ERR_SHAPE
+    b = bh.make_gdn_args(n_tok=1, gate_mode=bh.BH_SILU)
+    assert lib.bh_gdn_prep_fused(ctypes.byref(b), None) == bh.BH_ERR_ARG
+
+
+def test_batch_embed_range_error_text(bh, synth):
+    """src/weights.rs:337-341: the first out-of-range token is reported."""
+    lib = bh.lib()
+    table = synth.pq2_table(synth.Rng(1), 4, 256)
+    toks = np.array([0, 4, 9], np.uint32)
+    out = np.empty((3, 256), np.float32)
+    st = lib.bh_host_batch_embed(table.ctypes.data, table.size, 256, 4, toks.ctypes.data, 3,
+                                 out.ctypes.data)
+    assert st == bh.BH_ERR_RANGE
+    assert bh.last_error() == ("Weights: row_f32(token_embd.weight): row 4 out of range "
+                               "(n_rows 4)")
+    assert lib.bh_host_decode_pq2_0_row(table.ctypes.data, 10, 256, out.ctypes.data) == \
+        bh.BH_ERR_SHAPE
+
+
+def test_splitmix64_known_vector(synth):
+    """SplitMix64 with seed 0: the published first outputs."""
+    out = synth.splitmix64(0, 0, 3)
+    assert [int(v) for v in out] == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4,
+                                     0x06C45D188009454F]
+    r = synth.Rng(0)
+    assert int(r.u64(2)[1]) == 0x6E789E6AA1B965F4
+    assert int(r.u64(1)[0]) == 0x06C45D188009454F
+
+
+def test_synth_normal_moments(synth):
+    x = synth.Rng(42).normal(200000, 1.0, 0.1)
+    assert x.dtype == np.float32
+    assert abs(x.mean() - 1.0) < 2e-3 and abs(x.std() - 0.1) < 2e-3
+
+
+def test_pq2_pack_roundtrip(oracle, synth):
+    rng = np.random.default_rng(0)
+    codes = rng.integers(0, 4, size=(3, 300), dtype=np.uint8)
+    sc = synth.f32_to_half(np.abs(rng.standard_normal(9)).astype(np.float32) * 0.02)
+    packed = synth.pack_pq2_rows(codes, sc.reshape(3, 3))
+    assert packed.shape == (3, oracle.pq2_row_bytes(300))
+    scale = oracle.half_to_f32(sc).reshape(3, 3)
+    for r in range(3):
+        v = oracle.decode_pq2_0_row(packed[r], 300)
+        expect = (codes[r].astype(np.float32) - 1) * np.repeat(scale[r], 128)[:300]
+        assert np.array_equal(v, expect)
+
+
+def test_pq2_table_distribution(oracle, synth):
+    t = synth.pq2_table(synth.Rng(5), 64, 5120)
+    v = np.stack([oracle.decode_pq2_0_row(t[r], 5120) for r in range(64)])
+    sc = oracle.half_to_f32(t.reshape(64, 40, 34)[:, :, :2].copy().view(np.uint16)[..., 0])
+    codes = np.round(v / np.repeat(sc, 128, axis=1)) + 1
+    frac = [(codes == c).mean() for c in (0, 1, 2)]
+    assert all(abs(f - p) < 0.01 for f, p in zip(frac, (0.3, 0.4, 0.3)))
+    assert abs(np.abs(sc).mean() - 0.02 * np.sqrt(2 / np.pi)) < 5e-4

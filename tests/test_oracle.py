@@ -1,0 +1,378 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Every check comes from outside the oracle's own formulas:
+  * the reference's unit tests, restated with their literal inputs/answers
+    (src/kernels.rs:761-853, src/gguf.rs:950-1033, src/rope.rs:96-114);
+  * exhaustive or closed-form facts (all 65536 f16 patterns against numpy's
+    IEEE conversion, 2-element softmax = logistic, unit-norm L2 rows,
+    rotation by a double-precision brute force with a hand-derived band table);
+  * invariants chosen so a dropped term, a wrong sign or a swapped operand
+    fails (shift invariance, pair-norm preservation, untouched tail dims).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+
+# --- src/kernels.rs:761-772 rms_norm_matches_reference ----------------------
+def test_rms_norm_matches_reference(oracle):
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    w = np.array([0.5, 1.0, 1.5, 2.0], np.float32)
+    y = oracle.rms_norm(x, w, 1e-6)
+    s = np.float32(1.0) / np.sqrt(np.float32(7.5) + np.float32(1e-6))
+    expect = x * w * s
+    assert np.all(np.abs(y - expect) < 1e-6)
+
+
+# --- src/kernels.rs:774-787 pq2_decode_known_row ----------------------------
+def test_pq2_decode_known_row(oracle):
+    raw = np.zeros(34, np.uint8)
+    raw[0], raw[1] = 0x00, 0x40  # scale 2.0
+    raw[2] = 0b11                # j=0 code 3 -> +4
+    raw[3] = 0b10_01             # j=4 code 1 -> 0, j=5 code 2 -> +2
+    v = oracle.decode_pq2_0_row(raw, 128)
+    assert v[0] == 4.0
+    assert v[1] == -2.0
+    assert v[4] == 0.0
+    assert v[5] == 2.0
+
+
+# --- src/kernels.rs:789-812 rms_norm_rows_matches_single_row_math ----------
+def test_rms_norm_rows_matches_single_row_math(oracle):
+    x = np.array([1.0, 2.0, 3.0, 4.0, 0.5, -0.5, 2.0, -3.0], np.float32)
+    w = np.array([0.5, 1.0, 1.5, 2.0], np.float32)
+    eps = np.float32(1e-6)
+    y = oracle.rms_norm_rows(x, w, 4, eps)
+    for row in range(2):
+        src = x[row * 4:(row + 1) * 4]
+        ss = np.float32(0)
+        for v in src:
+            ss = np.float32(ss + v * v)
+        scale = np.float32(1.0) / np.sqrt(ss / np.float32(4) + eps)
+        want = src * scale * w
+        assert np.all(np.abs(y[row * 4:(row + 1) * 4] - want) < 1e-6)
+    with pytest.raises(ValueError):
+        oracle.rms_norm_rows(x, w, 3, eps)       # non-divisible
+    with pytest.raises(ValueError):
+        oracle.rms_norm_rows(x, w[:2], 4, eps)   # bad weight len
+
+
+# --- src/kernels.rs:814-828 l2_norm_rows_produce_unit_rows -----------------
+def test_l2_norm_rows_produce_unit_rows(oracle):
+    x = np.array([3.0, 4.0, 0.0, 0.0, 1.0, 1.0, 1.0, 1.0], np.float32)
+    y = oracle.l2_norm_rows(x, 4, 1e-12)
+    assert abs(y[0] - 0.6) < 1e-6
+    assert abs(y[1] - 0.8) < 1e-6
+    assert abs(float(np.sum(y[4:8] ** 2)) - 1.0) < 1e-6
+    z = oracle.l2_norm_rows(np.zeros(4, np.float32), 4, 1e-6)
+    assert np.array_equal(z, np.zeros(4, np.float32))
+    with pytest.raises(ValueError):
+        oracle.l2_norm_rows(x, 3, 1e-12)
+
+
+# --- src/kernels.rs:830-838 activations_hit_expected_points ----------------
+def test_activations_hit_expected_points(oracle):
+    assert oracle.silu(0.0) == 0.0
+    assert abs(oracle.silu(1000.0) - 1000.0) < 1e-3
+    assert abs(oracle.sigmoid(0.0) - 0.5) < 1e-7
+    assert oracle.sigmoid(-1000.0) == 0.0
+    assert abs(oracle.softplus(0.0) - math.log(2.0)) < 1e-7
+    assert oracle.softplus(100.0) == 100.0
+
+
+# --- src/kernels.rs:840-853 softmax_rows_are_normalized_and_mask_safe ------
+def test_softmax_rows_are_normalized_and_mask_safe(oracle):
+    x = np.array([1.0, 2.0, 3.0, -np.inf, 0.0, 0.0, 0.0, 0.0], np.float32)
+    y = oracle.softmax_rows(x, 4)
+    assert abs(float(y[0:4].sum()) - 1.0) < 1e-6
+    assert y[3] == 0.0
+    assert abs(float(y[4:8].sum()) - 1.0) < 1e-6
+    assert np.all(np.abs(y[4:8] - 0.25) < 1e-6)
+    with pytest.raises(ValueError):
+        oracle.softmax_rows(x, 3)
+
+
+# --- src/gguf.rs:950-963 half_conversions -----------------------------------
+def test_half_conversions(oracle):
+    h = oracle.half_to_f32
+    assert h([0x3C00])[0] == 1.0
+    assert h([0xC000])[0] == -2.0
+    assert h([0x0000])[0] == 0.0
+    assert h([0x3800])[0] == 0.5
+    assert h([0x0001])[0] == np.float32(5.9604645e-8)
+    assert abs(float(h([0x03FF])[0]) - 6.097555e-5) < 1e-10
+    assert h([0x7C00]).view(np.uint32)[0] == np.float32(np.inf).view(np.uint32)
+    assert np.isnan(h([0x7E00])[0])
+
+
+def test_half_to_f32_exhaustive(oracle):
+    """All 65536 patterns against numpy's IEEE widening (which also keeps
+    NaN payloads unquieted), bit for bit."""
+    pats = np.arange(65536, dtype=np.uint16)
+    ours = oracle.half_to_f32(pats).view(np.uint32)
+    ref = pats.view(np.float16).astype(np.float32).view(np.uint32)
+    assert np.array_equal(ours, ref)
+
+
+# --- src/gguf.rs:965-984 f32_to_half_roundtrips_and_rounds -----------------
+def test_f32_to_half_roundtrips_and_rounds(oracle):
+    f = lambda v: int(oracle.f32_to_half(np.array([v], np.float32))[0])
+    assert f(1.0) == 0x3C00
+    assert f(-2.0) == 0xC000
+    assert f(0.5) == 0x3800
+    assert f(0.0) == 0x0000
+    assert f(np.inf) == 0x7C00
+    assert f(-np.inf) == 0xFC00
+    s = 0x12345678
+    mask = (1 << 64) - 1
+    vals = []
+    for _ in range(2000):
+        s ^= (s << 13) & mask
+        s ^= s >> 7
+        s ^= (s << 17) & mask
+        vals.append(np.float32(np.float32((s >> 40)) / np.float32(1 << 24) * np.float32(20.0)
+                               - np.float32(10.0)))
+    v = np.array(vals, np.float32)
+    back = oracle.half_to_f32(oracle.f32_to_half(v))
+    tol = np.maximum(np.abs(v), 1e-3) * 1e-3
+    assert np.all(np.abs(back - v) <= tol)
+
+
+def test_f32_to_half_matches_ieee_in_normal_range(oracle):
+    """In the f16 normal range the reference rounds to nearest-even, which is
+    exactly numpy's float16 cast."""
+    rng = np.random.default_rng(7)
+    v = (rng.standard_normal(200000) * 50).astype(np.float32)
+    v = v[(np.abs(v) >= 6.2e-5) & (np.abs(v) < 65000)]
+    assert np.array_equal(oracle.f32_to_half(v), v.astype(np.float16).view(np.uint16))
+
+
+def test_synth_f32_to_half_matches_oracle(oracle, synth):
+    """The vectorised generator's conversion equals the restated reference,
+    including its subnormal truncation, overflow and NaN cases."""
+    rng = np.random.default_rng(3)
+    v = np.concatenate([
+        (rng.standard_normal(100000) * 0.02).astype(np.float32),
+        (rng.standard_normal(50000) * 1e-6).astype(np.float32),
+        (rng.standard_normal(20000) * 7e4).astype(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 65520.0, 6.1e-5, 5.96e-8,
+                  2.98e-8, 1e-9], np.float32),
+    ])
+    assert np.array_equal(synth.f32_to_half(v), oracle.f32_to_half(v))
+
+
+# --- src/gguf.rs:986-1033 pq2_0_decode_matches_reference -------------------
+def test_pq2_0_decode_matches_reference(oracle):
+    data = bytearray()
+    data += (0x3800).to_bytes(2, "little") + bytes(32)
+    qs = bytearray(32)
+    qs[0] = 0b11
+    qs[1] = 0b10_01
+    data += (0x4000).to_bytes(2, "little") + bytes(qs)
+    v = oracle.decode_pq2_0_row(np.frombuffer(bytes(data), np.uint8), 256)
+    assert v[0] == -0.5
+    assert v[128] == 4.0
+    assert v[129] == -2.0
+    assert v[132] == 0.0
+    assert v[133] == 2.0
+
+
+def test_pq2_partial_block_and_row_bytes(oracle, synth):
+    """ne0 not a multiple of 128: ceil(ne0/128) blocks, last one truncated."""
+    assert oracle.pq2_row_bytes(5120) == 1360
+    assert oracle.pq2_row_bytes(130) == 68
+    assert oracle.pq2_row_bytes(0) == 0
+    codes = np.array([[3, 0, 1, 2] * 50], np.uint8)[:, :200]
+    scales = synth.f32_to_half(np.array([0.5, 0.25], np.float32)).reshape(1, 2)
+    raw = synth.pack_pq2_rows(codes, scales)[0]
+    v = oracle.decode_pq2_0_row(raw, 200)
+    expect = (codes[0].astype(np.float32) - 1) * np.where(np.arange(200) < 128, 0.5, 0.25)
+    assert np.array_equal(v, expect.astype(np.float32))
+
+
+def test_pq2_sign_of_zero_and_nonfinite_scales(oracle):
+    """code 1 times a negative scale is -0.0; x86 gives the quieted NaN for a
+    NaN scale and the default NaN 0xFFC00000 for 0 * inf."""
+    raw = np.zeros(34 * 3, np.uint8)
+    for b, h in enumerate((0xB800, 0x7D01, 0x7C00)):  # -0.5, sNaN, +inf
+        raw[34 * b], raw[34 * b + 1] = h & 0xFF, h >> 8
+        raw[34 * b + 2] = 0b10_01_00_11  # codes 3, 0, 1, 2
+    v = oracle.decode_pq2_0_row(raw, 384).view(np.uint32)
+    assert v[2] == 0x80000000                       # 0 * -0.5 = -0.0
+    assert v[128] == 0x7FC00000 | (0x101 << 13)     # quieted payload of 0x7D01
+    assert v[256 + 2] == 0xFFC00000                 # 0 * inf
+    assert v[256 + 0] == 0x7F800000                 # 2 * inf
+
+
+# --- src/rope.rs:96-114 and IMROPE facts -----------------------------------
+SECTIONS = (11, 11, 10, 0)
+
+
+def test_rope_pos0_is_identity(oracle):
+    h = np.random.default_rng(0).standard_normal(256).astype(np.float32)
+    out = oracle.rope_imrope(h, 0, 0, 0, 0, 64, SECTIONS, 1e7)
+    assert np.array_equal(out, h)
+
+
+def test_rope_preserves_pair_norm_and_tail(oracle):
+    h = np.random.default_rng(1).standard_normal(256).astype(np.float32)
+    out = oracle.rope_imrope(h, 37, 37, 37, 37, 64, SECTIONS, 1e7)
+    n0 = h[:32] ** 2 + h[32:64] ** 2
+    n1 = out[:32] ** 2 + out[32:64] ** 2
+    assert np.all(np.abs(n0 - n1) < 1e-5 * np.maximum(1, n0))
+    assert np.array_equal(out[64:], h[64:])
+
+
+def _rope_double(h, pos4, n_dims, bands, base, chain=False):
+    """Rotation in double with theta_j = p_band(j) * base^(-2j/n_dims), or
+    (chain=True) with the f32 product chain p*s*...*s of the reference."""
+    h = h.astype(np.float64)
+    out = h.copy()
+    half = n_dims // 2
+    scale = np.float32(np.power(np.float32(base), np.float32(-2.0) / np.float32(n_dims)))
+    for j in range(half):
+        if chain:
+            th = np.float32(pos4[bands[j]])
+            for _ in range(j):
+                th = np.float32(th * scale)
+            th = float(th)
+        else:
+            th = pos4[bands[j]] * base ** (-2.0 * j / n_dims)
+        c, s = math.cos(th), math.sin(th)
+        out[j] = h[j] * c - h[j + half] * s
+        out[j + half] = h[j] * s + h[j + half] * c
+    return out
+
+
+def test_rope_matches_double_brute_force_qwen35(oracle):
+    """sections [11,11,10,0], 32 pairs: sector j < 33 always, so band = j % 3
+    except j % 3 == 2 with j >= 30 -> e (hand-derived from src/rope.rs:41-49)."""
+    bands = [(j % 3 if not (j % 3 == 2 and j >= 30) else 3) for j in range(32)]
+    assert bands[30] == 0 and bands[31] == 1 and bands[29] == 2
+    h = np.random.default_rng(2).standard_normal(256).astype(np.float32)
+    for pos in [(5, 5, 5, 5), (17, 17, 17, 17), (3, 5, 7, 0), (2047, 11, 900, 3)]:
+        out = oracle.rope_imrope(h, *pos, 64, SECTIONS, 1e7)
+        # closed-form angles: the f32 chain drifts ~1e-4 rad by position 2047
+        ref = _rope_double(h, pos, 64, bands, 1e7)
+        assert rel_err(out[:64], ref[:64]) < 3e-5, pos
+        # chained angles: only the f32 rounding of cos/sin and the rotation remain
+        ref = _rope_double(h, pos, 64, bands, 1e7, chain=True)
+        assert rel_err(out[:64], ref[:64]) < 1e-6, pos
+
+
+def test_rope_band_table_small_sections(oracle):
+    """sections [1,1,1,1]: sector = j % 4 -> bands t, h, w, e repeating."""
+    bands = [0, 1, 2, 3] * 4
+    h = np.random.default_rng(3).standard_normal(32).astype(np.float32)
+    pos = (3, 50, 700, 9000)
+    out = oracle.rope_imrope(h, *pos, 32, (1, 1, 1, 1), 1e4)
+    assert rel_err(out, _rope_double(h, pos, 32, bands, 1e4)) < 3e-5
+    assert rel_err(out, _rope_double(h, pos, 32, bands, 1e4, chain=True)) < 1e-6
+    # a wrong band (e.g. t and h swapped) is far off
+    swapped = [1, 0, 2, 3] * 4
+    assert rel_err(out, _rope_double(h, pos, 32, swapped, 1e4, chain=True)) > 1e-2
+
+
+def test_rope_theta_chain_is_sequential_products(oracle):
+    """theta_j is the rounded chain p*s*s*...: checked through the angle of a
+    unit pair (x0=1, x1=0 -> (cos, sin)) at a position where the chain and
+    the closed form differ in f32."""
+    n_dims = 64
+    s = np.float32(np.power(np.float32(1e7), np.float32(-2.0) / np.float32(n_dims)))
+    h = np.zeros(256, np.float32)
+    h[31] = 1.0  # pair j = 31
+    out = oracle.rope_imrope(h, 2047, 2047, 2047, 2047, n_dims, SECTIONS, 1e7)
+    th = np.float32(2047)
+    for _ in range(31):
+        th = np.float32(th * s)
+    assert out[31] == np.float32(math.cos(float(th))) or abs(out[31] - math.cos(float(th))) < 1e-7
+    assert abs(out[63] - math.sin(float(th))) < 1e-7
+
+
+# --- softmax facts -------------------------------------------------------------
+def test_softmax_two_elements_is_logistic(oracle):
+    a, b = 0.3, -1.7
+    y = oracle.softmax_rows(np.array([a, b], np.float32), 2)
+    assert abs(y[0] - 1 / (1 + math.exp(b - a))) < 1e-7
+    assert abs(y[1] - 1 / (1 + math.exp(a - b))) < 1e-7
+
+
+def test_softmax_shift_invariance_and_temperature(oracle):
+    x = np.random.default_rng(4).standard_normal(4096).astype(np.float32) * 3
+    y = oracle.softmax_rows(x, 1024)
+    y2 = oracle.softmax_rows(x + np.float32(8.0), 1024)
+    assert rel_err(y, y2) < 1e-5
+    assert np.array_equal(oracle.softmax_rows(x, 1024, 1.0), y)  # temp 1 is a no-op
+    t = oracle.softmax_rows(x, 1024, np.float32(1.0) / np.float32(0.7))
+    assert np.array_equal(t, oracle.softmax_rows(x * (np.float32(1) / np.float32(0.7)), 1024))
+    assert np.all(np.abs(t.reshape(4, 1024).sum(1) - 1) < 1e-5)
+
+
+def test_softmax_all_masked_row_is_nan(oracle):
+    """An all -inf row gives NaN (exp(-inf - -inf)), as the reference does."""
+    y = oracle.softmax_rows(np.full(8, -np.inf, np.float32), 8)
+    assert np.all(np.isnan(y))
+
+
+# --- gate prep ---------------------------------------------------------------
+def test_gdn_gate_prep_closed_forms(oracle):
+    alpha = np.array([[0.0, 25.0, -3.0]], np.float32)
+    dt = np.array([0.0, 0.0, 1.0], np.float32)
+    a = np.array([-1.0, -2.0, -0.5], np.float32)
+    beta_raw = np.array([[0.0, -1000.0, 2.0]], np.float32)
+    gate, beta = oracle.gdn_gate_prep(alpha, dt, a, beta_raw)
+    assert abs(gate[0, 0] + math.log(2.0)) < 1e-7         # softplus(0) * -1
+    assert gate[0, 1] == np.float32(-50.0)                # identity branch above 20
+    assert abs(gate[0, 2] - (-0.5 * math.log1p(math.exp(-2.0)))) < 1e-7
+    assert beta[0, 0] == 0.5 and beta[0, 1] == 0.0
+    assert abs(beta[0, 2] - 1 / (1 + math.exp(-2.0))) < 1e-7
+
+
+def test_silu_l2_part_unit_heads(oracle):
+    conv = np.random.default_rng(5).standard_normal((3, 512)).astype(np.float32)
+    out = oracle.silu_l2_part(conv, 256, 128, 1e-6)
+    heads = out[:, :256].reshape(3, 2, 128)
+    assert np.all(np.abs((heads.astype(np.float64) ** 2).sum(-1) - 1) < 1e-5)
+    silu = conv / (1 + np.exp(-conv.astype(np.float64)))
+    assert rel_err(out[:, 256:], silu[:, 256:]) < 1e-6
+    with pytest.raises(ValueError):
+        oracle.silu_l2_part(conv, 200, 128, 1e-6)
+
+
+def test_unary_modes_closed_form(oracle):
+    x = np.linspace(-30, 30, 1001).astype(np.float32)
+    b = np.linspace(2, -2, 1001).astype(np.float32)
+    xd = x.astype(np.float64)
+    sig = 1 / (1 + np.exp(-xd))
+    sp = np.where(xd > 20, xd, np.log1p(np.exp(xd)))
+    assert rel_err(oracle.unary(0, x), xd * sig) < 1e-6
+    assert rel_err(oracle.unary(1, x), sig) < 1e-6
+    assert rel_err(oracle.unary(2, x), sp) < 1e-6
+    assert rel_err(oracle.unary(3, x, b), b * xd * sig) < 1e-6
+    assert rel_err(oracle.unary(4, x, b), b * sig) < 1e-6
+
+
+def test_embed_gather_range_error(oracle, synth):
+    table = synth.pq2_table(synth.Rng(9), 4, 256)
+    out = oracle.embed_gather(table, 256, 4, np.array([3, 0, 3], np.uint32))
+    assert np.array_equal(out[0], out[2])
+    with pytest.raises(IndexError):
+        oracle.embed_gather(table, 256, 4, np.array([1, 4], np.uint32))
+
+
+def test_embed_gather_rms_is_rms_of_rows(oracle, synth):
+    table = synth.pq2_table(synth.Rng(10), 8, 5120)
+    w = synth.Rng(11).normal(5120, 1.0, 0.1)
+    ids = np.array([7, 1, 1], np.uint32)
+    emb, nrm = oracle.embed_gather(table, 5120, 8, ids, w, 1e-6)
+    for k in range(3):
+        assert np.array_equal(nrm[k], oracle.rms_norm(emb[k], w, 1e-6))
+    xd = emb.astype(np.float64)
+    ref = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-6) * w
+    # the reference sums 5120 squares sequentially in f32: ~1e-5 from exact
+    assert rel_err(nrm, ref) < 3e-5

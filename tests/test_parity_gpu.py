@@ -1,0 +1,504 @@
+"""GPU parity: every C-ABI entry point against the CPU oracle on the same
+seeded inputs, at the benchmark configurations' full sizes and at the edge
+cases the reference's tests cover.
+
+Bars (from the benchmark definition): the PQ2_0 gather is bit-exact; float
+kernels reach max|gpu-ref|/max(|ref|,|gpu|) <= 1e-5, softmax <= 2e-5.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import bits_equal, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+TOL_SOFTMAX = 2e-5
+SECTIONS = (11, 11, 10, 0)
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _h(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm family
+# ---------------------------------------------------------------------------
+
+def test_rms_norm_known_answer(bh, dev):
+    """src/kernels.rs:761-772 on the device."""
+    x = _t(np.array([1, 2, 3, 4], np.float32), dev)
+    w = _t(np.array([0.5, 1, 1.5, 2], np.float32), dev)
+    y = _h(bh.rms_norm_rows(x, w, 1e-6))
+    s = np.float32(1) / np.sqrt(np.float32(7.5) + np.float32(1e-6))
+    assert np.all(np.abs(y - np.array([1, 2, 3, 4], np.float32) * np.array([.5, 1, 1.5, 2]) * s)
+                  < 1e-6)
+
+
+@pytest.mark.parametrize("rows,row_len", [
+    (512, 5120),        # config 1 (block-per-row, 256 lanes x 5 float4)
+    (2048 * 24, 256),   # per-head q norm (one wave per row)
+    (4096, 128),        # ssm_norm heads (half-wave rows)
+    (33, 4),            # tiny rows, 64 rows per wave
+    (7, 10240),         # 512-lane groups
+    (5, 40000),         # beyond the register scheme: looped kernel
+    (9, 7),             # odd length: looped kernel
+    (3, 2052),          # 64-lane group with a ragged last float4 column
+])
+def test_rms_norm_rows(bh, oracle, synth, dev, rows, row_len):
+    _say("rms_norm_rows", rows, row_len)
+    r = synth.Rng(rows * 7 + row_len)
+    x = r.normal(rows * row_len)
+    w = r.normal(row_len, 1.0, 0.1)
+    ref = oracle.rms_norm_rows(x, w, row_len, 1e-6)
+    got = _h(bh.rms_norm_rows(_t(x, dev), _t(w, dev), 1e-6))
+    err = rel_err(got, ref)
+    _say("  rel", err)
+    assert err <= TOL
+
+
+def test_rms_norm_unaligned_and_inplace(bh, oracle, synth, dev):
+    r = synth.Rng(3)
+    x = r.normal(1 + 64 * 256)
+    w = r.normal(256, 1.0, 0.1)
+    xt = _t(x, dev)
+    view = xt[1:]                       # 4-byte aligned only: looped kernel
+    got = _h(bh.rms_norm_rows(view, _t(w, dev), 1e-6))
+    assert rel_err(got, oracle.rms_norm_rows(x[1:], w, 256, 1e-6)) <= TOL
+    xt2 = _t(x[:64 * 256], dev)         # in place (rms_norm_inplace)
+    bh.rms_norm_rows(xt2, _t(w, dev), 1e-6, out=xt2)
+    assert rel_err(_h(xt2), oracle.rms_norm_rows(x[:64 * 256], w, 256, 1e-6)) <= TOL
+
+
+def test_rms_norm_single_vector(bh, oracle, synth, dev):
+    r = synth.Rng(4)
+    x = r.normal(5120)
+    w = r.normal(5120, 1.0, 0.1)
+    out = _t(np.zeros(5120, np.float32), dev)
+    xt, wt = _t(x, dev), _t(w, dev)
+    bh.check(bh.lib().bh_rms_norm(xt.data_ptr(), wt.data_ptr(), 5120, 1e-6, out.data_ptr(), None))
+    assert rel_err(_h(out), oracle.rms_norm(x, w, 1e-6)) <= TOL
+
+
+@pytest.mark.parametrize("rows,row_len", [(2048, 5120), (3, 36)])
+def test_add_rms_norm_rows(bh, oracle, synth, dev, rows, row_len):
+    _say("add_rms_norm_rows", rows, row_len)
+    r = synth.Rng(11)
+    x = r.normal(rows * row_len)
+    a = r.normal(rows * row_len)
+    w = r.normal(row_len, 1.0, 0.1)
+    s_ref, y_ref = oracle.add_rms_norm_rows(x, a, w, row_len, 1e-6)
+    xt = _t(x, dev)
+    s, y = bh.add_rms_norm_rows(xt, _t(a, dev), _t(w, dev), 1e-6, sum_out=xt)  # cur += in place
+    assert bits_equal(_h(s), s_ref)
+    assert rel_err(_h(y), y_ref) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# L2 / activations / gate prep
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,row_len", [(4096 * 48, 128), (16, 128), (5, 6), (4, 2048)])
+def test_l2_norm_rows(bh, oracle, synth, dev, rows, row_len):
+    _say("l2_norm_rows", rows, row_len)
+    x = synth.Rng(rows + row_len).normal(rows * row_len)
+    x[:row_len] = 0.0  # a zero row stays zero (eps floor)
+    ref = oracle.l2_norm_rows(x, row_len, 1e-6)
+    got = _h(bh.l2_norm_rows(_t(x, dev), row_len, 1e-6))
+    assert np.all(got[:row_len] == 0)
+    err = rel_err(got, ref)
+    _say("  rel", err, "bit-identical:", bits_equal(got, ref))
+    assert err <= TOL
+
+
+def test_l2_known_rows(bh, dev):
+    """src/kernels.rs:814-828 on the device."""
+    x = _t(np.array([3, 4, 0, 0, 1, 1, 1, 1], np.float32), dev)
+    y = _h(bh.l2_norm_rows(x, 4, 1e-12))
+    assert abs(y[0] - 0.6) < 1e-6 and abs(y[1] - 0.8) < 1e-6
+    assert abs(float((y[4:] ** 2).sum()) - 1) < 1e-6
+
+
+def test_silu_l2_norm_rows(bh, oracle, synth, dev):
+    x = synth.Rng(21).normal(4096 * 6144).reshape(4096, 6144)
+    ref = oracle.silu_l2_part(x, 6144, 128, 1e-6)
+    got = _h(bh.l2_norm_rows(_t(x, dev), 128, 1e-6, silu_first=True))
+    assert rel_err(got, ref) <= TOL
+
+
+SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, 20.0, 20.000002, 19.999998, 1000.0, -1000.0, 88.0,
+                    -88.0, 1e-30, -1e-30, np.inf, -np.inf, np.nan, 3.4e38, -3.4e38], np.float32)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("n", [17408, 6151, 3])
+def test_unary_modes(bh, oracle, synth, dev, mode, n):
+    r = synth.Rng(100 + mode)
+    a = r.normal(n, 0.0, 4.0)
+    a[: min(n, SPECIAL.size)] = SPECIAL[: min(n, SPECIAL.size)]
+    b = r.normal(n)
+    ref = oracle.unary(mode, a, b)
+    got = _h(bh.unary(mode, _t(a, dev), _t(b, dev)))
+    err = rel_err(got, ref)
+    _say("unary", mode, n, "rel", err)
+    assert err <= TOL
+
+
+def test_unary_special_points_exact(bh, dev):
+    """src/kernels.rs:830-838 on the device."""
+    x = _t(np.array([0.0, 1000.0, -1000.0, 100.0], np.float32), dev)
+    silu = _h(bh.unary(bh.BH_SILU, x))
+    sig = _h(bh.unary(bh.BH_SIGMOID, x))
+    sp = _h(bh.unary(bh.BH_SOFTPLUS, x))
+    assert silu[0] == 0.0 and abs(silu[1] - 1000) < 1e-3
+    assert abs(sig[0] - 0.5) < 1e-7 and sig[2] == 0.0
+    assert abs(sp[0] - np.log(2)) < 1e-7 and sp[3] == 100.0
+
+
+def test_unary_unaligned_inplace(bh, oracle, synth, dev):
+    a = synth.Rng(5).normal(1001)
+    t = _t(a, dev)
+    v = t[1:]
+    bh.unary(bh.BH_SOFTPLUS, v, out=v)
+    assert rel_err(_h(v), oracle.unary(2, a[1:])) <= TOL
+
+
+def _gdn_inputs(synth, n_tok, conv_dim, inner, n_head, seed):
+    r = synth.Rng(seed)
+    conv = r.normal(n_tok * conv_dim).reshape(n_tok, conv_dim)
+    dt = r.normal(n_tok * n_head).reshape(n_tok, n_head)
+    bias = r.normal(n_head, 0.0, 0.5)
+    A = (-np.exp(r.uniform(n_head) * 2.0)).astype(np.float32)
+    beta = r.normal(n_tok * n_head).reshape(n_tok, n_head)
+    z = r.normal(n_tok * inner).reshape(n_tok, inner)
+    y = r.normal(n_tok * inner).reshape(n_tok, inner)
+    return conv, dt, bias, A, beta, z, y
+
+
+@pytest.mark.parametrize("gate_mode", [4, 3])
+@pytest.mark.parametrize("shape", [
+    (4096, 6144, 6144, 6144, 48),    # config 3: whole conv row L2-normed, 48 gates
+    (64, 10240, 4096, 6144, 48),     # model layout: q,k (4096 ch) L2, v (6144) silu only
+    (3, 100, 60, 10, 5),             # odd widths: looped kernel
+])
+def test_gdn_prep_fused(bh, oracle, synth, dev, gate_mode, shape):
+    import torch
+    n_tok, conv_dim, l2_dim, inner, n_head = shape
+    _say("gdn_prep_fused", shape, "mode", gate_mode)
+    head_dim = 128 if conv_dim % 128 == 0 else 20
+    conv, dt, bias, A, beta, z, y = _gdn_inputs(synth, n_tok, conv_dim, inner, n_head, 2)
+    d = {k: _t(v, dev) for k, v in dict(conv=conv, dt=dt, bias=bias, A=A, beta=beta, z=z,
+                                        y=y).items()}
+    conv_out = torch.empty_like(d["conv"])
+    gated = torch.empty_like(d["z"])
+    gate = torch.empty_like(d["dt"])
+    beta_o = torch.empty_like(d["beta"])
+    args = bh.make_gdn_args(conv=d["conv"], conv_out=conv_out, z=d["z"], y=d["y"],
+                            gated_out=gated, alpha_raw=d["dt"], dt_bias=d["bias"],
+                            ssm_a=d["A"], beta_raw=d["beta"], gate_out=gate, beta_out=beta_o,
+                            n_tok=n_tok, conv_dim=conv_dim, l2_dim=l2_dim, head_dim=head_dim,
+                            inner_dim=inner, n_v_head=n_head, gate_mode=gate_mode, eps=1e-6)
+    bh.gdn_prep_fused(args)
+    ref_conv = oracle.silu_l2_part(conv, l2_dim, head_dim, 1e-6)
+    ref_gated = oracle.unary(gate_mode, z, y)
+    ref_gate, ref_beta = oracle.gdn_gate_prep(dt, bias, A, beta)
+    errs = [rel_err(_h(conv_out), ref_conv), rel_err(_h(gated), ref_gated),
+            rel_err(_h(gate), ref_gate), rel_err(_h(beta_o), ref_beta)]
+    _say("  rel conv/gated/gate/beta", errs)
+    assert max(errs) <= TOL
+
+
+def test_gdn_gate_prep_standalone(bh, oracle, synth, dev):
+    _, dt, bias, A, beta, _, _ = _gdn_inputs(synth, 4096, 4, 4, 48, 9)
+    dt[0, :4] = [25.0, 20.0, -30.0, 0.0]  # identity branch, threshold, tiny
+    g, b = bh.gdn_gate_prep(_t(dt, dev), _t(bias, dev), _t(A, dev), _t(beta, dev))
+    rg, rb = oracle.gdn_gate_prep(dt, bias, A, beta)
+    assert rel_err(_h(g), rg) <= TOL and rel_err(_h(b), rb) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# Softmax
+# ---------------------------------------------------------------------------
+
+def test_softmax_vocab_temperature(bh, oracle, synth, dev):
+    """config 4a: [64, 248320] ~N(0,3) with 1% +10 spikes, temperature 0.7
+    (split-row path)."""
+    r = synth.Rng(3)
+    n = 64 * 248320
+    x = r.normal(n, 0.0, 3.0)
+    spikes = r.uniform(n) < 0.01
+    x[spikes] += np.float32(10.0)
+    inv_t = float(np.float32(1.0) / np.float32(0.7))
+    ref = oracle.softmax_rows(x, 248320, inv_t)
+    got = _h(bh.softmax_rows(_t(x, dev), 248320, inv_t))
+    err = rel_err(got, ref)
+    sums = got.reshape(64, -1).astype(np.float64).sum(1)
+    _say("softmax vocab rel", err, "row sums", sums.min(), sums.max())
+    assert err <= TOL_SOFTMAX
+    assert np.all(np.abs(sums - 1) < 1e-4)
+
+
+def test_softmax_attention_causal(bh, oracle, synth, dev):
+    """config 4b: scores [24, 2048, 2048] ~N(0,2), -inf above the diagonal."""
+    r = synth.Rng(4)
+    x = r.normal(24 * 2048 * 2048, 0.0, 2.0).reshape(24, 2048, 2048)
+    mask = np.triu(np.ones((2048, 2048), bool), 1)
+    x[:, mask] = -np.inf
+    ref = oracle.softmax_rows(x, 2048)
+    got = _h(bh.softmax_rows(_t(x, dev), 2048))
+    err = rel_err(got, ref)
+    _say("softmax causal rel", err)
+    assert err <= TOL_SOFTMAX
+    assert np.all(got.reshape(24, 2048, 2048)[:, mask] == 0)
+
+
+@pytest.mark.parametrize("rows,row_len", [(2, 4), (1000, 7), (3, 40000), (5000, 96),
+                                          (7, 16384), (2, 1)])
+def test_softmax_shapes(bh, oracle, synth, dev, rows, row_len):
+    x = synth.Rng(rows * row_len).normal(rows * row_len, 0.0, 2.0)
+    ref = oracle.softmax_rows(x, row_len)
+    got = _h(bh.softmax_rows(_t(x, dev), row_len))
+    assert rel_err(got, ref) <= TOL_SOFTMAX
+
+
+def test_softmax_mask_safe_and_nan_rows(bh, dev):
+    """src/kernels.rs:840-853, plus an all -inf row (NaN, as the reference)."""
+    x = np.array([1, 2, 3, -np.inf, 0, 0, 0, 0, -np.inf, -np.inf, -np.inf, -np.inf], np.float32)
+    y = _h(bh.softmax_rows(_t(x, dev), 4))
+    assert abs(y[:4].sum() - 1) < 1e-6 and y[3] == 0.0
+    assert np.all(np.abs(y[4:8] - 0.25) < 1e-6)
+    assert np.all(np.isnan(y[8:]))
+    # the same on the split path (long rows)
+    big = np.full(2 * 20000, -np.inf, np.float32)
+    big[:20000] = 0.0
+    yb = _h(bh.softmax_rows(_t(big, dev), 20000))
+    assert np.allclose(yb[:20000], 1 / 20000) and np.all(np.isnan(yb[20000:]))
+
+
+def test_softmax_inplace(bh, oracle, synth, dev):
+    x = synth.Rng(8).normal(49152)
+    for row_len in (2048, 49152):
+        t = _t(x, dev)
+        bh.softmax_rows(t, row_len, out=t)
+        assert rel_err(_h(t), oracle.softmax_rows(x, row_len)) <= TOL_SOFTMAX
+
+
+# ---------------------------------------------------------------------------
+# IMROPE and the attention pre-block
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("head_dim,n_dims,sections,pos", [
+    (256, 64, SECTIONS, (37, 37, 37, 37)),
+    (256, 64, SECTIONS, (3, 5, 7, 0)),
+    (128, 32, (2, 3, 1, 2), (100, 2000, 7, 9)),
+    (256, 256, SECTIONS, (2047, 2047, 2047, 2047)),
+    (100, 20, (1, 1, 1, 1), (3, 50, 700, 9000)),   # looped kernel
+])
+def test_rope_imrope_heads(bh, oracle, synth, dev, head_dim, n_dims, sections, pos):
+    n_head = 24
+    h = synth.Rng(head_dim + n_dims).normal(n_head * head_dim).reshape(1, n_head, head_dim)
+    ref = np.stack([oracle.rope_imrope(h[0, i], *pos, n_dims, sections, 1e7)
+                    for i in range(n_head)])[None]
+    t = _t(h, dev)
+    bh.rope_imrope(t, _t(np.array([pos], np.int32), dev), n_dims, sections, 1e7)
+    err = rel_err(_h(t), ref)
+    _say("rope", head_dim, n_dims, pos, "rel", err)
+    assert err <= TOL
+
+
+def test_host_rope_mirror(bh, oracle, synth):
+    h = synth.Rng(77).normal(256)
+    sec = (ctypes.c_int32 * 4)(*SECTIONS)
+    got = h.copy()
+    bh.check(bh.lib().bh_host_rope_imrope(got.ctypes.data, 256, 37, 37, 37, 37, 64, sec, 1e7))
+    assert rel_err(got, oracle.rope_imrope(h, 37, 37, 37, 37, 64, SECTIONS, 1e7)) <= TOL
+    # pos 0 is the identity on the device too
+    z = h.copy()
+    bh.check(bh.lib().bh_host_rope_imrope(z.ctypes.data, 256, 0, 0, 0, 0, 64, sec, 1e7))
+    assert np.array_equal(z, h)
+
+
+def _qk_case(synth, n_tok, n_q, n_k, hd, seed, stride=None):
+    r = synth.Rng(seed)
+    stride = stride or hd
+    q = r.normal(n_tok * n_q * stride).reshape(n_tok, n_q, stride)
+    k = r.normal(n_tok * n_k * hd).reshape(n_tok, n_k, hd)
+    wq = r.normal(hd, 1.0, 0.1)
+    wk = r.normal(hd, 1.0, 0.1)
+    return q, k, wq, wk, synth.positions(n_tok)
+
+
+def test_qk_norm_rope_config2(bh, oracle, synth, dev):
+    """config 2: q [2048,24,256], k [2048,4,256], rotary 64, sections
+    [11,11,10,0], theta 1e7, positions 0..2047."""
+    import torch
+    q, k, wq, wk, pos = _qk_case(synth, 2048, 24, 4, 256, 1)
+    rq, rk, _ = oracle.qk_norm_rope(q, k, wq, wk, pos, 24, 4, 256, 64, SECTIONS, 1e7, 1e-6)
+    d = [_t(a, dev) for a in (q, k, wq, wk, pos)]
+    qo, ko = torch.empty_like(d[0]), torch.empty_like(d[1])
+    bh.qk_norm_rope(bh.make_qk_args(d[0], qo, d[1], ko, d[2], d[3], d[4], 2048, 24, 4))
+    eq, ek = rel_err(_h(qo), rq), rel_err(_h(ko), rk)
+    _say("qk_norm_rope config2 rel q/k", eq, ek)
+    assert eq <= TOL and ek <= TOL
+    # in place gives the same bits
+    bh.qk_norm_rope(bh.make_qk_args(d[0], d[0], d[1], d[1], d[2], d[3], d[4], 2048, 24, 4))
+    assert bits_equal(_h(d[0]), _h(qo)) and bits_equal(_h(d[1]), _h(ko))
+
+
+def test_qk_norm_rope_fused_gate_split(bh, oracle, synth, dev):
+    """attn_q rows [q | gate] per head (src/forward.rs:237-241): split, norm,
+    rope and sigmoid(gate) in one pass."""
+    import torch
+    q, k, wq, wk, pos = _qk_case(synth, 64, 24, 4, 256, 2, stride=512)
+    pos = pos + 1000
+    rq, rk, rg = oracle.qk_norm_rope(q, k, wq, wk, pos, 24, 4, 256, 64, SECTIONS, 1e7, 1e-6,
+                                     q_head_stride=512, want_gate=True)
+    d = [_t(a, dev) for a in (q, k, wq, wk, pos)]
+    qo = torch.empty((64, 24, 256), dtype=torch.float32, device=dev)
+    go = torch.empty_like(qo)
+    ko = torch.empty_like(d[1])
+    bh.qk_norm_rope(bh.make_qk_args(d[0], qo, d[1], ko, d[2], d[3], d[4], 64, 24, 4,
+                                    q_head_stride=512, gate_out=go))
+    assert rel_err(_h(qo), rq) <= TOL and rel_err(_h(ko), rk) <= TOL
+    assert rel_err(_h(go), rg) <= TOL
+
+
+@pytest.mark.parametrize("hd,n_dims,n_q,n_k", [(128, 32, 16, 0), (64, 16, 3, 5), (96, 24, 4, 2)])
+def test_qk_norm_rope_other_shapes(bh, oracle, synth, dev, hd, n_dims, n_q, n_k):
+    import torch
+    q, k, wq, wk, pos = _qk_case(synth, 37, n_q, n_k, hd, 3)
+    pos[:, 1] += 5
+    pos[:, 3] *= 3
+    rq, rk, _ = oracle.qk_norm_rope(q, k if n_k else None, wq, wk, pos, n_q, n_k, hd, n_dims,
+                                    (2, 2, 1, 1), 1e4, 1e-6)
+    d = [_t(a, dev) for a in (q, k, wq, wk, pos)]
+    qo, ko = torch.empty_like(d[0]), torch.empty_like(d[1])
+    bh.qk_norm_rope(bh.make_qk_args(d[0], qo, d[1] if n_k else None, ko if n_k else None, d[2],
+                                    d[3], d[4], 37, n_q, n_k, head_dim=hd, n_dims=n_dims,
+                                    sections=(2, 2, 1, 1), freq_base=1e4))
+    assert rel_err(_h(qo), rq) <= TOL
+    if n_k:
+        assert rel_err(_h(ko), rk) <= TOL
+
+
+# ---------------------------------------------------------------------------
+# PQ2_0 gather
+# ---------------------------------------------------------------------------
+
+def test_pq2_gather_config5_bit_exact(bh, oracle, synth, dev):
+    """config 5: table 248320 x 5120 (built on the device), 8192 uniform ids;
+    every gathered row bit-exact, fused RMSNorm within tolerance."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    table = synth.torch_pq2_table(248320, 5120, dev, generator=g)
+    ids = synth.Rng(5).u64(8192) % np.uint64(248320)
+    ids = ids.astype(np.uint32)
+    w = synth.Rng(6).normal(5120, 1.0, 0.1)
+    idt, wt = _t(ids, dev), _t(w, dev)
+    emb, nrm = bh.pq2_embed_gather(table, 5120, 248320, idt, w=wt, eps=1e-6)
+    emb_only = bh.pq2_embed_gather(table, 5120, 248320, idt)
+    host_rows = _h(table[idt.long()])
+    ref_e, ref_n = oracle.embed_gather(host_rows, 5120, 8192, np.arange(8192, dtype=np.uint32),
+                                       w, 1e-6)
+    ge, gn = _h(emb), _h(nrm)
+    assert bits_equal(ge, ref_e)
+    assert bits_equal(_h(emb_only), ref_e)
+    err = rel_err(gn, ref_n)
+    _say("gather+rms rel", err, "bit-identical:", bits_equal(gn, ref_n))
+    assert err <= TOL
+
+
+def test_pq2_gather_every_f16_scale(bh, oracle, synth, dev):
+    """All 65536 f16 scale patterns x all 4 codes (NaN payloads, infinities,
+    subnormals, -0.0 from code 1), bit-exact against the x86 reference."""
+    rows, ne0 = 128, 512 * 128
+    scales = np.arange(65536, dtype=np.uint16).reshape(rows, 512)
+    codes = np.tile(np.array([0, 1, 2, 3], np.uint8), rows * ne0 // 4).reshape(rows, ne0)
+    table = synth.pack_pq2_rows(codes, scales)
+    ids = np.arange(rows, dtype=np.uint32)[::-1].copy()
+    got = _h(bh.pq2_embed_gather(_t(table, dev), ne0, rows, _t(ids, dev)))
+    ref = oracle.embed_gather(table, ne0, rows, ids)
+    assert bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("ne0", [128, 200, 256, 5120, 130])
+def test_pq2_gather_shapes(bh, oracle, synth, dev, ne0):
+    table = synth.pq2_table(synth.Rng(ne0), 50, ne0)
+    ids = (synth.Rng(1).u64(300) % np.uint64(50)).astype(np.uint32)
+    w = synth.Rng(2).normal(ne0, 1.0, 0.1)
+    emb, nrm = bh.pq2_embed_gather(_t(table, dev), ne0, 50, _t(ids, dev), w=_t(w, dev))
+    ref_e, ref_n = oracle.embed_gather(table, ne0, 50, ids, w, 1e-6)
+    assert bits_equal(_h(emb), ref_e)
+    assert rel_err(_h(nrm), ref_n) <= TOL
+
+
+def test_pq2_gather_bad_ids(bh, synth, dev):
+    import torch
+    table = synth.pq2_table(synth.Rng(1), 10, 5120)
+    ids = np.array([3, 10, 2, 4000000000], np.uint32)
+    bad = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    out = bh.pq2_embed_gather(_t(table, dev), 5120, 10, _t(ids, dev), bad_id=bad)
+    o = _h(out)
+    assert np.all(o[1] == 0) and np.all(o[3] == 0) and np.any(o[0] != 0)
+    assert int(_h(bad)[0]) & 0xFFFFFFFF in (10, 4000000000)
+
+
+def test_host_mirrors(bh, oracle, synth):
+    lib = bh.lib()
+    table = synth.pq2_table(synth.Rng(3), 20, 5120)
+    toks = np.array([19, 0, 7, 7], np.uint32)
+    out = np.empty((4, 5120), np.float32)
+    bh.check(lib.bh_host_batch_embed(table.ctypes.data, table.size, 5120, 20, toks.ctypes.data,
+                                     4, out.ctypes.data))
+    assert bits_equal(out, oracle.embed_gather(table, 5120, 20, toks))
+    row = np.empty(5120, np.float32)
+    bh.check(lib.bh_host_decode_pq2_0_row(table[7].ctypes.data, 1360, 5120, row.ctypes.data))
+    assert bits_equal(row, oracle.decode_pq2_0_row(table[7], 5120))
+    x = synth.Rng(4).normal(8 * 256)
+    w = synth.Rng(5).normal(256, 1.0, 0.1)
+    y = np.empty_like(x)
+    bh.check(lib.bh_host_rms_norm_rows(x.ctypes.data, x.size, w.ctypes.data, 256, 256, 1e-6,
+                                       y.ctypes.data))
+    assert rel_err(y, oracle.rms_norm_rows(x, w, 256, 1e-6)) <= TOL
+    bh.check(lib.bh_host_l2_norm_rows(x.ctypes.data, x.size, 128, 1e-6, y.ctypes.data))
+    assert rel_err(y, oracle.l2_norm_rows(x, 128, 1e-6)) <= TOL
+    bh.check(lib.bh_host_softmax_rows(x.ctypes.data, x.size, 256, y.ctypes.data))
+    assert rel_err(y, oracle.softmax_rows(x, 256)) <= TOL_SOFTMAX
+    m = x.copy()
+    bh.check(lib.bh_host_map_inplace(m.ctypes.data, m.size, bh.BH_SOFTPLUS))
+    assert rel_err(m, oracle.unary(2, x)) <= TOL
+    v = x[:5120].copy() if x.size >= 5120 else synth.Rng(6).normal(5120)
+    wv = synth.Rng(7).normal(v.size, 1.0, 0.1)
+    yv = np.empty_like(v)
+    bh.check(lib.bh_host_rms_norm(v.ctypes.data, v.size, wv.ctypes.data, 1e-6, yv.ctypes.data))
+    assert rel_err(yv, oracle.rms_norm(v, wv, 1e-6)) <= TOL
+
+
+def test_side_stream(bh, oracle, synth, dev):
+    """Work enqueued on a non-default stream lands there."""
+    import torch
+    s = torch.cuda.Stream()
+    x = synth.Rng(9).normal(4096 * 256)
+    w = synth.Rng(10).normal(256, 1.0, 0.1)
+    xt, wt = _t(x, dev), _t(w, dev)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        y = bh.rms_norm_rows(xt, wt, 1e-6, stream=s)
+    s.synchronize()
+    assert rel_err(y.cpu().numpy(), oracle.rms_norm_rows(x, w, 256, 1e-6)) <= TOL
