@@ -50,18 +50,28 @@ def n_sets(bytes_per_set: int, max_sets: int = 32) -> int:
 
 
 def time_launches(launch, n_rot: int, steps: int, warmup: int, stream) -> float:
-    """Average ms per launch, HIP events on the launch stream."""
+    """Average ms per launch.  The W warmup launches run eagerly; the K timed
+    launches are captured into one HIP graph (so the Python/ctypes launch
+    cost does not space them out) and replayed once between two HIP events
+    recorded on the launch stream, with synchronisation on both sides."""
     import torch
-    for i in range(warmup):
+    for i in range(max(1, warmup)):
         launch(i % n_rot)
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(steps):
-        launch(i % n_rot)
-    e1.record(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            launch(i % n_rot)
+    with torch.cuda.stream(stream):  # replay() launches on the current stream
+        graph.replay()  # untimed: first replay uploads the graph
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
     torch.cuda.synchronize()
+    del graph
     return e0.elapsed_time(e1) / steps
 
 

@@ -85,6 +85,16 @@ __device__ __forceinline__ T group_reduce(T v, Op op, T *lds) {
   return v;
 }
 
+// Streaming 16-byte load that is not kept in the caches (data read once).
+__device__ __forceinline__ float4 load_stream(const float4 *p) {
+  float4 v;
+  v.x = __builtin_nontemporal_load(&p->x);
+  v.y = __builtin_nontemporal_load(&p->y);
+  v.z = __builtin_nontemporal_load(&p->z);
+  v.w = __builtin_nontemporal_load(&p->w);
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // Device: scalar functions of the reference
 // ---------------------------------------------------------------------------

@@ -8,13 +8,12 @@
 //   bh_gdn_prep_fused   every small op of a recurrent layer for a batch of
 //                       tokens, one launch (src/forward.rs:497-551)
 //
-// All of these are streaming, HBM-bound maps.  The elementwise kernel gives
-// every block a contiguous run of 4 x 256 float4 (16 KB per input), issued as
-// four independent 16-byte loads per lane before any math.  The fused gate
-// prep gives one block one token: the token's conv row (silu, then L2 per
-// head of head_dim lanes-groups reduced with shuffles in f64, as
-// src/kernels.rs:134-140), its z/y gate row and its n_v_head scalar gates,
-// so a recurrent layer's prep is a single pass over its inputs.
+// All of these are streaming, HBM-bound maps, written in the shape that
+// streams best on this GPU: one 16-byte vector per lane, many short blocks.
+// The fused gate prep covers a token with a few such blocks: its conv row
+// (silu, then L2 per head of head_dim/4-lane groups reduced with shuffles in
+// f64, as src/kernels.rs:134-140), its z/y gate row and its n_v_head scalar
+// gates, so a recurrent layer's prep is one pass over its inputs.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -25,7 +24,7 @@ namespace bh {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 1;  // float4 per lane: one streams best here
 
 template <int MODE>
 __device__ __forceinline__ float unary_op(float a, float b) {
@@ -139,71 +138,55 @@ __device__ __forceinline__ float4 silu4(float4 v) {
   return make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
 }
 
-// One block per token; G = head_dim / 4 lanes per L2 head.
+// One float4 per lane.  A token's work is split over bc conv blocks (256
+// float4 = 8 L2 heads of 128 each) and bg gate blocks (256 float4 of z/y);
+// the first conv block of a token also computes its n_v_head scalar gates.
+// G = head_dim / 4 lanes per L2 head (a divisor of 256, so heads never
+// straddle blocks).
 template <int G>
-__global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a) {
-  const size_t t = blockIdx.x;
+__global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a, int bc, int bg) {
+  const int per_tok = bc + bg;
+  const size_t t = blockIdx.x / per_tok;
+  const int part = blockIdx.x % per_tok;
   const int tid = threadIdx.x;
 
-  // (1) scalar gates of this token
-  for (int h = tid; h < a.n_v_head; h += kBlock) small_gates(a, t * a.n_v_head + h, h);
-
-  // (2) conv row: silu, then L2 per head over the first l2_dim channels
-  if (a.conv_out != nullptr) {
+  if (part < bc) {
     const int n4 = a.conv_dim >> 2;
-    const int l2_4 = a.l2_dim >> 2;
+    const int i = part * kBlock + tid;
     const float4 *c4 = reinterpret_cast<const float4 *>(a.conv) + t * n4;
-    float4 *o4 = reinterpret_cast<float4 *>(a.conv_out) + t * n4;
-    for (int base = 0; base < n4; base += kBlock * kUnroll) {  // uniform trip count
-      float4 v[kUnroll];
+    float4 v = i < n4 ? c4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (part == 0)
+      for (int h = tid; h < a.n_v_head; h += kBlock) small_gates(a, t * a.n_v_head + h, h);
+    // conv output: silu, then L2 per head over the first l2_dim channels
+    float4 s = silu4(v);
+    double ss = static_cast<double>(s.x) * static_cast<double>(s.x);
+    ss += static_cast<double>(s.y) * static_cast<double>(s.y);
+    ss += static_cast<double>(s.z) * static_cast<double>(s.z);
+    ss += static_cast<double>(s.w) * static_cast<double>(s.w);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int i = base + u * kBlock + tid;
-        v[u] = i < n4 ? c4[i] : make_float4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int i = base + u * kBlock + tid;
-        float4 s = silu4(v[u]);
-        double ss = static_cast<double>(s.x) * static_cast<double>(s.x);
-        ss += static_cast<double>(s.y) * static_cast<double>(s.y);
-        ss += static_cast<double>(s.z) * static_cast<double>(s.z);
-        ss += static_cast<double>(s.w) * static_cast<double>(s.w);
-#pragma unroll
-        for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        if (i < l2_4) {
-          const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
-          s = make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
-        }
-        if (i < n4) o4[i] = s;
-      }
+    for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (i < (a.l2_dim >> 2)) {
+      const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
+      s = make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
     }
-  }
-
-  // (3) output gate row: y * act(z)
-  if (a.gated_out != nullptr) {
+    if (i < n4) reinterpret_cast<float4 *>(a.conv_out)[t * n4 + i] = s;
+  } else {
+    // output gate row: y * act(z)
     const int n4 = a.inner_dim >> 2;
-    const float4 *z4 = reinterpret_cast<const float4 *>(a.z) + t * n4;
-    const float4 *y4 = reinterpret_cast<const float4 *>(a.y) + t * n4;
-    float4 *o4 = reinterpret_cast<float4 *>(a.gated_out) + t * n4;
-    for (int base = 0; base < n4; base += kBlock * kUnroll) {
-      float4 vz[kUnroll], vy[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int i = base + u * kBlock + tid;
-        vz[u] = i < n4 ? z4[i] : make_float4(0, 0, 0, 0);
-        vy[u] = i < n4 ? y4[i] : make_float4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int i = base + u * kBlock + tid;
-        if (i < n4) {
-          o4[i] = a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(vz[u], vy[u])
-                                 : unary_op4<BH_SILU_MUL>(vz[u], vy[u]);
-        }
-      }
+    const int i = (part - bc) * kBlock + tid;
+    if (i < n4) {
+      const float4 z = reinterpret_cast<const float4 *>(a.z)[t * n4 + i];
+      const float4 y = reinterpret_cast<const float4 *>(a.y)[t * n4 + i];
+      reinterpret_cast<float4 *>(a.gated_out)[t * n4 + i] =
+          a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(z, y) : unary_op4<BH_SILU_MUL>(z, y);
     }
   }
+}
+
+// Scalar gates only (no conv / gated rows requested).
+__global__ __launch_bounds__(kBlock) void gdn_small_gates_kernel(GdnParams a, size_t total) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i < total) small_gates(a, i, static_cast<int>(i % a.n_v_head));
 }
 
 // Looped version for layouts the fast kernel does not cover (odd widths,
@@ -334,14 +317,33 @@ extern "C" int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream)
                          (g.inner_dim % 4 == 0 && aligned16(g.z) && aligned16(g.y) &&
                           aligned16(g.gated_out));
   if (conv_fast && gate_fast) {
+    if (g.conv_out == nullptr && g.gated_out == nullptr) {
+      const size_t total = g.n_tok * static_cast<size_t>(p.n_v_head);
+      if (total == 0) return ok();
+      const size_t blocks = (total + kBlock - 1) / kBlock;
+      if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: too many gates");
+      BH_LAUNCH(gdn_small_gates_kernel, static_cast<unsigned>(blocks), kBlock, 0, st, p, total);
+      return ok();
+    }
+    // conv blocks (at least one per token: it also carries the scalar gates)
+    const int bc = g.conv_out ? static_cast<int>((g.conv_dim / 4 + kBlock - 1) / kBlock) : 1;
+    const int bg = g.gated_out ? static_cast<int>((g.inner_dim / 4 + kBlock - 1) / kBlock) : 0;
+    const size_t blocks = g.n_tok * static_cast<size_t>(bc + bg);
+    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: too many blocks");
+    const unsigned fgrid = static_cast<unsigned>(blocks);
+    if (g.conv_out == nullptr) {
+      // conv part disabled: its block only computes the scalar gates
+      p.conv_dim = 0;
+      p.l2_dim = 0;
+    }
     switch (g.conv_out == nullptr ? 64 : hq) {
-      case 1: BH_LAUNCH(gdn_prep_fused_kernel<1>, grid, kBlock, 0, st, p); return ok();
-      case 2: BH_LAUNCH(gdn_prep_fused_kernel<2>, grid, kBlock, 0, st, p); return ok();
-      case 4: BH_LAUNCH(gdn_prep_fused_kernel<4>, grid, kBlock, 0, st, p); return ok();
-      case 8: BH_LAUNCH(gdn_prep_fused_kernel<8>, grid, kBlock, 0, st, p); return ok();
-      case 16: BH_LAUNCH(gdn_prep_fused_kernel<16>, grid, kBlock, 0, st, p); return ok();
-      case 32: BH_LAUNCH(gdn_prep_fused_kernel<32>, grid, kBlock, 0, st, p); return ok();
-      case 64: BH_LAUNCH(gdn_prep_fused_kernel<64>, grid, kBlock, 0, st, p); return ok();
+      case 1: BH_LAUNCH(gdn_prep_fused_kernel<1>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
+      case 2: BH_LAUNCH(gdn_prep_fused_kernel<2>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
+      case 4: BH_LAUNCH(gdn_prep_fused_kernel<4>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
+      case 8: BH_LAUNCH(gdn_prep_fused_kernel<8>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
+      case 16: BH_LAUNCH(gdn_prep_fused_kernel<16>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
+      case 32: BH_LAUNCH(gdn_prep_fused_kernel<32>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
+      case 64: BH_LAUNCH(gdn_prep_fused_kernel<64>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
       default: break;
     }
   }

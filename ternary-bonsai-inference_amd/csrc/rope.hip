@@ -5,14 +5,14 @@
 //                     the gate half (src/forward.rs:379)
 //   bh_rope_imrope    rope::rope_imrope (src/rope.rs:9-70) over a batch of heads
 //
-// Design.  One block of 256 lanes owns one token: all of its q heads and k
-// heads (24 + 4 rows of 256 floats in Ternary-Bonsai-27B).  A head row is held
-// by G = head_dim/4 lanes, one float4 each, so the RMSNorm sum is a G-lane
-// shuffle reduction and the rotation partner of dim j (j + n_dims/2) sits in
-// lane gl + n_dims/8 of the same group: one cross-lane read per component,
-// no LDS traffic for the data.  The token's cos/sin table (n_dims/2 pairs)
-// is built once per block into LDS by the first n_dims/2 lanes, while the
-// first rows' loads are in flight.
+// Design.  A head row is held by G = head_dim/4 lanes, one float4 each, so
+// the RMSNorm sum is a G-lane shuffle reduction and the rotation partner of
+// dim j (j + n_dims/2) sits in lane gl + n_dims/8 of the same group: one
+// cross-lane read per component (a DPP row rotation for n_dims 64), no LDS
+// traffic for the data.  A block of 256 lanes holds 16 head rows of one
+// token (4 per lane group, their loads issued together); the token's
+// cos/sin table (n_dims/2 pairs) is built into LDS by the first n_dims/2
+// lanes while the rows' loads are in flight, and shared by all 16 rows.
 //
 // Angles.  The reference computes theta for pair j by multiplying the
 // position by theta_scale once per pair (src/rope.rs:54-57), so theta_j is a
@@ -32,7 +32,6 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kMaxHalf = 128;  // n_dims/2 for head_dim <= 256
-constexpr int kBatch = 4;      // rows whose loads are in flight together
 
 struct RopeParams {
   const float *q;
@@ -72,20 +71,60 @@ __device__ __forceinline__ float rot(float own, float other, float c, float s, b
   return role1 ? (other * s + own * c) : (own * c - other * s);
 }
 
-template <int G, bool NORM>
-__global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a) {
-  constexpr int SLOTS = kBlock / G;  // head rows processed side by side
+
+// Fills the cos/sin table of `half` pairs for the token at `p` into LDS.
+__device__ __forceinline__ void fill_table(const RopeParams &a, const int32_t *p, int half,
+                                           float *cs_cos, float *cs_sin) {
+  if (threadIdx.x < half) {
+    const float th = imrope_theta(threadIdx.x, p, a);
+    float sn, cn;
+    sincosf(th, &sn, &cn);
+    cs_cos[threadIdx.x] = cn;
+    cs_sin[threadIdx.x] = sn;
+  }
+}
+
+// A block holds rows of ONE token: blockDim.x/G row slots, R rows per slot
+// (the loads of all R rows go out first), one float4 per lane per row.  A
+// token's rows (q heads, then k heads) are spread over blocks_per_tok
+// consecutive blocks.  The token's cos/sin table is built in LDS by the
+// first n_dims/2 lanes while the loads are in flight.  DPP8: the rotation
+// partner is 8 lanes away (n_dims 64), a DPP row rotation inside each
+// 16-lane row instead of an LDS-crossbar permute.
+template <int G, bool NORM, int R, bool DPP8>
+__global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int blocks_per_tok) {
+  const int slots = blockDim.x / G;
   __shared__ float cs_cos[kMaxHalf];
   __shared__ float cs_sin[kMaxHalf];
 
-  const size_t t = blockIdx.x;
+  const size_t t = blockIdx.x / blocks_per_tok;
+  const int row0 = (blockIdx.x % blocks_per_tok) * slots * R + threadIdx.x / G;
   const int gl = threadIdx.x % G;
-  const int slot = threadIdx.x / G;
   const int lane = threadIdx.x & 63;
   const int n_rows = a.n_q + a.n_k;
   const int half = a.n_dims >> 1;
 
-  // rotation role of this lane's 4 dims
+  float4 x[R], g[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int r = row0 + k * slots;
+    x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    g[k] = x[k];
+    if (r < a.n_q) {
+      const float *src = a.q + (t * a.n_q + r) * a.q_stride;
+      x[k] = reinterpret_cast<const float4 *>(src)[gl];
+      if (a.gate_out != nullptr) g[k] = reinterpret_cast<const float4 *>(src + a.head_dim)[gl];
+    } else if (r < n_rows) {
+      x[k] = reinterpret_cast<const float4 *>(a.k + (t * a.n_k + (r - a.n_q)) * a.head_dim)[gl];
+    }
+  }
+  float4 wq = make_float4(1.f, 1.f, 1.f, 1.f), wk = wq;
+  if (NORM) {
+    if (a.n_q > 0) wq = reinterpret_cast<const float4 *>(a.wq)[gl];
+    if (a.n_k > 0) wk = reinterpret_cast<const float4 *>(a.wk)[gl];
+  }
+
+  // rotation partner: dim j <-> j + n_dims/2, i.e. lane gl <-> gl +- n_dims/8
   const int d0 = 4 * gl;
   const bool rotates = d0 < a.n_dims;
   const bool role1 = d0 >= half;
@@ -93,86 +132,61 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a) {
   const int src_lane = lane - gl + partner;
   const int j0 = role1 ? d0 - half : d0;
 
-  const float4 w_q = (NORM && a.n_q > 0) ? reinterpret_cast<const float4 *>(a.wq)[gl]
-                                         : make_float4(1, 1, 1, 1);
-  const float4 w_k = (NORM && a.n_k > 0) ? reinterpret_cast<const float4 *>(a.wk)[gl]
-                                         : make_float4(1, 1, 1, 1);
-
-  // Rows are visited in batches of kBatch * SLOTS; the batch base is the same
-  // for every lane of the block, so the trip count is uniform (the lane
-  // shuffles below never see a diverged group).
-  float4 v[kBatch];
-  auto load_batch = [&](int base) {
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int r = base + slot + b * SLOTS;
-      if (r < a.n_q) {
-        v[b] = reinterpret_cast<const float4 *>(a.q + (t * a.n_q + r) * a.q_stride)[gl];
-      } else if (r < n_rows) {
-        v[b] = reinterpret_cast<const float4 *>(a.k + (t * a.n_k + (r - a.n_q)) * a.head_dim)[gl];
-      } else {
-        v[b] = make_float4(0, 0, 0, 0);
-      }
-    }
-  };
-  // first batch of loads goes out before the table is built
-  load_batch(0);
-
-  if (threadIdx.x < half) {
-    const float th = imrope_theta(threadIdx.x, a.pos + 4 * t, a);
-    float s, c;
-    sincosf(th, &s, &c);
-    cs_cos[threadIdx.x] = c;
-    cs_sin[threadIdx.x] = s;
-  }
-  __syncthreads();
-  float4 cv = make_float4(1, 1, 1, 1), sv = make_float4(0, 0, 0, 0);
+  float4 cv = make_float4(1.f, 1.f, 1.f, 1.f), sv = make_float4(0.f, 0.f, 0.f, 0.f);
+  fill_table(a, a.pos + 4 * t, half, cs_cos, cs_sin);
+  __syncthreads();  // table ready
   if (rotates) {
     cv = make_float4(cs_cos[j0], cs_cos[j0 + 1], cs_cos[j0 + 2], cs_cos[j0 + 3]);
     sv = make_float4(cs_sin[j0], cs_sin[j0 + 1], cs_sin[j0 + 2], cs_sin[j0 + 3]);
   }
 
-  for (int base = 0; base < n_rows; base += kBatch * SLOTS) {
-    if (base != 0) load_batch(base);
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int r = base + slot + b * SLOTS;
-      float4 x = v[b];
-      if constexpr (NORM) {
-        float ss = x.x * x.x;
-        ss += x.y * x.y;
-        ss += x.z * x.z;
-        ss += x.w * x.w;
+  for (int k = 0; k < R; ++k) {
+    const int r = row0 + k * slots;
+    const bool is_q = r < a.n_q;
+    float4 v = x[k];
+    if constexpr (NORM) {
+      // src/kernels.rs:112-120: (x * scale) * w, scale = 1/sqrt(sum(x^2)/n + eps)
+      float ss = v.x * v.x;
+      ss += v.y * v.y;
+      ss += v.z * v.z;
+      ss += v.w * v.w;
 #pragma unroll
-        for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        const float scale = 1.0f / sqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
-        const float4 w = r < a.n_q ? w_q : w_k;
-        x.x = (x.x * scale) * w.x;
-        x.y = (x.y * scale) * w.y;
-        x.z = (x.z * scale) * w.z;
-        x.w = (x.w * scale) * w.w;
+      for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      const float scale = 1.0f / sqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
+      const float4 w = is_q ? wq : wk;
+      v.x = (v.x * scale) * w.x;
+      v.y = (v.y * scale) * w.y;
+      v.z = (v.z * scale) * w.z;
+      v.w = (v.w * scale) * w.w;
+    }
+    float px, py, pz, pw;
+    if constexpr (DPP8) {
+      // lane i <- lane i^8 inside each 16-lane row: DPP row_ror:8 (0x128)
+      px = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.x), 0x128, 0xf, 0xf, false));
+      py = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.y), 0x128, 0xf, 0xf, false));
+      pz = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.z), 0x128, 0xf, 0xf, false));
+      pw = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.w), 0x128, 0xf, 0xf, false));
+    } else {
+      px = __shfl(v.x, src_lane, 64);
+      py = __shfl(v.y, src_lane, 64);
+      pz = __shfl(v.z, src_lane, 64);
+      pw = __shfl(v.w, src_lane, 64);
+    }
+    if (rotates) {
+      v.x = rot(v.x, px, cv.x, sv.x, role1);
+      v.y = rot(v.y, py, cv.y, sv.y, role1);
+      v.z = rot(v.z, pz, cv.z, sv.z, role1);
+      v.w = rot(v.w, pw, cv.w, sv.w, role1);
+    }
+    if (is_q) {
+      reinterpret_cast<float4 *>(a.q_out + (t * a.n_q + r) * a.head_dim)[gl] = v;
+      if (a.gate_out != nullptr) {
+        reinterpret_cast<float4 *>(a.gate_out + (t * a.n_q + r) * a.head_dim)[gl] =
+            make_float4(sigmoid(g[k].x), sigmoid(g[k].y), sigmoid(g[k].z), sigmoid(g[k].w));
       }
-      const float px = __shfl(x.x, src_lane, 64);
-      const float py = __shfl(x.y, src_lane, 64);
-      const float pz = __shfl(x.z, src_lane, 64);
-      const float pw = __shfl(x.w, src_lane, 64);
-      if (rotates) {
-        x.x = rot(x.x, px, cv.x, sv.x, role1);
-        x.y = rot(x.y, py, cv.y, sv.y, role1);
-        x.z = rot(x.z, pz, cv.z, sv.z, role1);
-        x.w = rot(x.w, pw, cv.w, sv.w, role1);
-      }
-      if (r < a.n_q) {
-        reinterpret_cast<float4 *>(a.q_out + (t * a.n_q + r) * a.head_dim)[gl] = x;
-        if (a.gate_out != nullptr) {
-          const float4 g = reinterpret_cast<const float4 *>(
-              a.q + (t * a.n_q + r) * a.q_stride + a.head_dim)[gl];
-          reinterpret_cast<float4 *>(a.gate_out + (t * a.n_q + r) * a.head_dim)[gl] =
-              make_float4(sigmoid(g.x), sigmoid(g.y), sigmoid(g.z), sigmoid(g.w));
-        }
-      } else if (r < n_rows) {
-        reinterpret_cast<float4 *>(a.k_out + (t * a.n_k + (r - a.n_q)) * a.head_dim)[gl] = x;
-      }
+    } else if (r < n_rows) {
+      reinterpret_cast<float4 *>(a.k_out + (t * a.n_k + (r - a.n_q)) * a.head_dim)[gl] = v;
     }
   }
 }
@@ -228,14 +242,32 @@ int launch_rope(const RopeParams &p, size_t n_tok, hipStream_t st) {
                     aligned16(p.q_out) && (p.gate_out == nullptr || aligned16(p.gate_out)) &&
                     (p.n_k == 0 || (aligned16(p.k) && aligned16(p.k_out))) &&
                     (!NORM || (aligned16(p.wq) && (p.n_k == 0 || aligned16(p.wk))));
-  if (n_tok > 0x7fffffffu) return fail(BH_ERR_SHAPE, "rope: too many tokens");
-  const unsigned grid = static_cast<unsigned>(n_tok);
   if (fast) {
-    switch (p.head_dim / 4) {
-      case 8: BH_LAUNCH((qk_norm_rope_kernel<8, NORM>), grid, kBlock, 0, st, p); return ok();
-      case 16: BH_LAUNCH((qk_norm_rope_kernel<16, NORM>), grid, kBlock, 0, st, p); return ok();
-      case 32: BH_LAUNCH((qk_norm_rope_kernel<32, NORM>), grid, kBlock, 0, st, p); return ok();
-      case 64: BH_LAUNCH((qk_norm_rope_kernel<64, NORM>), grid, kBlock, 0, st, p); return ok();
+    // 4 waves per block, 4 rows per row slot (measured best on MI355X for
+    // the 24 + 4 heads of 256: 16 head rows per block, 1.75 blocks per token)
+    constexpr int kRowsPerSlot = 4;
+    const int G = p.head_dim / 4;
+    const int n_rows = p.n_q + p.n_k;
+    const int rows_per_block = (kBlock / G) * kRowsPerSlot;
+    const int bpt = (n_rows + rows_per_block - 1) / rows_per_block;  // blocks per token
+    const size_t blocks = n_tok * static_cast<size_t>(bpt);
+    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "rope: too many head rows");
+    const unsigned grid = static_cast<unsigned>(blocks);
+    const bool dpp8 = p.n_dims == 64 && G >= 16;
+    constexpr int R = kRowsPerSlot;
+    if (dpp8) {
+      switch (G) {
+        case 16: BH_LAUNCH((qk_norm_rope_kernel<16, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
+        case 32: BH_LAUNCH((qk_norm_rope_kernel<32, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
+        case 64: BH_LAUNCH((qk_norm_rope_kernel<64, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
+        default: break;
+      }
+    }
+    switch (G) {
+      case 8: BH_LAUNCH((qk_norm_rope_kernel<8, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+      case 16: BH_LAUNCH((qk_norm_rope_kernel<16, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+      case 32: BH_LAUNCH((qk_norm_rope_kernel<32, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+      case 64: BH_LAUNCH((qk_norm_rope_kernel<64, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
       default: break;
     }
   }

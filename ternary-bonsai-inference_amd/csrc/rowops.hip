@@ -10,16 +10,19 @@
 //
 // Design.  Every op here reads a row once from HBM and writes it once; the
 // arithmetic is < 1 flop/byte, so the roofline is HBM bandwidth and the
-// kernels are built around it:
-//   * a row is owned by a "group" of G lanes (G a power of two).  Rows of up
-//     to 256 floats are owned by part of one wave (128-float L2 heads: 32
-//     lanes, 256-float q/k heads: 64 lanes); rows of up to 2048 floats by one
-//     wave; longer rows (5120-float hidden rows) by G/64 waves of one block;
-//   * each lane holds VPT <= 8 float4 of its row in registers, loaded with
-//     16-byte coalesced loads (lane gl reads float4 gl, gl+G, ...), so the
-//     reduction and the scaled write-back need no second HBM pass;
-//   * row reductions run with cross-lane shuffles inside the wave and an LDS
-//     combine across waves, in a fixed order (deterministic output);
+// kernels are built around it.  Measured on MI355X, streaming runs fastest
+// when every lane moves only one or two 16-byte vectors (a copy at one
+// float4 per lane: 6.2 TB/s; at eight per lane: 5.3 TB/s), so rows are
+// spread over as many lanes as that takes:
+//   * rows of up to 256 floats are owned by a group of G = row_len/4 lanes
+//     inside one wave (128-float L2 heads: 32 lanes, 256-float heads: 64),
+//     one float4 per lane, several rows per 256-lane block;
+//   * longer rows are owned by one block of NT <= 1024 lanes with VPT =
+//     ceil(row_len/4/1024) float4 per lane (5120-float hidden rows: 640
+//     lanes x 2; 2048-float attention rows: 512 lanes x 1);
+//   * the row stays in registers between the reduction and the write-back
+//     (no second HBM pass); reductions are cross-lane shuffles inside the
+//     wave plus an LDS combine across waves in wave order (deterministic);
 //   * rows that do not fit this scheme (length not a multiple of 4, unaligned
 //     pointers, > 32768 floats) go to a block-per-row looped kernel; rows
 //     that are both long and few (the 248320-wide vocabulary softmax) are
@@ -37,86 +40,138 @@ namespace {
 
 constexpr int kBlock = 256;
 
-template <int G>
-constexpr int block_of() {
-  return G > kBlock ? G : kBlock;
-}
-
 template <int N>
 using IC = std::integral_constant<int, N>;
 
-// Lanes-per-row G and float4-per-lane VPT for a row of row_len floats.
+// Row geometry: G > 0 -> G lanes per row (power of two <= 64), 256-lane
+// blocks, one float4 per lane; G == 0 -> one block of NT lanes per row, VPT
+// float4 per lane.
 struct RowGeom {
   int G = 0;
   int VPT = 0;
+  int NT = 0;
 };
 
 // Returns false when the register scheme does not apply (the caller then
 // uses the looped kernel).
-bool pick_geom(size_t row_len, RowGeom &g) {
+bool pick_geom(size_t row_len, RowGeom &g, bool wave_rows = false) {
   if (row_len == 0 || (row_len & 3u) != 0) return false;
   const size_t r4 = row_len / 4;
+  if (wave_rows && r4 > 64 && r4 <= 512) {
+    // one wave per row, no block barrier (used where two reductions and a
+    // transcendental per element make barriers costly)
+    g.G = 64;
+    g.VPT = static_cast<int>((r4 + 63) / 64);
+    g.NT = kBlock;
+    return true;
+  }
   if (r4 <= 64) {
     g.G = pow2ceil(r4);
     g.VPT = 1;
-  } else if (r4 <= 512) {
-    g.G = 64;
-    g.VPT = static_cast<int>((r4 + 63) / 64);
-  } else if (r4 <= 8192) {
-    g.G = pow2ceil((r4 + 7) / 8);
-    g.VPT = static_cast<int>((r4 + g.G - 1) / g.G);
-    if (g.VPT < 4 || g.VPT > 8) return false;
-  } else {
-    return false;
+    g.NT = kBlock;
+    return true;
   }
+  if (r4 > 8192) return false;
+  const int vpt = static_cast<int>((r4 + 1023) / 1024);
+  const int lanes = static_cast<int>((r4 + vpt - 1) / vpt);
+  g.G = 0;
+  g.VPT = vpt;
+  g.NT = (lanes + 63) / 64 * 64;
   return true;
 }
 
-// Calls f(IC<G>, IC<VPT>) for the instantiated geometries; returns -999 when
-// the geometry has no instantiation.
+// Calls f(IC<G>, IC<VPT>) for the instantiated geometries; -999 if none.
 template <class F>
 int with_geom(const RowGeom &g, F &&f) {
-#define BH_G_SMALL(GV) \
-  case GV:             \
-    return f(IC<GV>{}, IC<1>{});
-#define BH_G_BIG(GV)                      \
-  case GV:                                \
-    switch (g.VPT) {                      \
-      case 4: return f(IC<GV>{}, IC<4>{}); \
-      case 5: return f(IC<GV>{}, IC<5>{}); \
-      case 6: return f(IC<GV>{}, IC<6>{}); \
-      case 7: return f(IC<GV>{}, IC<7>{}); \
-      case 8: return f(IC<GV>{}, IC<8>{}); \
-      default: return -999;               \
+  if (g.G > 0) {
+    switch (g.G) {
+      case 1: return f(IC<1>{}, IC<1>{});
+      case 2: return f(IC<2>{}, IC<1>{});
+      case 4: return f(IC<4>{}, IC<1>{});
+      case 8: return f(IC<8>{}, IC<1>{});
+      case 16: return f(IC<16>{}, IC<1>{});
+      case 32: return f(IC<32>{}, IC<1>{});
+      case 64:
+        switch (g.VPT) {
+          case 1: return f(IC<64>{}, IC<1>{});
+          case 2: return f(IC<64>{}, IC<2>{});
+          case 3: return f(IC<64>{}, IC<3>{});
+          case 4: return f(IC<64>{}, IC<4>{});
+          case 5: return f(IC<64>{}, IC<5>{});
+          case 6: return f(IC<64>{}, IC<6>{});
+          case 7: return f(IC<64>{}, IC<7>{});
+          case 8: return f(IC<64>{}, IC<8>{});
+          default: return -999;
+        }
+      default: return -999;
     }
-  switch (g.G) {
-    BH_G_SMALL(1)
-    BH_G_SMALL(2)
-    BH_G_SMALL(4)
-    BH_G_SMALL(8)
-    BH_G_SMALL(16)
-    BH_G_SMALL(32)
-    case 64:
-      switch (g.VPT) {
-        case 1: return f(IC<64>{}, IC<1>{});
-        case 2: return f(IC<64>{}, IC<2>{});
-        case 3: return f(IC<64>{}, IC<3>{});
-        case 4: return f(IC<64>{}, IC<4>{});
-        case 5: return f(IC<64>{}, IC<5>{});
-        case 6: return f(IC<64>{}, IC<6>{});
-        case 7: return f(IC<64>{}, IC<7>{});
-        case 8: return f(IC<64>{}, IC<8>{});
-        default: return -999;
-      }
-    BH_G_BIG(128)
-    BH_G_BIG(256)
-    BH_G_BIG(512)
-    BH_G_BIG(1024)
-    default:
-      return -999;
   }
-#undef BH_G_SMALL
-#undef BH_G_BIG
+  switch (g.VPT) {
+    case 1: return f(IC<0>{}, IC<1>{});
+    case 2: return f(IC<0>{}, IC<2>{});
+    case 3: return f(IC<0>{}, IC<3>{});
+    case 4: return f(IC<0>{}, IC<4>{});
+    case 5: return f(IC<0>{}, IC<5>{});
+    case 6: return f(IC<0>{}, IC<6>{});
+    case 7: return f(IC<0>{}, IC<7>{});
+    case 8: return f(IC<0>{}, IC<8>{});
+    default: return -999;
+  }
+}
+
+// Lane <-> row mapping of a geometry.
+template <int G>
+struct RowLane {
+  size_t row;  // row index
+  int gl;      // lane within the row
+  int stride;  // lanes per row
+  bool live;   // row exists (group mode pads the last block)
+  __device__ explicit RowLane(size_t rows) {
+    if constexpr (G == 0) {
+      row = blockIdx.x;
+      gl = threadIdx.x;
+      stride = blockDim.x;
+      live = true;
+    } else {
+      row = static_cast<size_t>(blockIdx.x) * (kBlock / G) + threadIdx.x / G;
+      gl = threadIdx.x % G;
+      stride = G;
+      live = row < rows;
+    }
+  }
+};
+
+// Reduction over the lanes of a row: G-lane shuffles, or (G == 0) the whole
+// block through `lds` (blockDim.x/64 entries), combined in wave order.
+template <int G, class T, class Op>
+__device__ __forceinline__ T row_reduce(T v, Op op, T *lds) {
+  if constexpr (G > 0) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    return v;
+  } else {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    T r = lds[0];
+    const int nw = blockDim.x >> 6;
+    for (int i = 1; i < nw; ++i) r = op(r, lds[i]);
+    return r;
+  }
+}
+
+constexpr int kMaxWaves = 1024 / 64;
+
+
+
+int launch_grid(const RowGeom &g, size_t rows, unsigned *grid, unsigned *block) {
+  const size_t rpb = g.G > 0 ? static_cast<size_t>(kBlock / g.G) : 1;
+  const size_t n = (rows + rpb - 1) / rpb;
+  if (n > 0x7fffffffu) return fail(BH_ERR_SHAPE, "row count exceeds the launch grid limit");
+  *grid = static_cast<unsigned>(n);
+  *block = static_cast<unsigned>(g.NT);
+  return BH_OK;
 }
 
 __device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
@@ -130,31 +185,28 @@ __device__ __forceinline__ float4 f4_zero() { return make_float4(0.f, 0.f, 0.f, 
 // operation for operation; only the order of the sum of squares differs
 // (lane partials + tree instead of one sequential loop).
 template <int G, int VPT, bool ADD>
-__global__ __launch_bounds__(block_of<G>()) void rms_rows_kernel(
+__global__ __launch_bounds__(1024) void rms_rows_kernel(
     const float *x, const float *__restrict__ r, const float *__restrict__ w,
     float *sum_out, float *out, size_t rows, int row_len, float eps) {
-  constexpr int RPB = block_of<G>() / G;
-  __shared__ float lds[block_of<G>() / 64];
-  const int gl = threadIdx.x % G;
-  const size_t row = static_cast<size_t>(blockIdx.x) * RPB + threadIdx.x / G;
-  const bool live = row < rows;
+  __shared__ float lds[kMaxWaves];
+  const RowLane<G> L(rows);
   const int r4 = row_len >> 2;
-  const size_t off = live ? row * r4 : 0;
+  const size_t off = L.live ? L.row * r4 : 0;
   const float4 *x4 = reinterpret_cast<const float4 *>(x) + off;
 
   float4 v[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int c = gl + i * G;
-    v[i] = (live && c < r4) ? x4[c] : f4_zero();
+    const int c = L.gl + i * L.stride;
+    v[i] = (L.live && c < r4) ? x4[c] : f4_zero();
   }
   if constexpr (ADD) {
     const float4 *r4p = reinterpret_cast<const float4 *>(r) + off;
     float4 *s4 = reinterpret_cast<float4 *>(sum_out) + off;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int c = gl + i * G;
-      if (live && c < r4) {
+      const int c = L.gl + i * L.stride;
+      if (L.live && c < r4) {
         const float4 a = r4p[c];
         v[i].x += a.x;
         v[i].y += a.y;
@@ -172,14 +224,14 @@ __global__ __launch_bounds__(block_of<G>()) void rms_rows_kernel(
     ss += v[i].z * v[i].z;
     ss += v[i].w * v[i].w;
   }
-  ss = group_reduce<G>(ss, SumOp{}, lds);
+  ss = row_reduce<G>(ss, SumOp{}, lds);
   const float scale = 1.0f / sqrtf(ss / static_cast<float>(row_len) + eps);
   const float4 *w4 = reinterpret_cast<const float4 *>(w);
   float4 *o4 = reinterpret_cast<float4 *>(out) + off;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int c = gl + i * G;
-    if (live && c < r4) {
+    const int c = L.gl + i * L.stride;
+    if (L.live && c < r4) {
       const float4 wv = w4[c];
       float4 o;
       o.x = (v[i].x * scale) * wv.x;
@@ -223,22 +275,19 @@ __global__ __launch_bounds__(kBlock) void rms_rows_loop_kernel(
 // out = v * (1 / max(sqrt((f32) sum_f64(v^2)), eps)), v = x or silu(x)
 // (src/kernels.rs:136-143; silu src/kernels.rs:148-150).
 template <int G, int VPT, bool SILU>
-__global__ __launch_bounds__(block_of<G>()) void l2_rows_kernel(
-    const float *x, float *out, size_t rows, int row_len, float eps) {
-  constexpr int RPB = block_of<G>() / G;
-  __shared__ double lds[block_of<G>() / 64];
-  const int gl = threadIdx.x % G;
-  const size_t row = static_cast<size_t>(blockIdx.x) * RPB + threadIdx.x / G;
-  const bool live = row < rows;
+__global__ __launch_bounds__(1024) void l2_rows_kernel(const float *x, float *out, size_t rows,
+                                                       int row_len, float eps) {
+  __shared__ double lds[kMaxWaves];
+  const RowLane<G> L(rows);
   const int r4 = row_len >> 2;
-  const size_t off = live ? row * r4 : 0;
+  const size_t off = L.live ? L.row * r4 : 0;
   const float4 *x4 = reinterpret_cast<const float4 *>(x) + off;
 
   float4 v[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int c = gl + i * G;
-    v[i] = (live && c < r4) ? x4[c] : f4_zero();
+    const int c = L.gl + i * L.stride;
+    v[i] = (L.live && c < r4) ? x4[c] : f4_zero();
     if constexpr (SILU) {
       v[i].x = silu(v[i].x);
       v[i].y = silu(v[i].y);
@@ -254,13 +303,13 @@ __global__ __launch_bounds__(block_of<G>()) void l2_rows_kernel(
     ss += static_cast<double>(v[i].z) * static_cast<double>(v[i].z);
     ss += static_cast<double>(v[i].w) * static_cast<double>(v[i].w);
   }
-  ss = group_reduce<G>(ss, SumOp{}, lds);
+  ss = row_reduce<G>(ss, SumOp{}, lds);
   const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), eps);
   float4 *o4 = reinterpret_cast<float4 *>(out) + off;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int c = gl + i * G;
-    if (live && c < r4) {
+    const int c = L.gl + i * L.stride;
+    if (L.live && c < r4) {
       o4[c] = make_float4(v[i].x * scale, v[i].y * scale, v[i].z * scale, v[i].w * scale);
     }
   }
@@ -294,24 +343,21 @@ __global__ __launch_bounds__(kBlock) void l2_rows_loop_kernel(const float *x, fl
 // e = expf(y - m); s = sum_f64(e); out = e * (1 / (f32)s)
 // (src/kernels.rs:184-200).  -inf entries give expf(-inf) = 0.
 template <int G, int VPT>
-__global__ __launch_bounds__(block_of<G>()) void softmax_rows_kernel(
-    const float *x, float *out, size_t rows, int row_len, float inv_t) {
-  constexpr int RPB = block_of<G>() / G;
-  __shared__ float lds_m[block_of<G>() / 64];
-  __shared__ double lds_s[block_of<G>() / 64];
-  const int gl = threadIdx.x % G;
-  const size_t row = static_cast<size_t>(blockIdx.x) * RPB + threadIdx.x / G;
-  const bool live = row < rows;
+__global__ __launch_bounds__(1024) void softmax_rows_kernel(const float *x, float *out, size_t rows,
+                                                            int row_len, float inv_t) {
+  __shared__ float lds_m[kMaxWaves];
+  __shared__ double lds_s[kMaxWaves];
+  const RowLane<G> L(rows);
   const int r4 = row_len >> 2;
-  const size_t off = live ? row * r4 : 0;
+  const size_t off = L.live ? L.row * r4 : 0;
   const float4 *x4 = reinterpret_cast<const float4 *>(x) + off;
   const float ninf = -INFINITY;
 
   float4 v[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int c = gl + i * G;
-    if (live && c < r4) {
+    const int c = L.gl + i * L.stride;
+    if (L.live && c < r4) {
       v[i] = x4[c];
       v[i].x *= inv_t;
       v[i].y *= inv_t;
@@ -330,12 +376,12 @@ __global__ __launch_bounds__(block_of<G>()) void softmax_rows_kernel(
     m = mx(m, v[i].z);
     m = mx(m, v[i].w);
   }
-  m = group_reduce<G>(m, mx, lds_m);
+  m = row_reduce<G>(m, mx, lds_m);
   double s = 0.0;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int c = gl + i * G;
-    if (live && c < r4) {
+    const int c = L.gl + i * L.stride;
+    if (L.live && c < r4) {
       v[i].x = expf(v[i].x - m);
       v[i].y = expf(v[i].y - m);
       v[i].z = expf(v[i].z - m);
@@ -346,13 +392,13 @@ __global__ __launch_bounds__(block_of<G>()) void softmax_rows_kernel(
       s += static_cast<double>(v[i].w);
     }
   }
-  s = group_reduce<G>(s, SumOp{}, lds_s);
+  s = row_reduce<G>(s, SumOp{}, lds_s);
   const float inv = 1.0f / static_cast<float>(s);
   float4 *o4 = reinterpret_cast<float4 *>(out) + off;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int c = gl + i * G;
-    if (live && c < r4) {
+    const int c = L.gl + i * L.stride;
+    if (L.live && c < r4) {
       o4[c] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
     }
   }
@@ -479,14 +525,14 @@ int rms_rows_impl(const float *x, const float *r, const float *w, float *sum_out
     int st_code = with_geom(g, [&](auto GC, auto VC) -> int {
       constexpr int G_ = decltype(GC)::value;
       constexpr int V_ = decltype(VC)::value;
-      unsigned grid;
-      if (int e = grid_for(rows, block_of<G_>() / G_, &grid)) return e;
+      unsigned grid, block;
+      if (int e = launch_grid(g, rows, &grid, &block)) return e;
       if (add) {
-        BH_LAUNCH((rms_rows_kernel<G_, V_, true>), grid, block_of<G_>(), 0, st, x, r, w,
-                  sum_out, out, rows, static_cast<int>(row_len), eps);
+        BH_LAUNCH((rms_rows_kernel<G_, V_, true>), grid, block, 0, st, x, r, w, sum_out, out,
+                  rows, static_cast<int>(row_len), eps);
       } else {
-        BH_LAUNCH((rms_rows_kernel<G_, V_, false>), grid, block_of<G_>(), 0, st, x, r, w,
-                  sum_out, out, rows, static_cast<int>(row_len), eps);
+        BH_LAUNCH((rms_rows_kernel<G_, V_, false>), grid, block, 0, st, x, r, w, sum_out, out,
+                  rows, static_cast<int>(row_len), eps);
       }
       return ok();
     });
@@ -514,9 +560,9 @@ int l2_rows_impl(const float *x, float *out, size_t rows, size_t row_len, float 
     int st_code = with_geom(g, [&](auto GC, auto VC) -> int {
       constexpr int G_ = decltype(GC)::value;
       constexpr int V_ = decltype(VC)::value;
-      unsigned grid;
-      if (int e = grid_for(rows, block_of<G_>() / G_, &grid)) return e;
-      BH_LAUNCH((l2_rows_kernel<G_, V_, SILU>), grid, block_of<G_>(), 0, st, x, out, rows,
+      unsigned grid, block;
+      if (int e = launch_grid(g, rows, &grid, &block)) return e;
+      BH_LAUNCH((l2_rows_kernel<G_, V_, SILU>), grid, block, 0, st, x, out, rows,
                 static_cast<int>(row_len), eps);
       return ok();
     });
@@ -634,15 +680,17 @@ extern "C" int bh_softmax_rows(const float *x, size_t x_len, size_t row_len, flo
   const size_t rows = x_len / row_len;
   hipStream_t st = as_stream(stream);
   RowGeom g;
-  const bool fits = pick_geom(row_len, g) && aligned16(x) && aligned16(out);
+  // rows of up to 2048 floats: one wave per row (no block barriers around the
+  // two reductions; measured faster than a block per row for softmax)
+  const bool fits = pick_geom(row_len, g, true) && aligned16(x) && aligned16(out);
   const bool few_long_rows = rows < 1024 && row_len >= 16384;
   if (fits && !few_long_rows) {
     int st_code = with_geom(g, [&](auto GC, auto VC) -> int {
       constexpr int G_ = decltype(GC)::value;
       constexpr int V_ = decltype(VC)::value;
-      unsigned grid;
-      if (int e = grid_for(rows, block_of<G_>() / G_, &grid)) return e;
-      BH_LAUNCH((softmax_rows_kernel<G_, V_>), grid, block_of<G_>(), 0, st, x, out, rows,
+      unsigned grid, block;
+      if (int e = launch_grid(g, rows, &grid, &block)) return e;
+      BH_LAUNCH((softmax_rows_kernel<G_, V_>), grid, block, 0, st, x, out, rows,
                 static_cast<int>(row_len), inv_temp);
       return ok();
     });
