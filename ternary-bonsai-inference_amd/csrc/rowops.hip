@@ -24,9 +24,10 @@
 //     (no second HBM pass); reductions are cross-lane shuffles inside the
 //     wave plus an LDS combine across waves in wave order (deterministic);
 //   * rows that do not fit this scheme (length not a multiple of 4, unaligned
-//     pointers, > 32768 floats) go to a block-per-row looped kernel; rows
-//     that are both long and few (the 248320-wide vocabulary softmax) are
-//     split over many blocks with an online (max, sum) first pass.
+//     pointers, > 32768 floats) go to a block-per-row looped kernel; softmax
+//     rows that are both long and few (the 248320-wide vocabulary rows) are
+//     split: pass 1 reduces 32 KB chunks to (max, f64 sum) partials, pass 2
+//     (one float4 per lane) folds a row's partials and writes it.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -404,102 +405,150 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(const float *x, floa
   }
 }
 
-// Online (max, sum) state of a stream of y values: sum of expf(y - m) in f64
-// relative to the running max m.  -inf values contribute nothing; NaN
-// poisons the sum exactly as it poisons the reference's.
+// (max, f64 sum of expf(y - max)) of a part of a row.  Merging two parts
+// rescales each sum by exp(part max - merged max) in f64.  A part with no
+// value above -inf (m = -inf) adds its sum unscaled: 0, or NaN if it held a
+// NaN, which the reference's sum carries through.  A row with no value above
+// -inf ends with S = 0 and an output of expf(-inf - -inf) * inf = NaN, as
+// the reference's.
 struct MaxSum {
   float m;
   double s;
 };
 
-__device__ __forceinline__ void ms_push(MaxSum &a, float y) {
-  if (y > a.m) {
-    a.s = (a.m == -INFINITY) ? 0.0 : a.s * static_cast<double>(expf(a.m - y));
-    a.m = y;
-  }
-  if (y != -INFINITY) a.s += static_cast<double>(expf(y - a.m));
+__device__ __forceinline__ double ms_scaled(const MaxSum &a, double M) {
+  return a.m == -INFINITY ? a.s : a.s * exp(static_cast<double>(a.m) - M);
 }
 
 __device__ __forceinline__ MaxSum ms_merge(MaxSum a, MaxSum b) {
   const float M = b.m > a.m ? b.m : a.m;
-  if (M == -INFINITY) return MaxSum{M, 0.0};
-  double s = 0.0;
-  if (a.m != -INFINITY) s += a.s * exp(static_cast<double>(a.m) - static_cast<double>(M));
-  if (b.m != -INFINITY) s += b.s * exp(static_cast<double>(b.m) - static_cast<double>(M));
-  return MaxSum{M, s};
+  const double dM = static_cast<double>(M);
+  return MaxSum{M, ms_scaled(a, dM) + ms_scaled(b, dM)};
 }
 
-// Split-row pass 1: block (c, r) reduces chunk c of row r to (max, sum).
-template <bool VEC>
-__global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(
-    const float *x, size_t row_len, size_t chunk, float inv_t, float *part_m,
-    double *part_s) {
+// Split-row pass 1: block (c, r) reduces chunk c of row r (kSplitVPT float4
+// per lane, loaded up front) to (max, sum of expf(y - max)).  The chunk max
+// comes first, so each element costs one expf.  A one-wave-per-row kernel
+// then folds each row's chunk states into (M, 1/(f32)S) for pass 2 (kernel
+// boundaries order the three launches; no block waits for another).
+constexpr int kSplitVPT = 4;
+constexpr size_t kMaxSplitRows = 65535;  // grid.y limit of passes 1 and 3
+constexpr size_t kSplitChunk4 = static_cast<size_t>(kBlock) * kSplitVPT;  // float4 per chunk
+
+struct SplitScratch {
+  double *part_s;     // [rows][nch]
+  float *part_m;      // [rows][nch]
+  float2 *row_stat;   // [rows] (M, 1/S)
+};
+
+__global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float4 *x, size_t r4,
+                                                                     float inv_t, SplitScratch sc) {
   __shared__ float lm[kBlock / 64];
   __shared__ double ls[kBlock / 64];
   const size_t r = blockIdx.y;
-  const size_t c0 = blockIdx.x * chunk;
-  const size_t c1 = (c0 + chunk < row_len) ? c0 + chunk : row_len;
-  const float *xr = x + r * row_len;
-  MaxSum a{-INFINITY, 0.0};
-  if constexpr (VEC) {
-    const float4 *x4 = reinterpret_cast<const float4 *>(xr);
-    for (size_t c = c0 / 4 + threadIdx.x; c < c1 / 4; c += kBlock) {
-      const float4 v = x4[c];
-      ms_push(a, v.x * inv_t);
-      ms_push(a, v.y * inv_t);
-      ms_push(a, v.z * inv_t);
-      ms_push(a, v.w * inv_t);
+  const int nch = gridDim.x;
+  const size_t base = r * r4 + blockIdx.x * kSplitChunk4;
+  const size_t end = (r + 1) * r4;
+  const float ninf = -INFINITY;
+  float4 v[kSplitVPT];
+#pragma unroll
+  for (int i = 0; i < kSplitVPT; ++i) {
+    const size_t c = base + threadIdx.x + i * kBlock;
+    if (c < end) {
+      v[i] = x[c];
+      v[i].x *= inv_t;
+      v[i].y *= inv_t;
+      v[i].z *= inv_t;
+      v[i].w *= inv_t;
+    } else {
+      v[i] = make_float4(ninf, ninf, ninf, ninf);
+    }
+  }
+  const MaxOp mx;
+  float m = ninf;
+#pragma unroll
+  for (int i = 0; i < kSplitVPT; ++i) {
+    m = mx(m, v[i].x);
+    m = mx(m, v[i].y);
+    m = mx(m, v[i].z);
+    m = mx(m, v[i].w);
+  }
+  m = group_reduce<kBlock>(m, mx, lm);
+  double s = 0.0;
+  if (m != ninf) {
+#pragma unroll
+    for (int i = 0; i < kSplitVPT; ++i) {
+      // masked (-inf) and padding entries give expf(-inf) = 0
+      s += static_cast<double>(expf(v[i].x - m));
+      s += static_cast<double>(expf(v[i].y - m));
+      s += static_cast<double>(expf(v[i].z - m));
+      s += static_cast<double>(expf(v[i].w - m));
     }
   } else {
-    for (size_t c = c0 + threadIdx.x; c < c1; c += kBlock) ms_push(a, xr[c] * inv_t);
-  }
+    // a chunk with no number above -inf adds 0, unless it holds a NaN
+    // (which the reference's sum carries through)
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    MaxSum b{__shfl_xor(a.m, off, 64), __shfl_xor(a.s, off, 64)};
-    a = ms_merge(a, b);
+    for (int i = 0; i < kSplitVPT; ++i)
+      if (isnan(v[i].x) || isnan(v[i].y) || isnan(v[i].z) || isnan(v[i].w)) s = NAN;
   }
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    lm[wave] = a.m;
-    ls[wave] = a.s;
-  }
-  __syncthreads();
+  s = group_reduce<kBlock>(s, SumOp{}, ls);
   if (threadIdx.x == 0) {
-    MaxSum t{lm[0], ls[0]};
-    for (int i = 1; i < kBlock / 64; ++i) t = ms_merge(t, MaxSum{lm[i], ls[i]});
-    part_m[r * gridDim.x + blockIdx.x] = t.m;
-    part_s[r * gridDim.x + blockIdx.x] = t.s;
+    sc.part_m[r * nch + blockIdx.x] = m;
+    sc.part_s[r * nch + blockIdx.x] = s;
   }
 }
 
-// Split-row pass 2: every block folds its row's chunk states in chunk order
-// (same bits in all blocks of the row), then writes expf(y - M) * inv.
-template <bool VEC>
-__global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(
-    const float *x, float *out, size_t row_len, size_t chunk, float inv_t,
-    const float *part_m, const double *part_s) {
+// Fold of a row's chunk states (one wave per row): lane i takes chunks i,
+// i+64, ...; the cross-lane tree is fixed, so results are deterministic.
+__global__ __launch_bounds__(64) void softmax_split_fold_kernel(SplitScratch sc, int nch) {
+  const size_t r = blockIdx.x;
+  const MaxOp mx;
+  const float *pm = sc.part_m + r * nch;
+  const double *ps = sc.part_s + r * nch;
+  float M = -INFINITY;
+  for (int i = threadIdx.x; i < nch; i += 64) M = mx(M, pm[i]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = mx(M, __shfl_xor(M, off, 64));
+  double S = 0.0;
+  for (int i = threadIdx.x; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off, 64);
+  if (threadIdx.x == 0) sc.row_stat[r] = make_float2(M, 1.0f / static_cast<float>(S));
+}
+
+// Split-row pass 2: one float4 per lane, expf(y - M) * (1 / (f32)S), the
+// reference's output formula, with the row's (M, 1/S) from pass 1.
+__global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float4 *x, float4 *out,
+                                                                     size_t r4, float inv_t,
+                                                                     const float2 *row_stat) {
   const size_t r = blockIdx.y;
-  const int nch = gridDim.x;
-  MaxSum t{part_m[r * nch], part_s[r * nch]};
-  for (int i = 1; i < nch; ++i) t = ms_merge(t, MaxSum{part_m[r * nch + i], part_s[r * nch + i]});
-  const float M = t.m;
-  const float inv = 1.0f / static_cast<float>(t.s);
-  const size_t c0 = blockIdx.x * chunk;
-  const size_t c1 = (c0 + chunk < row_len) ? c0 + chunk : row_len;
-  const float *xr = x + r * row_len;
-  float *orow = out + r * row_len;
-  if constexpr (VEC) {
-    const float4 *x4 = reinterpret_cast<const float4 *>(xr);
-    float4 *o4 = reinterpret_cast<float4 *>(orow);
-    for (size_t c = c0 / 4 + threadIdx.x; c < c1 / 4; c += kBlock) {
-      const float4 v = x4[c];
-      o4[c] = make_float4(expf(v.x * inv_t - M) * inv, expf(v.y * inv_t - M) * inv,
-                          expf(v.z * inv_t - M) * inv, expf(v.w * inv_t - M) * inv);
-    }
-  } else {
-    for (size_t c = c0 + threadIdx.x; c < c1; c += kBlock)
-      orow[c] = expf(xr[c] * inv_t - M) * inv;
-  }
+  const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (c >= r4) return;
+  const float2 st = row_stat[r];
+  const float4 v = x[r * r4 + c];
+  out[r * r4 + c] = make_float4(expf(v.x * inv_t - st.x) * st.y, expf(v.y * inv_t - st.x) * st.y,
+                                expf(v.z * inv_t - st.x) * st.y, expf(v.w * inv_t - st.x) * st.y);
+}
+
+// Looped fallback for rows whose length is not a multiple of 4 or whose
+// pointers are unaligned: one block per row, three sweeps (max, sum, write).
+__global__ __launch_bounds__(kBlock) void softmax_loop_kernel(const float *x, float *out,
+                                                              size_t row_len, float inv_t) {
+  __shared__ float lm[kBlock / 64];
+  __shared__ double ls[kBlock / 64];
+  const float *xr = x + blockIdx.x * row_len;
+  float *orow = out + blockIdx.x * row_len;
+  const MaxOp mx;
+  float m = -INFINITY;
+  for (size_t c = threadIdx.x; c < row_len; c += kBlock) m = mx(m, xr[c] * inv_t);
+  m = group_reduce<kBlock>(m, mx, lm);
+  double s = 0.0;
+  for (size_t c = threadIdx.x; c < row_len; c += kBlock)
+    s += static_cast<double>(expf(xr[c] * inv_t - m));
+  s = group_reduce<kBlock>(s, SumOp{}, ls);
+  const float inv = 1.0f / static_cast<float>(s);
+  // each element is read by the lane that writes it: in place is safe
+  for (size_t c = threadIdx.x; c < row_len; c += kBlock) orow[c] = expf(xr[c] * inv_t - m) * inv;
 }
 
 // ---------------------------------------------------------------------------
@@ -577,34 +626,38 @@ int l2_rows_impl(const float *x, float *out, size_t rows, size_t row_len, float 
 
 int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float inv_t,
                   hipStream_t st) {
-  if (rows > 65535) return fail(BH_ERR_SHAPE, "softmax_rows: too many wide rows for one launch");
-  // about 2048 blocks over the chip, chunks of >= 4096 floats, multiple of 4
-  size_t nch = (2048 + rows - 1) / rows;
-  const size_t max_ch = (row_len + 4095) / 4096;
-  if (nch > max_ch) nch = max_ch;
-  if (nch < 1) nch = 1;
-  if (nch > 1024) nch = 1024;
-  size_t chunk = (row_len + nch - 1) / nch;
-  chunk = (chunk + 3) & ~static_cast<size_t>(3);
-  nch = (row_len + chunk - 1) / chunk;
-  const size_t nparts = rows * nch;
-  char *scratch = static_cast<char *>(device_scratch(nparts * (sizeof(double) + sizeof(float))));
-  if (scratch == nullptr) return BH_ERR_HIP;
-  double *part_s = reinterpret_cast<double *>(scratch);
-  float *part_m = reinterpret_cast<float *>(scratch + nparts * sizeof(double));
-  const dim3 grid(static_cast<unsigned>(nch), static_cast<unsigned>(rows));
+  if (rows > kMaxSplitRows)
+    return fail(BH_ERR_SHAPE, "softmax_rows: too many wide rows for one launch");
   const bool vec = (row_len % 4 == 0) && aligned16(x) && aligned16(out);
-  if (vec) {
-    BH_LAUNCH((softmax_split_stats_kernel<true>), grid, kBlock, 0, st, x, row_len, chunk, inv_t,
-              part_m, part_s);
-    BH_LAUNCH((softmax_split_write_kernel<true>), grid, kBlock, 0, st, x, out, row_len, chunk,
-              inv_t, part_m, part_s);
-  } else {
-    BH_LAUNCH((softmax_split_stats_kernel<false>), grid, kBlock, 0, st, x, row_len, chunk, inv_t,
-              part_m, part_s);
-    BH_LAUNCH((softmax_split_write_kernel<false>), grid, kBlock, 0, st, x, out, row_len, chunk,
-              inv_t, part_m, part_s);
+  if (!vec) {
+    if (rows > 0x7fffffffu) return fail(BH_ERR_SHAPE, "softmax_rows: too many rows");
+    BH_LAUNCH(softmax_loop_kernel, static_cast<unsigned>(rows), kBlock, 0, st, x, out, row_len,
+              inv_t);
+    return ok();
   }
+  const size_t r4 = row_len / 4;
+  const size_t nch = (r4 + kSplitChunk4 - 1) / kSplitChunk4;
+  if (nch > 65535) return fail(BH_ERR_SHAPE, "softmax_rows: row too long");
+  const size_t nparts = rows * nch;
+  // scratch: per-row (M, 1/S), f64 partial sums, f32 partial maxima
+  const size_t off_s = (rows * sizeof(float2) + 15) / 16 * 16;
+  const size_t off_m = off_s + nparts * sizeof(double);
+  char *scratch = static_cast<char *>(device_scratch(off_m + nparts * sizeof(float)));
+  if (scratch == nullptr) return BH_ERR_HIP;
+  SplitScratch sc;
+  sc.row_stat = reinterpret_cast<float2 *>(scratch);
+  sc.part_s = reinterpret_cast<double *>(scratch + off_s);
+  sc.part_m = reinterpret_cast<float *>(scratch + off_m);
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  BH_LAUNCH(softmax_split_stats_kernel, dim3(static_cast<unsigned>(nch), static_cast<unsigned>(rows)),
+            kBlock, 0, st, x4, r4, inv_t, sc);
+  BH_LAUNCH(softmax_split_fold_kernel, static_cast<unsigned>(rows), 64, 0, st, sc,
+            static_cast<int>(nch));
+  const size_t wblocks = (r4 + kBlock - 1) / kBlock;
+  if (wblocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "softmax_rows: row too long");
+  BH_LAUNCH(softmax_split_write_kernel,
+            dim3(static_cast<unsigned>(wblocks), static_cast<unsigned>(rows)), kBlock, 0, st, x4,
+            reinterpret_cast<float4 *>(out), r4, inv_t, sc.row_stat);
   return ok();
 }
 

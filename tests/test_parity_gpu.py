@@ -290,6 +290,35 @@ def test_softmax_mask_safe_and_nan_rows(bh, dev):
     assert np.allclose(yb[:20000], 1 / 20000) and np.all(np.isnan(yb[20000:]))
 
 
+def test_softmax_nan_and_inf_entries(bh, oracle, synth, dev):
+    """NaN anywhere in a row makes the whole row NaN (it reaches the f64 sum),
+    +inf too (inf - inf); a row whose only finite part is one chunk still
+    normalises.  Checked on the register path and on the split path."""
+    for row_len in (2048, 40000):
+        x = synth.Rng(row_len).normal(4 * row_len)
+        x[0:row_len] = np.nan                      # all-NaN row
+        x[row_len + 17] = np.nan                   # one NaN
+        x[2 * row_len + 3] = np.inf                # one +inf
+        x[3 * row_len: 3 * row_len + row_len // 2] = -np.inf   # half masked
+        got = _h(bh.softmax_rows(_t(x, dev), row_len))
+        ref = oracle.softmax_rows(x, row_len)
+        assert rel_err(got, ref) <= TOL_SOFTMAX
+
+
+def test_softmax_split_repeated_mixed_shapes(bh, oracle, synth, dev):
+    """The wide-row path keeps per-row arrival counters in the library's
+    scratch and re-arms them itself: repeated calls with changing shapes
+    (including ones whose partials overlap earlier counters' neighbours)
+    must all give the oracle's result."""
+    cases = [(64, 248320), (3, 40000), (200, 20480), (3, 40000), (64, 248320), (1, 16384)]
+    for i, (rows, row_len) in enumerate(cases):
+        x = synth.Rng(500 + i).normal(rows * row_len, 0.0, 3.0)
+        got = _h(bh.softmax_rows(_t(x, dev), row_len, 1.25))
+        err = rel_err(got, oracle.softmax_rows(x, row_len, 1.25))
+        _say("split repeat", rows, row_len, err)
+        assert err <= TOL_SOFTMAX
+
+
 def test_softmax_inplace(bh, oracle, synth, dev):
     x = synth.Rng(8).normal(49152)
     for row_len in (2048, 49152):
