@@ -43,10 +43,15 @@ inline int pow2ceil(size_t v) {
   return p;
 }
 
-// Per-device scratch owned by the library (grown on demand, never shrunk).
-// Used only by the split-row softmax.  Returns nullptr on allocation failure
-// (the status is already recorded).
-void *device_scratch(size_t bytes);
+// Per-device scratch owned by the library (grown on demand, never shrunk),
+// one buffer per client so different entry points never share one.  Calls
+// of the same client on one device must not overlap in time.  Returns
+// nullptr on allocation failure (the status is already recorded).
+constexpr int kScratchSoftmax = 0;  // split-row softmax partials
+constexpr int kScratchGather = 1;   // fused gather + RMSNorm row scales
+constexpr int kScratchSlots = 2;
+void *device_scratch(size_t bytes, int slot);
+
 
 // ---------------------------------------------------------------------------
 // Device: reductions

@@ -10,14 +10,12 @@
 // 2-bit codes, LSB first (weight j of the block: byte j/4, bits 2*(j%4)).
 // Weight = (code - 1) * scale.
 //
-// Design.  One block of 256 lanes per output row.  The packed row (1360 B for
-// ne0 = 5120) is first staged into LDS with 16-byte loads by the first
-// row_bytes/16 lanes -- one HBM transaction stream per row, independent of
-// the odd 34-byte block stride.  Each lane then produces float4 outputs: a
-// float4 of weights 4q..4q+3 of block b is exactly byte q of that block's
-// codes, so one LDS byte plus the block's scale give one 16-byte coalesced
-// store.  The output (20 KB per row) dominates the traffic; the packed read
-// is 1/15 of it.
+// Design.  One float4 of output per lane over the flat [n_ids][ne0/4]
+// range: the lane reads its 128-block's f16 scale (an aligned halfword:
+// blocks start on even bytes) and one code byte -- exactly the 4 weights of
+// its float4 -- and stores 16 bytes.  The output (20 KB per row) dominates the
+// traffic; the packed read (1360 B per row, cache-resident across the 320
+// lanes that share it) is 1/15 of it.
 //
 // Fused RMSNorm, bit-exact.  The reference sums the 5120 squares of a row
 // one after another in f32 (src/kernels.rs:65-68); on quantised embedding
@@ -45,6 +43,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kPq2Block = 34;
+constexpr size_t kMaxSeqSmem = 128 * 1024;  // LDS of a chain block (gfx950: 160 KB per CU)
 
 // Decodes float4 number f (weights 4f..4f+3 of the row) from the staged row.
 __device__ __forceinline__ float4 decode4(const uint8_t *rowb, int f) {
@@ -60,91 +59,129 @@ __device__ __forceinline__ float4 decode4(const uint8_t *rowb, int f) {
                      pq2_weight((c >> 6) & 3u, scale, finite));
 }
 
-// Plain gather, fast path: row_bytes % 16 == 0, ne0 % 4 == 0, 16-byte
-// aligned pointers.  One block per output row.
-__global__ __launch_bounds__(kBlock) void pq2_gather_kernel(
-    const uint8_t *__restrict__ table, int row_bytes, int ne0, uint32_t n_rows,
-    const uint32_t *__restrict__ ids, float *__restrict__ out, uint32_t *bad_id) {
-  extern __shared__ uint4 stage[];
-  const size_t t = blockIdx.x;
-  const uint32_t id = ids[t];
-  const int n4 = ne0 >> 2;
-  float4 *o4 = reinterpret_cast<float4 *>(out) + t * n4;
-  if (id >= n_rows) {  // block-uniform: no barrier is skipped by only some lanes
-    if (bad_id != nullptr && threadIdx.x == 0) *bad_id = id;
-    for (int f = threadIdx.x; f < n4; f += kBlock) o4[f] = make_float4(0, 0, 0, 0);
-    return;
-  }
-  const uint4 *src = reinterpret_cast<const uint4 *>(table + static_cast<size_t>(id) * row_bytes);
-  for (int i = threadIdx.x; i < (row_bytes >> 4); i += kBlock) stage[i] = src[i];
-  __syncthreads();
-  const uint8_t *rowb = reinterpret_cast<const uint8_t *>(stage);
-  for (int f = threadIdx.x; f < n4; f += kBlock) o4[f] = decode4(rowb, f);
+// ---------------------------------------------------------------------------
+// Fused gather + RMSNorm with the reference's sequential f32 sum of squares.
+// Launch 1 = chain blocks (row scales) + embedding writer blocks; launch 2 =
+// norm writer blocks.  Requires the fast-path layout.
+// ---------------------------------------------------------------------------
+constexpr int kSeqRows = 16;               // rows per chain block = chain lanes
+constexpr int kSeqThreads = 1024;          // wave 0: chain, waves 1..15: producers
+constexpr int kChunkQ = 32;                // float4 columns per chunk (128 weights)
+constexpr int kRingStride = kSeqRows + 1;  // float4 slots per column (padded)
+
+// LDS of a chain block: staged packed rows, the per-(row, 128-block) table
+// of the four possible squared weights (row stride padded to an odd number
+// of float4 against bank conflicts) and the two-chunk ring.
+size_t seq_terms_stride(size_t row_bytes) { return (row_bytes / kPq2Block) | 1u; }
+size_t seq_smem_bytes(size_t row_bytes) {
+  return kSeqRows * row_bytes + kSeqRows * seq_terms_stride(row_bytes) * sizeof(float4) +
+         2 * kChunkQ * kRingStride * sizeof(float4);
 }
 
-// Fused gather + RMSNorm with the reference's sequential f32 sum of squares
-// (see the file comment).  Requires the fast-path layout.
-constexpr int kSeqRows = 16;                 // rows per block = chain lanes
-constexpr int kSeqThreads = 256;             // wave 0: chain, waves 1..3: producers
-constexpr int kChunkQ = 32;                  // float4 columns per chunk (128 weights)
-constexpr int kRingStride = kSeqRows + 1;    // float4 slots per column (padded)
+// Decodes float4 f of the packed row at `rowb` straight from global memory
+// (the scale halfword and one code byte; the row is 16-byte aligned and a
+// block starts on an even byte, so the halfword load is aligned).
+__device__ __forceinline__ float4 decode4_global(const uint8_t *rowb, int f) {
+  const uint8_t *blk = rowb + (f >> 5) * kPq2Block;
+  const uint32_t h = *reinterpret_cast<const uint16_t *>(blk);
+  const uint32_t c = blk[2 + (f & 31)];
+  const float scale = __uint_as_float(half_bits_to_f32_bits(h));
+  const bool finite = (h & 0x7c00u) != 0x7c00u;
+  return make_float4(pq2_weight(c & 3u, scale, finite), pq2_weight((c >> 2) & 3u, scale, finite),
+                     pq2_weight((c >> 4) & 3u, scale, finite),
+                     pq2_weight((c >> 6) & 3u, scale, finite));
+}
 
-__global__ __launch_bounds__(kSeqThreads) void pq2_gather_rms_seq_kernel(
-    const uint8_t *__restrict__ table, int row_bytes, int ne0, uint32_t n_rows,
-    const uint32_t *__restrict__ ids, int n_ids, float *__restrict__ out,
-    const float *__restrict__ w, float eps, float *__restrict__ out_norm, uint32_t *bad_id) {
-  extern __shared__ uint4 smem[];
-  const int rb16 = row_bytes >> 4;
-  uint4 *stage = smem;                                                       // [kSeqRows][rb16]
-  float4 *ring = reinterpret_cast<float4 *>(smem + kSeqRows * rb16);         // [2][kChunkQ][kRingStride]
-  __shared__ float row_scale[kSeqRows];
+struct GatherArgs {
+  const uint8_t *table;
+  const uint32_t *ids;
+  float *out;        // embedding rows
+  float *out_norm;   // norm rows
+  const float *w;
+  float *row_scale;  // [n_ids] 1/sqrt(mean(x^2)+eps), written by launch 1
+  uint32_t *bad_id;
+  int row_bytes, ne0, n_ids;
+  uint32_t n_rows;
+  float eps;
+  int n_chain;       // chain blocks in launch 1
+};
+
+// Chain block: rows [row0, row0 + kSeqRows).  The packed rows are staged in
+// LDS together with, per (row, 128-weight block), the four values the
+// reference can add for that block: fl(v * v) for v = (code - 1) * scale,
+// code 0..3 (computed with the same operations, so non-finite scales give
+// the same NaN/inf terms).  Producer waves then turn chunk c (128 columns of
+// every row) into squares by table lookup and write them to an LDS ring laid
+// out column-major; the chain wave (lane = row, alone on its SIMD) adds
+// chunk c-1 in column order (the chain is latency-bound: ~10 cycles per
+// dependent add, ~21 us per 5120-weight row).  Same additions, same order as
+// src/kernels.rs:65-68, so the scale is bit-identical to the CPU's.
+__device__ void chain_block(const GatherArgs &a, int blk, uint4 *smem) {
   __shared__ int row_ok[kSeqRows];
-
+  const int rb16 = a.row_bytes >> 4;
+  const int nblk = a.row_bytes / kPq2Block;
+  const int tstride = nblk | 1;
+  uint4 *stage = smem;                                                       // [kSeqRows][rb16]
+  float4 *terms = reinterpret_cast<float4 *>(smem + kSeqRows * rb16);        // [kSeqRows][tstride]
+  float4 *ring = terms + kSeqRows * tstride;                                 // [2][kChunkQ][kRingStride]
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const size_t row0 = static_cast<size_t>(blockIdx.x) * kSeqRows;
-  const int nr = (n_ids - static_cast<int>(row0)) < kSeqRows ? n_ids - static_cast<int>(row0)
-                                                             : kSeqRows;
-  const int n4 = ne0 >> 2;
+  const int row0 = blk * kSeqRows;
+  const int nr = (a.n_ids - row0) < kSeqRows ? a.n_ids - row0 : kSeqRows;
+  const int n4 = a.ne0 >> 2;
 
-  if (tid < kSeqRows) {
-    int ok = 0;
-    if (tid < nr) {
-      const uint32_t id = ids[row0 + tid];
-      ok = id < n_rows;
-      if (!ok && bad_id != nullptr) *bad_id = id;
-    }
-    row_ok[tid] = ok;
-  }
-  // stage the packed rows (16-byte loads; rows with a bad id are not read)
+  if (tid < kSeqRows) row_ok[tid] = tid < nr && a.ids[row0 + tid] < a.n_rows;
   for (int i = tid; i < nr * rb16; i += kSeqThreads) {
     const int r = i / rb16;
-    const int k = i - r * rb16;
-    const uint32_t id = ids[row0 + r];
-    if (id < n_rows)
-      stage[i] = reinterpret_cast<const uint4 *>(table + static_cast<size_t>(id) * row_bytes)[k];
+    const uint32_t id = a.ids[row0 + r];
+    if (id < a.n_rows)
+      stage[i] = reinterpret_cast<const uint4 *>(a.table + static_cast<size_t>(id) * a.row_bytes)[i - r * rb16];
+  }
+  __syncthreads();
+  for (int i = tid; i < nr * nblk; i += kSeqThreads) {
+    const int r = i / nblk;
+    const int b = i - r * nblk;
+    const uint8_t *bp = reinterpret_cast<const uint8_t *>(stage + r * rb16) + b * kPq2Block;
+    const uint32_t h = static_cast<uint32_t>(bp[0]) | (static_cast<uint32_t>(bp[1]) << 8);
+    const float scale = __uint_as_float(half_bits_to_f32_bits(h));
+    const bool finite = (h & 0x7c00u) != 0x7c00u;
+    float4 t;
+    float v = pq2_weight(0u, scale, finite);
+    t.x = v * v;
+    v = pq2_weight(1u, scale, finite);
+    t.y = v * v;
+    v = pq2_weight(2u, scale, finite);
+    t.z = v * v;
+    v = pq2_weight(3u, scale, finite);
+    t.w = v * v;
+    terms[r * tstride + b] = t;
   }
   __syncthreads();
 
+  // The chain is latency-bound and shares CUs with streaming writer blocks:
+  // raise this block's wave priority (wave-level, not the stream's) so writer
+  // waves do not stretch the 5120-add sequence.
+  __builtin_amdgcn_s_setprio(2);
   const int n_chunks = (n4 + kChunkQ - 1) / kChunkQ;
   float ss = 0.0f;  // chain lane `lane` accumulates row `lane`
   for (int c = 0; c <= n_chunks; ++c) {
     if (wave != 0) {
       if (c < n_chunks) {
         float4 *dst = ring + (c & 1) * (kChunkQ * kRingStride);
+        // lanes walk rows fastest: conflict-free ring writes
         for (int i = tid - 64; i < kSeqRows * kChunkQ; i += kSeqThreads - 64) {
-          const int r = i / kChunkQ;
-          const int q = i - r * kChunkQ;
+          const int r = i % kSeqRows;
+          const int q = i / kSeqRows;
           const int f = c * kChunkQ + q;
           float4 t = make_float4(0.f, 0.f, 0.f, 0.f);  // adding +0 leaves a sum unchanged
-          if (r < nr && f < n4) {
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (row_ok[r]) {
-              v = decode4(reinterpret_cast<const uint8_t *>(stage + r * rb16), f);
-              t = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
-            }
-            reinterpret_cast<float4 *>(out)[(row0 + r) * n4 + f] = v;
+          if (r < nr && f < n4 && row_ok[r]) {
+            const int b = f >> 5;
+            const uint32_t code =
+                reinterpret_cast<const uint8_t *>(stage + r * rb16)[b * kPq2Block + 2 + (f & 31)];
+            const float *tb = reinterpret_cast<const float *>(terms + r * tstride + b);
+            t = make_float4(tb[code & 3u], tb[(code >> 2) & 3u], tb[(code >> 4) & 3u],
+                            tb[code >> 6]);
           }
           dst[q * kRingStride + r] = t;
         }
@@ -162,32 +199,65 @@ __global__ __launch_bounds__(kSeqThreads) void pq2_gather_rms_seq_kernel(
     }
     __syncthreads();
   }
-  if (wave == 0 && lane < kSeqRows) {
+  if (wave == 0 && lane < nr) {
     // src/kernels.rs:69-70: mean = ss / n; scale = 1 / sqrt(mean + eps)
-    row_scale[lane] = 1.0f / sqrtf(ss / static_cast<float>(ne0) + eps);
-  }
-  __syncthreads();
-  // norm rows: column-outer so each lane loads its weight float4 once, then
-  // writes that column of every row (stores stay coalesced along each row)
-  const float4 *w4 = reinterpret_cast<const float4 *>(w);
-  for (int f = tid; f < n4; f += kSeqThreads) {
-    const float4 wv = w4[f];
-#pragma unroll 4
-    for (int r = 0; r < nr; ++r) {
-      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (row_ok[r]) {
-        const float4 v = decode4(reinterpret_cast<const uint8_t *>(stage + r * rb16), f);
-        const float scale = row_scale[r];
-        o = make_float4((v.x * scale) * wv.x, (v.y * scale) * wv.y, (v.z * scale) * wv.z,
-                        (v.w * scale) * wv.w);
-      }
-      reinterpret_cast<float4 *>(out_norm)[(row0 + r) * n4 + f] = o;
-    }
+    a.row_scale[row0 + lane] = 1.0f / sqrtf(ss / static_cast<float>(a.ne0) + a.eps);
   }
 }
 
-size_t seq_smem_bytes(size_t row_bytes) {
-  return kSeqRows * row_bytes + 2 * kChunkQ * kRingStride * sizeof(float4);
+// Launch 1: blocks [0, n_chain) are chain blocks (dispatched first, so they
+// start at once and their ~20 us add sequences run under the streaming
+// stores), the rest write the embedding rows, one float4 per lane over the
+// flat [n_ids][ne0/4] range.
+__global__ __launch_bounds__(kSeqThreads) void pq2_gather_rms_pass1_kernel(GatherArgs a) {
+  extern __shared__ uint4 smem[];
+  if (static_cast<int>(blockIdx.x) < a.n_chain) {
+    chain_block(a, blockIdx.x, smem);
+    return;
+  }
+  const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
+  const uint32_t idx = (blockIdx.x - a.n_chain) * static_cast<uint32_t>(kSeqThreads) + threadIdx.x;
+  if (idx >= static_cast<uint32_t>(a.n_ids) * n4) return;
+  const uint32_t t = idx / n4;
+  const uint32_t f = idx - t * n4;
+  const uint32_t id = a.ids[t];
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (id < a.n_rows) {
+    v = decode4_global(a.table + static_cast<size_t>(id) * a.row_bytes, f);
+  } else if (f == 0 && a.bad_id != nullptr) {
+    *a.bad_id = id;
+  }
+  reinterpret_cast<float4 *>(a.out)[idx] = v;
+}
+
+// Embedding rows (NORM false) or norm rows (NORM true: (v * scale) * w,
+// src/kernels.rs:71-73, with the row's scale), one float4 per lane over the
+// flat [n_ids][ne0/4] range (fits 32 bits: checked by the host).  One 16-byte
+// store per lane is the store shape that streams best here (measured: four
+// contiguous float4 per lane is 1.5x slower).
+template <bool NORM>
+__global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
+  const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  if (idx >= static_cast<uint32_t>(a.n_ids) * n4) return;
+  const uint32_t t = idx / n4;
+  const uint32_t f = idx - t * n4;
+  const uint32_t id = a.ids[t];
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (id < a.n_rows) {
+    const float4 v = decode4_global(a.table + static_cast<size_t>(id) * a.row_bytes, f);
+    if constexpr (NORM) {
+      const float4 wv = reinterpret_cast<const float4 *>(a.w)[f];
+      const float scale = a.row_scale[t];
+      o = make_float4((v.x * scale) * wv.x, (v.y * scale) * wv.y, (v.z * scale) * wv.z,
+                      (v.w * scale) * wv.w);
+    } else {
+      o = v;
+    }
+  } else if (!NORM && f == 0 && a.bad_id != nullptr) {
+    *a.bad_id = id;
+  }
+  reinterpret_cast<float4 *>(NORM ? a.out_norm : a.out)[idx] = o;
 }
 
 // Any ne0 / alignment: byte reads straight from the table.
@@ -243,17 +313,51 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
   const size_t row_bytes = bh_pq2_row_bytes(ne0);
   const unsigned grid = static_cast<unsigned>(n_ids);
   const uint32_t nr = static_cast<uint32_t>(n_rows);
-  const bool fast = (row_bytes % 16 == 0) && (ne0 % 4 == 0) && row_bytes <= 65536 &&
-                    aligned16(table) && aligned16(out) &&
-                    (!norm || (aligned16(out_norm) && aligned16(w)));
-  if (fast && norm && seq_smem_bytes(row_bytes) <= 65536) {
-    const unsigned sgrid = static_cast<unsigned>((n_ids + kSeqRows - 1) / kSeqRows);
-    BH_LAUNCH(pq2_gather_rms_seq_kernel, sgrid, kSeqThreads, seq_smem_bytes(row_bytes), st,
-              table, static_cast<int>(row_bytes), static_cast<int>(ne0), nr, ids,
-              static_cast<int>(n_ids), out, w, eps, out_norm, bad_id);
-  } else if (fast && !norm) {
-    BH_LAUNCH(pq2_gather_kernel, grid, kBlock, row_bytes, st, table, static_cast<int>(row_bytes),
-              static_cast<int>(ne0), nr, ids, out, bad_id);
+  // row writers: ne0/16 lanes per row, 16-byte stores, halfword table loads;
+  // the chain blocks stage rows with 16-byte loads
+  const bool rows_ok = (ne0 % 4 == 0) && n_ids * (ne0 / 4) < 0xffffff00u && aligned16(table) &&
+                       aligned16(out) && (!norm || (aligned16(out_norm) && aligned16(w)));
+  const unsigned wgrid = static_cast<unsigned>((n_ids * (ne0 / 4) + 255) / 256);
+  GatherArgs ga{};
+  ga.table = table;
+  ga.ids = ids;
+  ga.out = out;
+  ga.out_norm = out_norm;
+  ga.w = w;
+  ga.bad_id = bad_id;
+  ga.row_bytes = static_cast<int>(row_bytes);
+  ga.ne0 = static_cast<int>(ne0);
+  ga.n_ids = static_cast<int>(n_ids);
+  ga.n_rows = nr;
+  ga.eps = eps;
+  if (rows_ok && !norm) {
+    BH_LAUNCH((pq2_rows_write_kernel<false>), wgrid, 256, 0, st, ga);
+    return ok();
+  }
+  if (rows_ok && norm && row_bytes % 16 == 0 && seq_smem_bytes(row_bytes) <= kMaxSeqSmem) {
+    ga.table = table;
+    ga.ids = ids;
+    ga.out = out;
+    ga.out_norm = out_norm;
+    ga.w = w;
+    ga.bad_id = bad_id;
+    ga.row_bytes = static_cast<int>(row_bytes);
+    ga.ne0 = static_cast<int>(ne0);
+    ga.n_ids = static_cast<int>(n_ids);
+    ga.n_rows = nr;
+    ga.eps = eps;
+    ga.n_chain = static_cast<int>((n_ids + kSeqRows - 1) / kSeqRows);
+    ga.row_scale = static_cast<float *>(device_scratch(n_ids * sizeof(float), kScratchGather));
+    if (ga.row_scale == nullptr) return BH_ERR_HIP;
+    const size_t smem = seq_smem_bytes(row_bytes);
+    if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_gather_rms_pass1_kernel),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              static_cast<int>(smem)),
+                          "hipFuncSetAttribute"))
+      return e;
+    const size_t g1 = ga.n_chain + (n_ids * (ne0 / 4) + kSeqThreads - 1) / kSeqThreads;
+    BH_LAUNCH(pq2_gather_rms_pass1_kernel, static_cast<unsigned>(g1), kSeqThreads, smem, st, ga);
+    BH_LAUNCH((pq2_rows_write_kernel<true>), wgrid, 256, 0, st, ga);
   } else {
     if (norm) {
       BH_LAUNCH((pq2_gather_loop_kernel<true>), grid, kBlock, 0, st, table, row_bytes,

@@ -642,7 +642,7 @@ int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float
   // scratch: per-row (M, 1/S), f64 partial sums, f32 partial maxima
   const size_t off_s = (rows * sizeof(float2) + 15) / 16 * 16;
   const size_t off_m = off_s + nparts * sizeof(double);
-  char *scratch = static_cast<char *>(device_scratch(off_m + nparts * sizeof(float)));
+  char *scratch = static_cast<char *>(device_scratch(off_m + nparts * sizeof(float), kScratchSoftmax));
   if (scratch == nullptr) return BH_ERR_HIP;
   SplitScratch sc;
   sc.row_stat = reinterpret_cast<float2 *>(scratch);

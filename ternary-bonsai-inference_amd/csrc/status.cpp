@@ -21,7 +21,7 @@ struct Scratch {
   size_t bytes = 0;
 };
 std::mutex g_scratch_mu;
-std::vector<Scratch> g_scratch;  // indexed by device ordinal
+std::vector<Scratch> g_scratch;  // indexed by device ordinal * kScratchSlots + slot
 }  // namespace
 
 int fail(int code, const std::string &msg) {
@@ -43,12 +43,13 @@ int check_launch(const char *what) {
   return check_hip(hipGetLastError(), what);
 }
 
-void *device_scratch(size_t bytes) {
+void *device_scratch(size_t bytes, int slot) {
   int dev = 0;
   if (check_hip(hipGetDevice(&dev), "hipGetDevice") != BH_OK) return nullptr;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch.size() <= static_cast<size_t>(dev)) g_scratch.resize(dev + 1);
-  Scratch &s = g_scratch[dev];
+  const size_t idx = static_cast<size_t>(dev) * kScratchSlots + slot;
+  if (g_scratch.size() <= idx) g_scratch.resize(idx + 1);
+  Scratch &s = g_scratch[idx];
   if (s.bytes >= bytes) return s.ptr;
   // grow: the old buffer may still be read by queued work, so wait for the
   // device before releasing it

@@ -1,0 +1,90 @@
+"""HIP-graph capture of the entry points a serving loop would capture: the
+fused gather + RMSNorm (two streams, fork/join) and the wide-row softmax
+(three launches, library scratch).  Each graph is replayed several times with
+eager work and synchronisation in between; every replay must reproduce the
+eager result bit for bit."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _replay_check(make_out, run, dev, replays=4):
+    import torch
+    s = torch.cuda.Stream()
+    eager = [o.clone() for o in run(s)]
+    torch.cuda.synchronize()
+    outs = make_out()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run(s, outs)
+    for i in range(replays):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o.view(torch.int32), e.view(torch.int32)), f"replay {i} differs"
+        # unrelated eager work between replays
+        run(s)
+        torch.cuda.synchronize()
+
+
+def test_graph_gather_rms(bh, synth, dev):
+    import torch
+    table = _t(synth.pq2_table(synth.Rng(1), 300, 5120), dev)
+    ids = _t((synth.Rng(2).u64(1000) % np.uint64(300)).astype(np.uint32), dev)
+    w = _t(synth.Rng(3).normal(5120, 1.0, 0.1), dev)
+
+    def make_out():
+        return [torch.empty((1000, 5120), device=dev), torch.empty((1000, 5120), device=dev)]
+
+    def run(s, outs=None):
+        outs = outs or make_out()
+        e, n = bh.pq2_embed_gather(table, 5120, 300, ids, w=w, out=outs[0], out_norm=outs[1],
+                                   stream=s)
+        return [e, n]
+
+    _replay_check(make_out, run, dev)
+
+
+def test_graph_softmax_wide(bh, synth, dev):
+    import torch
+    x = _t(synth.Rng(4).normal(16 * 248320, 0.0, 3.0).reshape(16, 248320), dev)
+
+    def make_out():
+        return [torch.empty_like(x)]
+
+    def run(s, outs=None):
+        outs = outs or make_out()
+        return [bh.softmax_rows(x, 248320, 1.25, out=outs[0], stream=s)]
+
+    _replay_check(make_out, run, dev)
+
+
+def test_graph_qk_norm_rope(bh, synth, dev):
+    import torch
+    q = _t(synth.Rng(5).normal(64 * 24 * 256).reshape(64, 24, 256), dev)
+    k = _t(synth.Rng(6).normal(64 * 4 * 256).reshape(64, 4, 256), dev)
+    wq = _t(synth.Rng(7).normal(256, 1.0, 0.1), dev)
+    wk = _t(synth.Rng(8).normal(256, 1.0, 0.1), dev)
+    pos = _t(synth.positions(64), dev)
+
+    def make_out():
+        return [torch.empty_like(q), torch.empty_like(k)]
+
+    def run(s, outs=None):
+        outs = outs or make_out()
+        bh.qk_norm_rope(bh.make_qk_args(q, outs[0], k, outs[1], wq, wk, pos, 64, 24, 4), stream=s)
+        return outs
+
+    _replay_check(make_out, run, dev)
