@@ -66,6 +66,22 @@ def build_library(jobs: int | None = None) -> Path:
     return LIB
 
 
+CPP_TEST_SRC = REPO / "tests" / "cpp" / "test_kernels.cpp"
+CPP_TEST_BIN = REPO / "tests" / "cpp" / "test_kernels"
+
+
+def build_cpp_tests() -> Path:
+    """Host-only C++ program restating the reference's unit tests against the
+    C++ interface mirror (host/bonsai_kernels.hpp), linked to the library."""
+    cmd = [HIPCC, "-O2", "-std=c++17", str(CPP_TEST_SRC), "-o", str(CPP_TEST_BIN),
+           f"-L{LIB.parent}", "-lbonsai_hip", f"-Wl,-rpath,{LIB.parent}",
+           "-Wl,-rpath,$ORIGIN/../../ternary-bonsai-inference_amd/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"C++ mirror tests failed to build:\n{res.stderr}")
+    return CPP_TEST_BIN
+
+
 def build_oracle() -> Path:
     """Build oracle/liboracle.so (test infrastructure) with its Makefile."""
     res = subprocess.run(["make", "-B", "-C", str(ORACLE_DIR)], capture_output=True, text=True)
@@ -80,4 +96,5 @@ def clean() -> None:
 
 if __name__ == "__main__":
     print(build_library())
+    print(build_cpp_tests())
     print(build_oracle())

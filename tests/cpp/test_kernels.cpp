@@ -1,0 +1,194 @@
+// The reference's own kernel unit tests, restated against the C++ mirror of
+// its interface (ternary-bonsai-inference_amd/host/bonsai_kernels.hpp), so
+// every case runs on the GPU through the bonsai HIP library.  Each test
+// cites the Rust #[test] it restates; literal inputs and answers are the
+// reference's.  Run by tests/test_cpp_mirror_gpu.py; exit status 0 = all pass.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "../../ternary-bonsai-inference_amd/host/bonsai_kernels.hpp"
+
+using namespace bonsai;
+
+static int g_fail = 0;
+#define CHECK(cond)                                                        \
+  do {                                                                     \
+    if (!(cond)) {                                                         \
+      std::printf("  check failed at line %d: %s\n", __LINE__, #cond);     \
+      ++g_fail;                                                            \
+    }                                                                      \
+  } while (0)
+
+static void run(const char *name, const std::function<void()> &f) {
+  const int before = g_fail;
+  try {
+    f();
+  } catch (const std::exception &e) {
+    std::printf("  exception: %s\n", e.what());
+    ++g_fail;
+  }
+  std::printf("%s %s\n", g_fail == before ? "PASS" : "FAIL", name);
+}
+
+int main() {
+  // src/kernels.rs:761-772
+  run("rms_norm_matches_reference", [] {
+    std::vector<float> x{1.0f, 2.0f, 3.0f, 4.0f}, w{0.5f, 1.0f, 1.5f, 2.0f};
+    auto y = kernels::rms_norm(x, w, 1e-6f);
+    const float s = 1.0f / std::sqrt(7.5f + 1e-6f);
+    for (size_t i = 0; i < 4; ++i) CHECK(std::fabs(y[i] - x[i] * w[i] * s) < 1e-6f);
+  });
+
+  // src/kernels.rs:774-787
+  run("pq2_decode_known_row", [] {
+    std::vector<uint8_t> raw(34, 0);
+    raw[0] = 0x00;
+    raw[1] = 0x40;     // scale 2.0
+    raw[2] = 0b11;     // j=0 -> code 3 -> +4
+    raw[3] = 0b1001;   // j=4 -> code 1 -> 0; j=5 -> code 2 -> +2
+    auto v = kernels::decode_pq2_0_row(raw, 128);
+    CHECK(v[0] == 4.0f);
+    CHECK(v[1] == -2.0f);
+    CHECK(v[4] == 0.0f);
+    CHECK(v[5] == 2.0f);
+  });
+
+  // src/kernels.rs:789-812
+  run("rms_norm_rows_matches_single_row_math", [] {
+    std::vector<float> x{1.0f, 2.0f, 3.0f, 4.0f, 0.5f, -0.5f, 2.0f, -3.0f};
+    std::vector<float> w{0.5f, 1.0f, 1.5f, 2.0f};
+    const float eps = 1e-6f;
+    auto y = kernels::rms_norm_rows(x, w, 4, eps).unwrap();
+    for (int row = 0; row < 2; ++row) {
+      float ss = 0.0f;
+      for (int i = 0; i < 4; ++i) ss += x[row * 4 + i] * x[row * 4 + i];
+      const float scale = 1.0f / std::sqrt(ss / 4.0f + eps);
+      for (int i = 0; i < 4; ++i) CHECK(std::fabs(y[row * 4 + i] - x[row * 4 + i] * scale * w[i]) < 1e-6f);
+    }
+    CHECK(kernels::rms_norm_rows(x, w, 3, eps).is_err());  // non-divisible
+    std::vector<float> w2{0.5f, 1.0f};
+    CHECK(kernels::rms_norm_rows(x, w2, 4, eps).is_err());  // bad weight len
+    CHECK(kernels::rms_norm_rows(x, w2, 4, eps).error() == "rms_norm_rows: weight len 2 != row_len 4");
+  });
+
+  // src/kernels.rs:814-828
+  run("l2_norm_rows_produce_unit_rows", [] {
+    std::vector<float> x{3.0f, 4.0f, 0.0f, 0.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+    auto y = kernels::l2_norm_rows(x, 4, 1e-12f).unwrap();
+    CHECK(std::fabs(y[0] - 0.6f) < 1e-6f);
+    CHECK(std::fabs(y[1] - 0.8f) < 1e-6f);
+    float ss = 0.0f;
+    for (int i = 4; i < 8; ++i) ss += y[i] * y[i];
+    CHECK(std::fabs(ss - 1.0f) < 1e-6f);
+    auto z = kernels::l2_norm_rows(std::vector<float>(4, 0.0f), 4, 1e-6f).unwrap();
+    for (float v : z) CHECK(v == 0.0f);
+    CHECK(kernels::l2_norm_rows(x, 3, 1e-12f).is_err());
+  });
+
+  // src/kernels.rs:830-838
+  run("activations_hit_expected_points", [] {
+    CHECK(kernels::silu(0.0f) == 0.0f);
+    CHECK(std::fabs(kernels::silu(1000.0f) - 1000.0f) < 1e-3f);
+    CHECK(std::fabs(kernels::sigmoid(0.0f) - 0.5f) < 1e-7f);
+    CHECK(kernels::sigmoid(-1000.0f) == 0.0f);
+    CHECK(std::fabs(kernels::softplus(0.0f) - std::log(2.0f)) < 1e-7f);
+    CHECK(kernels::softplus(100.0f) == 100.0f);
+  });
+
+  // src/kernels.rs:840-853
+  run("softmax_rows_are_normalized_and_mask_safe", [] {
+    std::vector<float> x{1.0f, 2.0f, 3.0f, -INFINITY, 0.0f, 0.0f, 0.0f, 0.0f};
+    auto y = kernels::softmax_rows(x, 4).unwrap();
+    CHECK(std::fabs(y[0] + y[1] + y[2] + y[3] - 1.0f) < 1e-6f);
+    CHECK(y[3] == 0.0f);
+    CHECK(std::fabs(y[4] + y[5] + y[6] + y[7] - 1.0f) < 1e-6f);
+    for (int i = 4; i < 8; ++i) CHECK(std::fabs(y[i] - 0.25f) < 1e-6f);
+    CHECK(kernels::softmax_rows(x, 3).is_err());
+  });
+
+  // src/gguf.rs:950-963, through the decode: code 2 (value +1) times the scale
+  run("half_conversions", [] {
+    auto one = [](uint16_t h) {
+      std::vector<uint8_t> raw(34, 0xAA);  // every code 2: weight = +1 * scale
+      raw[0] = h & 0xff;
+      raw[1] = h >> 8;
+      return kernels::decode_pq2_0_row(raw, 128)[0];
+    };
+    CHECK(one(0x3C00) == 1.0f);
+    CHECK(one(0xC000) == -2.0f);
+    CHECK(one(0x0000) == 0.0f);
+    CHECK(one(0x3800) == 0.5f);
+    CHECK(one(0x0001) == 5.9604645e-8f);
+    CHECK(std::fabs(one(0x03FF) - 6.097555e-5f) < 1e-10f);
+    CHECK(std::isinf(one(0x7C00)) && one(0x7C00) > 0);
+    CHECK(std::isnan(one(0x7E00)));
+  });
+
+  // src/gguf.rs:986-1033
+  run("pq2_0_decode_matches_reference", [] {
+    std::vector<uint8_t> data(68, 0);
+    data[0] = 0x00;
+    data[1] = 0x38;   // block 0: scale 0.5, codes 0 -> -0.5
+    data[34] = 0x00;
+    data[35] = 0x40;  // block 1: scale 2.0
+    data[36] = 0b11;
+    data[37] = 0b1001;
+    auto v = kernels::decode_pq2_0_row(data, 256);
+    CHECK(v[0] == -0.5f);
+    CHECK(v[128] == 4.0f);
+    CHECK(v[129] == -2.0f);
+    CHECK(v[132] == 0.0f);
+    CHECK(v[133] == 2.0f);
+  });
+
+  // src/rope.rs:96-104 (neox_pos0_is_identity), for the IMROPE path
+  run("imrope_pos0_is_identity", [] {
+    std::vector<float> h{1.0f, 2.0f, 3.0f, 4.0f};
+    auto orig = h;
+    rope::rope_imrope(h, 0, 0, 0, 0, 4, {11, 11, 10, 0}, 10000.0f);
+    for (size_t i = 0; i < h.size(); ++i) CHECK(std::fabs(h[i] - orig[i]) < 1e-6f);
+  });
+
+  // src/rope.rs:106-114 (neox_preserves_pair_norm), for the IMROPE path
+  run("imrope_preserves_pair_norm", [] {
+    std::vector<float> h{0.7f, -0.3f, 1.1f, 0.2f};
+    const float n0 = h[0] * h[0] + h[2] * h[2], n1 = h[1] * h[1] + h[3] * h[3];
+    rope::rope_imrope(h, 3, 3, 3, 3, 4, {11, 11, 10, 0}, 10000.0f);
+    CHECK(std::fabs(h[0] * h[0] + h[2] * h[2] - n0) < 1e-5f);
+    CHECK(std::fabs(h[1] * h[1] + h[3] * h[3] - n1) < 1e-5f);
+  });
+
+  // src/bin/bonsai-batch.rs:64-115: batch_embed(N) == N x row_f32, by bits;
+  // and the row_f32 range error (src/weights.rs:337-341)
+  run("batch_embed_equals_row_f32", [] {
+    const size_t ne0 = 5120, n_rows = 6, rb = kernels::pq2_row_bytes(ne0);
+    std::vector<uint8_t> payload(rb * n_rows);
+    uint32_t s = 0x9e3779b9u;
+    for (auto &b : payload) {
+      s ^= s << 13;
+      s ^= s >> 17;
+      s ^= s << 5;
+      b = static_cast<uint8_t>(s);
+    }
+    for (size_t r = 0; r < n_rows * (ne0 / 128); ++r) {  // finite scales
+      payload[r * 34 + 1] &= 0x3b;
+    }
+    std::vector<uint32_t> toks{5, 0, 3, 3};
+    auto tile = prefill::batch_embed(payload, ne0, n_rows, toks).unwrap();
+    for (size_t k = 0; k < toks.size(); ++k) {
+      std::vector<uint8_t> raw(payload.begin() + toks[k] * rb, payload.begin() + (toks[k] + 1) * rb);
+      auto row = kernels::decode_pq2_0_row(raw, ne0);
+      CHECK(std::memcmp(row.data(), tile.data() + k * ne0, ne0 * 4) == 0);
+    }
+    auto bad = prefill::batch_embed(payload, ne0, n_rows, {1, 6});
+    CHECK(bad.is_err());
+    CHECK(bad.error() == "Weights: row_f32(token_embd.weight): row 6 out of range (n_rows 6)");
+  });
+
+  std::printf("%s: %d failed checks\n", g_fail ? "FAILED" : "OK", g_fail);
+  return g_fail ? 1 : 0;
+}
