@@ -19,7 +19,9 @@ def _t(a, dev):
 def _replay_check(make_out, run, dev, replays=4):
     import torch
     s = torch.cuda.Stream()
-    eager = [o.clone() for o in run(s)]
+    eager = run(s)
+    torch.cuda.synchronize()  # the work ran on `s`; clone only after it finished
+    eager = [o.clone() for o in eager]
     torch.cuda.synchronize()
     outs = make_out()
     g = torch.cuda.CUDAGraph()
