@@ -19,7 +19,8 @@
 //     one float4 per lane, several rows per 256-lane block;
 //   * longer rows are owned by one block of NT <= 1024 lanes with VPT =
 //     ceil(row_len/4/1024) float4 per lane (5120-float hidden rows: 640
-//     lanes x 2; 2048-float attention rows: 512 lanes x 1);
+//     lanes x 2; softmax takes at least 2 per lane: 2048-float attention rows
+//     on 256 lanes x 2);
 //   * the row stays in registers between the reduction and the write-back
 //     (no second HBM pass); reductions are cross-lane shuffles inside the
 //     wave plus an LDS combine across waves in wave order (deterministic);
@@ -54,18 +55,12 @@ struct RowGeom {
 };
 
 // Returns false when the register scheme does not apply (the caller then
-// uses the looped kernel).
-bool pick_geom(size_t row_len, RowGeom &g, bool wave_rows = false) {
+// uses the looped kernel).  min_vpt raises the float4 per lane of block rows
+// (softmax: 2, measured 143 us vs 158 us for one wave per row and 193 us for
+// one float4 per lane on [49152, 2048]).
+bool pick_geom(size_t row_len, RowGeom &g, int min_vpt = 1) {
   if (row_len == 0 || (row_len & 3u) != 0) return false;
   const size_t r4 = row_len / 4;
-  if (wave_rows && r4 > 64 && r4 <= 512) {
-    // one wave per row, no block barrier (used where two reductions and a
-    // transcendental per element make barriers costly)
-    g.G = 64;
-    g.VPT = static_cast<int>((r4 + 63) / 64);
-    g.NT = kBlock;
-    return true;
-  }
   if (r4 <= 64) {
     g.G = pow2ceil(r4);
     g.VPT = 1;
@@ -73,7 +68,8 @@ bool pick_geom(size_t row_len, RowGeom &g, bool wave_rows = false) {
     return true;
   }
   if (r4 > 8192) return false;
-  const int vpt = static_cast<int>((r4 + 1023) / 1024);
+  int vpt = static_cast<int>((r4 + 1023) / 1024);
+  if (vpt < min_vpt) vpt = min_vpt;
   const int lanes = static_cast<int>((r4 + vpt - 1) / vpt);
   g.G = 0;
   g.VPT = vpt;
@@ -92,18 +88,7 @@ int with_geom(const RowGeom &g, F &&f) {
       case 8: return f(IC<8>{}, IC<1>{});
       case 16: return f(IC<16>{}, IC<1>{});
       case 32: return f(IC<32>{}, IC<1>{});
-      case 64:
-        switch (g.VPT) {
-          case 1: return f(IC<64>{}, IC<1>{});
-          case 2: return f(IC<64>{}, IC<2>{});
-          case 3: return f(IC<64>{}, IC<3>{});
-          case 4: return f(IC<64>{}, IC<4>{});
-          case 5: return f(IC<64>{}, IC<5>{});
-          case 6: return f(IC<64>{}, IC<6>{});
-          case 7: return f(IC<64>{}, IC<7>{});
-          case 8: return f(IC<64>{}, IC<8>{});
-          default: return -999;
-        }
+      case 64: return f(IC<64>{}, IC<1>{});
       default: return -999;
     }
   }
@@ -733,9 +718,7 @@ extern "C" int bh_softmax_rows(const float *x, size_t x_len, size_t row_len, flo
   const size_t rows = x_len / row_len;
   hipStream_t st = as_stream(stream);
   RowGeom g;
-  // rows of up to 2048 floats: one wave per row (no block barriers around the
-  // two reductions; measured faster than a block per row for softmax)
-  const bool fits = pick_geom(row_len, g, true) && aligned16(x) && aligned16(out);
+  const bool fits = pick_geom(row_len, g, 2) && aligned16(x) && aligned16(out);
   const bool few_long_rows = rows < 1024 && row_len >= 16384;
   if (fits && !few_long_rows) {
     int st_code = with_geom(g, [&](auto GC, auto VC) -> int {
