@@ -5,14 +5,15 @@
 //                     the gate half (src/forward.rs:379)
 //   bh_rope_imrope    rope::rope_imrope (src/rope.rs:9-70) over a batch of heads
 //
-// Design.  A head row is held by G = head_dim/4 lanes, one float4 each, so
-// the RMSNorm sum is a G-lane shuffle reduction and the rotation partner of
-// dim j (j + n_dims/2) sits in lane gl + n_dims/8 of the same group: one
+// Design.  A head row is held by G = head_dim/8 lanes, two float4 each (the
+// first half-row slice and the second), so the RMSNorm sum is a G-lane
+// shuffle reduction and the rotation partner of dim j (j + n_dims/2, always
+// in the first slice) sits in lane gl + n_dims/8 of the same group: one
 // cross-lane read per component (a DPP row rotation for n_dims 64), no LDS
 // traffic for the data.  A block of 256 lanes holds 16 head rows of one
-// token (4 per lane group, their loads issued together); the token's
-// cos/sin table (n_dims/2 pairs) is built into LDS by the first n_dims/2
-// lanes while the rows' loads are in flight, and shared by all 16 rows.
+// token (2 per lane group, all loads issued together); the token's cos/sin
+// table (n_dims/2 pairs) is built into LDS by the first n_dims/2 lanes while
+// the rows' loads are in flight, and shared by all 16 rows.
 //
 // Angles.  The reference computes theta for pair j by multiplying the
 // position by theta_scale once per pair (src/rope.rs:54-57), so theta_j is a
@@ -85,13 +86,14 @@ __device__ __forceinline__ void fill_table(const RopeParams &a, const int32_t *p
 }
 
 // A block holds rows of ONE token: blockDim.x/G row slots, R rows per slot
-// (the loads of all R rows go out first), one float4 per lane per row.  A
-// token's rows (q heads, then k heads) are spread over blocks_per_tok
-// consecutive blocks.  The token's cos/sin table is built in LDS by the
-// first n_dims/2 lanes while the loads are in flight.  DPP8: the rotation
-// partner is 8 lanes away (n_dims 64), a DPP row rotation inside each
-// 16-lane row instead of an LDS-crossbar permute.
-template <int G, bool NORM, int R, bool DPP8>
+// (the loads of all R rows go out first), V float4 per lane per row (lane gl
+// holds float4 gl, gl+G, ...: G*V*4 = head_dim).  A token's rows (q heads,
+// then k heads) are spread over blocks_per_tok consecutive blocks.  The
+// token's cos/sin table is built in LDS by the first n_dims/2 lanes while the
+// loads are in flight.  Rotated dims all live in the first float4 slice
+// (n_dims <= 4G).  DPP8: the rotation partner is 8 lanes away (n_dims 64), a
+// DPP row rotation inside each 16-lane row instead of an LDS-crossbar permute.
+template <int G, int V, bool NORM, int R, bool DPP8>
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int blocks_per_tok) {
   const int slots = blockDim.x / G;
   __shared__ float cs_cos[kMaxHalf];
@@ -104,27 +106,44 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
   const int n_rows = a.n_q + a.n_k;
   const int half = a.n_dims >> 1;
 
-  float4 x[R], g[R];
+  float4 x[R][V], g[R][V];
 #pragma unroll
   for (int k = 0; k < R; ++k) {
     const int r = row0 + k * slots;
-    x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-    g[k] = x[k];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      x[k][v] = make_float4(0.f, 0.f, 0.f, 0.f);
+      g[k][v] = x[k][v];
+    }
     if (r < a.n_q) {
-      const float *src = a.q + (t * a.n_q + r) * a.q_stride;
-      x[k] = reinterpret_cast<const float4 *>(src)[gl];
-      if (a.gate_out != nullptr) g[k] = reinterpret_cast<const float4 *>(src + a.head_dim)[gl];
+      const float4 *src = reinterpret_cast<const float4 *>(a.q + (t * a.n_q + r) * a.q_stride);
+#pragma unroll
+      for (int v = 0; v < V; ++v) x[k][v] = src[gl + v * G];
+      if (a.gate_out != nullptr) {
+        const float4 *gs = reinterpret_cast<const float4 *>(a.q + (t * a.n_q + r) * a.q_stride + a.head_dim);
+#pragma unroll
+        for (int v = 0; v < V; ++v) g[k][v] = gs[gl + v * G];
+      }
     } else if (r < n_rows) {
-      x[k] = reinterpret_cast<const float4 *>(a.k + (t * a.n_k + (r - a.n_q)) * a.head_dim)[gl];
+      const float4 *src = reinterpret_cast<const float4 *>(a.k + (t * a.n_k + (r - a.n_q)) * a.head_dim);
+#pragma unroll
+      for (int v = 0; v < V; ++v) x[k][v] = src[gl + v * G];
     }
   }
-  float4 wq = make_float4(1.f, 1.f, 1.f, 1.f), wk = wq;
-  if (NORM) {
-    if (a.n_q > 0) wq = reinterpret_cast<const float4 *>(a.wq)[gl];
-    if (a.n_k > 0) wk = reinterpret_cast<const float4 *>(a.wk)[gl];
+  float4 wq[V], wk[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    wq[v] = make_float4(1.f, 1.f, 1.f, 1.f);
+    wk[v] = wq[v];
+    if (NORM) {
+      if (a.n_q > 0) wq[v] = reinterpret_cast<const float4 *>(a.wq)[gl + v * G];
+      if (a.n_k > 0) wk[v] = reinterpret_cast<const float4 *>(a.wk)[gl + v * G];
+    }
   }
 
-  // rotation partner: dim j <-> j + n_dims/2, i.e. lane gl <-> gl +- n_dims/8
+  fill_table(a, a.pos + 4 * t, half, cs_cos, cs_sin);
+
+  // rotation partner (first slice): dim j <-> j + n_dims/2, lane gl <-> gl +- n_dims/8
   const int d0 = 4 * gl;
   const bool rotates = d0 < a.n_dims;
   const bool role1 = d0 >= half;
@@ -132,9 +151,8 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
   const int src_lane = lane - gl + partner;
   const int j0 = role1 ? d0 - half : d0;
 
-  float4 cv = make_float4(1.f, 1.f, 1.f, 1.f), sv = make_float4(0.f, 0.f, 0.f, 0.f);
-  fill_table(a, a.pos + 4 * t, half, cs_cos, cs_sin);
   __syncthreads();  // table ready
+  float4 cv = make_float4(1.f, 1.f, 1.f, 1.f), sv = make_float4(0.f, 0.f, 0.f, 0.f);
   if (rotates) {
     cv = make_float4(cs_cos[j0], cs_cos[j0 + 1], cs_cos[j0 + 2], cs_cos[j0 + 3]);
     sv = make_float4(cs_sin[j0], cs_sin[j0 + 1], cs_sin[j0 + 2], cs_sin[j0 + 3]);
@@ -144,49 +162,66 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
   for (int k = 0; k < R; ++k) {
     const int r = row0 + k * slots;
     const bool is_q = r < a.n_q;
-    float4 v = x[k];
+    float4 vv[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) vv[v] = x[k][v];
     if constexpr (NORM) {
       // src/kernels.rs:112-120: (x * scale) * w, scale = 1/sqrt(sum(x^2)/n + eps)
-      float ss = v.x * v.x;
-      ss += v.y * v.y;
-      ss += v.z * v.z;
-      ss += v.w * v.w;
+      float ss = 0.0f;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        ss += vv[v].x * vv[v].x;
+        ss += vv[v].y * vv[v].y;
+        ss += vv[v].z * vv[v].z;
+        ss += vv[v].w * vv[v].w;
+      }
 #pragma unroll
       for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
       const float scale = 1.0f / sqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
-      const float4 w = is_q ? wq : wk;
-      v.x = (v.x * scale) * w.x;
-      v.y = (v.y * scale) * w.y;
-      v.z = (v.z * scale) * w.z;
-      v.w = (v.w * scale) * w.w;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float4 w = is_q ? wq[v] : wk[v];
+        vv[v].x = (vv[v].x * scale) * w.x;
+        vv[v].y = (vv[v].y * scale) * w.y;
+        vv[v].z = (vv[v].z * scale) * w.z;
+        vv[v].w = (vv[v].w * scale) * w.w;
+      }
     }
     float px, py, pz, pw;
+    const float4 &u = vv[0];
     if constexpr (DPP8) {
       // lane i <- lane i^8 inside each 16-lane row: DPP row_ror:8 (0x128)
-      px = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.x), 0x128, 0xf, 0xf, false));
-      py = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.y), 0x128, 0xf, 0xf, false));
-      pz = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.z), 0x128, 0xf, 0xf, false));
-      pw = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v.w), 0x128, 0xf, 0xf, false));
+      px = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.x), 0x128, 0xf, 0xf, false));
+      py = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.y), 0x128, 0xf, 0xf, false));
+      pz = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.z), 0x128, 0xf, 0xf, false));
+      pw = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.w), 0x128, 0xf, 0xf, false));
     } else {
-      px = __shfl(v.x, src_lane, 64);
-      py = __shfl(v.y, src_lane, 64);
-      pz = __shfl(v.z, src_lane, 64);
-      pw = __shfl(v.w, src_lane, 64);
+      px = __shfl(u.x, src_lane, 64);
+      py = __shfl(u.y, src_lane, 64);
+      pz = __shfl(u.z, src_lane, 64);
+      pw = __shfl(u.w, src_lane, 64);
     }
     if (rotates) {
-      v.x = rot(v.x, px, cv.x, sv.x, role1);
-      v.y = rot(v.y, py, cv.y, sv.y, role1);
-      v.z = rot(v.z, pz, cv.z, sv.z, role1);
-      v.w = rot(v.w, pw, cv.w, sv.w, role1);
+      vv[0].x = rot(u.x, px, cv.x, sv.x, role1);
+      vv[0].y = rot(u.y, py, cv.y, sv.y, role1);
+      vv[0].z = rot(u.z, pz, cv.z, sv.z, role1);
+      vv[0].w = rot(u.w, pw, cv.w, sv.w, role1);
     }
     if (is_q) {
-      reinterpret_cast<float4 *>(a.q_out + (t * a.n_q + r) * a.head_dim)[gl] = v;
+      float4 *dst = reinterpret_cast<float4 *>(a.q_out + (t * a.n_q + r) * a.head_dim);
+#pragma unroll
+      for (int v = 0; v < V; ++v) dst[gl + v * G] = vv[v];
       if (a.gate_out != nullptr) {
-        reinterpret_cast<float4 *>(a.gate_out + (t * a.n_q + r) * a.head_dim)[gl] =
-            make_float4(sigmoid(g[k].x), sigmoid(g[k].y), sigmoid(g[k].z), sigmoid(g[k].w));
+        float4 *gd = reinterpret_cast<float4 *>(a.gate_out + (t * a.n_q + r) * a.head_dim);
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+          gd[gl + v * G] = make_float4(sigmoid(g[k][v].x), sigmoid(g[k][v].y),
+                                       sigmoid(g[k][v].z), sigmoid(g[k][v].w));
       }
     } else if (r < n_rows) {
-      reinterpret_cast<float4 *>(a.k_out + (t * a.n_k + (r - a.n_q)) * a.head_dim)[gl] = v;
+      float4 *dst = reinterpret_cast<float4 *>(a.k_out + (t * a.n_k + (r - a.n_q)) * a.head_dim);
+#pragma unroll
+      for (int v = 0; v < V; ++v) dst[gl + v * G] = vv[v];
     }
   }
 }
@@ -234,42 +269,49 @@ __global__ __launch_bounds__(64) void qk_norm_rope_loop_kernel(RopeParams a) {
   }
 }
 
+// Launches the register kernel with V float4 per lane and R rows per lane
+// group; returns -999 when the shape does not fit that geometry.
+template <int V, int R, bool NORM>
+int launch_rope_v(const RopeParams &p, size_t n_tok, hipStream_t st) {
+  if (p.head_dim % (4 * V) != 0) return -999;
+  const int G = p.head_dim / 4 / V;
+  if (G < 8 || G > 64 || (G & (G - 1)) != 0 || p.n_dims > 4 * G) return -999;
+  const int n_rows = p.n_q + p.n_k;
+  const int rows_per_block = (kBlock / G) * R;
+  const int bpt = (n_rows + rows_per_block - 1) / rows_per_block;  // blocks per token
+  const size_t blocks = n_tok * static_cast<size_t>(bpt);
+  if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "rope: too many head rows");
+  const unsigned grid = static_cast<unsigned>(blocks);
+  if (p.n_dims == 64 && G >= 16) {  // partner 8 lanes away: DPP
+    switch (G) {
+      case 16: BH_LAUNCH((qk_norm_rope_kernel<16, V, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
+      case 32: BH_LAUNCH((qk_norm_rope_kernel<32, V, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
+      case 64: BH_LAUNCH((qk_norm_rope_kernel<64, V, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
+      default: return -999;
+    }
+  }
+  switch (G) {
+    case 8: BH_LAUNCH((qk_norm_rope_kernel<8, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+    case 16: BH_LAUNCH((qk_norm_rope_kernel<16, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+    case 32: BH_LAUNCH((qk_norm_rope_kernel<32, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+    case 64: BH_LAUNCH((qk_norm_rope_kernel<64, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+    default: return -999;
+  }
+}
+
 template <bool NORM>
 int launch_rope(const RopeParams &p, size_t n_tok, hipStream_t st) {
   const bool fast = (p.head_dim % 4 == 0) && (p.n_dims % 8 == 0) && (p.q_stride % 4 == 0) &&
-                    p.head_dim <= 256 && p.head_dim >= 32 &&
-                    ((p.head_dim / 4) & (p.head_dim / 4 - 1)) == 0 && aligned16(p.q) &&
+                    p.head_dim <= 512 && p.head_dim >= 32 && aligned16(p.q) &&
                     aligned16(p.q_out) && (p.gate_out == nullptr || aligned16(p.gate_out)) &&
                     (p.n_k == 0 || (aligned16(p.k) && aligned16(p.k_out))) &&
                     (!NORM || (aligned16(p.wq) && (p.n_k == 0 || aligned16(p.wk))));
   if (fast) {
-    // 4 waves per block, 4 rows per row slot (measured best on MI355X for
-    // the 24 + 4 heads of 256: 16 head rows per block, 1.75 blocks per token)
-    constexpr int kRowsPerSlot = 4;
-    const int G = p.head_dim / 4;
-    const int n_rows = p.n_q + p.n_k;
-    const int rows_per_block = (kBlock / G) * kRowsPerSlot;
-    const int bpt = (n_rows + rows_per_block - 1) / rows_per_block;  // blocks per token
-    const size_t blocks = n_tok * static_cast<size_t>(bpt);
-    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "rope: too many head rows");
-    const unsigned grid = static_cast<unsigned>(blocks);
-    const bool dpp8 = p.n_dims == 64 && G >= 16;
-    constexpr int R = kRowsPerSlot;
-    if (dpp8) {
-      switch (G) {
-        case 16: BH_LAUNCH((qk_norm_rope_kernel<16, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
-        case 32: BH_LAUNCH((qk_norm_rope_kernel<32, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
-        case 64: BH_LAUNCH((qk_norm_rope_kernel<64, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
-        default: break;
-      }
-    }
-    switch (G) {
-      case 8: BH_LAUNCH((qk_norm_rope_kernel<8, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
-      case 16: BH_LAUNCH((qk_norm_rope_kernel<16, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
-      case 32: BH_LAUNCH((qk_norm_rope_kernel<32, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
-      case 64: BH_LAUNCH((qk_norm_rope_kernel<64, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
-      default: break;
-    }
+    // 2 float4 per lane, 2 rows per lane group (measured on config 2: 25.2 us
+    // vs 26.5-28.6 us at one float4 and 4 rows); shapes whose rotated dims
+    // do not fit the first half-row slice take one float4 per lane
+    if (int e = launch_rope_v<2, 2, NORM>(p, n_tok, st); e != -999) return e;
+    if (int e = launch_rope_v<1, 4, NORM>(p, n_tok, st); e != -999) return e;
   }
   const size_t blocks = n_tok * static_cast<size_t>(p.n_q + p.n_k);
   if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "rope: too many head rows");
