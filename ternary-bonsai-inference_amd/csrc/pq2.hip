@@ -20,13 +20,13 @@
 // Fused RMSNorm, bit-exact.  The reference sums the 5120 squares of a row
 // one after another in f32 (src/kernels.rs:65-68); on quantised embedding
 // rows that sequence drifts ~1e-5 from any tree-ordered sum, so the fused
-// kernel reproduces the sequence itself.  A block owns kSeqRows rows: its
+// kernel reproduces the sequence itself.  A block owns kFusedRows rows: its
 // rows are staged in LDS, "producer" waves decode them chunk by chunk (128
 // columns), store the embedding rows and write the f32 squares to an LDS
 // ring laid out column-major, while one "chain" wave adds them in column
 // order, one row per lane -- the same additions in the same order as the
 // CPU, so the norm output is bit-identical too.  The chain (5120 dependent
-// adds, ~10 us) runs under the embedding stores; the norm rows are then
+// adds, ~21 us) runs under the embedding stores; the norm rows are then
 // decoded a second time from LDS and stored.
 //
 // Bit-exactness: the f16 scale is widened with integer arithmetic (exact for
@@ -43,7 +43,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kPq2Block = 34;
-constexpr size_t kMaxSeqSmem = 128 * 1024;  // LDS of a chain block (gfx950: 160 KB per CU)
+constexpr size_t kMaxSeqSmem = 128 * 1024;  // LDS cap of a fused block (gfx950: 160 KB per CU)
 
 // Decodes float4 number f (weights 4f..4f+3 of the row) from the staged row.
 __device__ __forceinline__ float4 decode4(const uint8_t *rowb, int f) {
@@ -60,22 +60,157 @@ __device__ __forceinline__ float4 decode4(const uint8_t *rowb, int f) {
 }
 
 // ---------------------------------------------------------------------------
-// Fused gather + RMSNorm with the reference's sequential f32 sum of squares.
-// Launch 1 = chain blocks (row scales) + embedding writer blocks; launch 2 =
-// norm writer blocks.  Requires the fast-path layout.
+// Fused gather + RMSNorm with the reference's sequential f32 sum of squares:
+// one launch, one block of kFusedThreads lanes per kFusedRows output rows.
 // ---------------------------------------------------------------------------
-constexpr int kSeqRows = 16;               // rows per chain block = chain lanes
-constexpr int kSeqThreads = 1024;          // wave 0: chain, waves 1..15: producers
+constexpr int kFusedRows = 16;             // rows per block = chain lanes
+constexpr int kFusedThreads = 1024;        // wave 0: chain, waves 1..15: producers
 constexpr int kChunkQ = 32;                // float4 columns per chunk (128 weights)
-constexpr int kRingStride = kSeqRows + 1;  // float4 slots per column (padded)
+constexpr int kRingStride = kFusedRows + 1;  // float4 slots per column (padded)
 
-// LDS of a chain block: staged packed rows, the per-(row, 128-block) table
-// of the four possible squared weights (row stride padded to an odd number
-// of float4 against bank conflicts) and the two-chunk ring.
-size_t seq_terms_stride(size_t row_bytes) { return (row_bytes / kPq2Block) | 1u; }
-size_t seq_smem_bytes(size_t row_bytes) {
-  return kSeqRows * row_bytes + kSeqRows * seq_terms_stride(row_bytes) * sizeof(float4) +
-         2 * kChunkQ * kRingStride * sizeof(float4);
+// LDS of a block: staged packed rows, the f32 scale of every (row, 128-block)
+// and the two-chunk ring of squared weights.
+size_t fused_smem_bytes(size_t row_bytes) {
+  const size_t n_scales = (kFusedRows * (row_bytes / kPq2Block) + 3) & ~static_cast<size_t>(3);
+  return kFusedRows * row_bytes + n_scales * sizeof(float) + 2 * kChunkQ * kRingStride * sizeof(float4);
+}
+
+struct GatherArgs {
+  const uint8_t *table;
+  const uint32_t *ids;
+  float *out;       // embedding rows
+  float *out_norm;  // norm rows
+  const float *w;
+  uint32_t *bad_id;
+  int row_bytes, ne0, n_ids;
+  uint32_t n_rows;
+  float eps;
+};
+
+// Phase 1 (column chunks of 128 weights, ring of squares):
+//   producer waves decode chunk c of all the block's rows, store those
+//   embedding float4 and write their f32 squares to the ring, column-major;
+//   the chain wave (lane = row) adds chunk c-1 in column order -- the same
+//   additions in the same order as src/kernels.rs:65-68, so the row scale
+//   is bit-identical to the CPU's.  The chain is latency-bound (~10 cycles
+//   per dependent add, ~21 us for 5120 weights) and runs under the stores.
+// Phase 2: all waves decode the rows again from LDS and store the norm rows
+//   (v * scale) * w (src/kernels.rs:71-73), flat over the block's rows.
+__global__ __launch_bounds__(kFusedThreads) void pq2_gather_rms_kernel(GatherArgs a) {
+  extern __shared__ uint4 smem[];
+  __shared__ int row_ok[kFusedRows];
+  __shared__ float row_scale[kFusedRows];
+  const int rb16 = a.row_bytes >> 4;
+  const int nblk = a.row_bytes / kPq2Block;
+  uint4 *stage = smem;                                                  // [rows][rb16]
+  float *scales = reinterpret_cast<float *>(smem + kFusedRows * rb16);  // [rows][nblk]
+  float4 *ring = reinterpret_cast<float4 *>(scales + ((kFusedRows * nblk + 3) & ~3));
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const size_t row0 = static_cast<size_t>(blockIdx.x) * kFusedRows;
+  const int nr = (a.n_ids - static_cast<int>(row0)) < kFusedRows ? a.n_ids - static_cast<int>(row0)
+                                                                 : kFusedRows;
+  const int n4 = a.ne0 >> 2;
+
+  if (tid < kFusedRows) {
+    int okr = 0;
+    if (tid < nr) {
+      const uint32_t id = a.ids[row0 + tid];
+      okr = id < a.n_rows;
+      if (!okr && a.bad_id != nullptr) *a.bad_id = id;
+    }
+    row_ok[tid] = okr;
+  }
+  for (int i = tid; i < nr * rb16; i += kFusedThreads) {
+    const int r = i / rb16;
+    const uint32_t id = a.ids[row0 + r];
+    if (id < a.n_rows)
+      stage[i] = reinterpret_cast<const uint4 *>(a.table + static_cast<size_t>(id) * a.row_bytes)[i - r * rb16];
+  }
+  __syncthreads();
+  // f32 scale of every staged 128-block (the f16 bits kept in the scale slot
+  // would be needed only for non-finite scales, which are re-read from the row)
+  for (int i = tid; i < nr * nblk; i += kFusedThreads) {
+    const int r = i / nblk;
+    const uint8_t *bp = reinterpret_cast<const uint8_t *>(stage + r * rb16) + (i - r * nblk) * kPq2Block;
+    const uint32_t h = static_cast<uint32_t>(bp[0]) | (static_cast<uint32_t>(bp[1]) << 8);
+    scales[i] = __uint_as_float(half_bits_to_f32_bits(h));
+  }
+  __syncthreads();
+
+  const int n_chunks = (n4 + kChunkQ - 1) / kChunkQ;
+  float ss = 0.0f;  // chain lane `lane` accumulates row `lane`
+  for (int c = 0; c <= n_chunks; ++c) {
+    if (wave != 0) {
+      if (c < n_chunks) {
+        float4 *dst = ring + (c & 1) * (kChunkQ * kRingStride);
+        for (int i = tid - 64; i < kFusedRows * kChunkQ; i += kFusedThreads - 64) {
+          const int r = i / kChunkQ;  // lanes walk a row's 32 columns: 512-byte store runs
+          const int q = i - r * kChunkQ;
+          const int f = c * kChunkQ + q;
+          float4 t = make_float4(0.f, 0.f, 0.f, 0.f);  // adding +0 leaves a sum unchanged
+          if (r < nr && f < n4) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row_ok[r]) {
+              const uint8_t *rowb = reinterpret_cast<const uint8_t *>(stage + r * rb16);
+              const int b = f >> 5;
+              const uint32_t h = static_cast<uint32_t>(rowb[b * kPq2Block]) |
+                                 (static_cast<uint32_t>(rowb[b * kPq2Block + 1]) << 8);
+              const uint32_t code = rowb[b * kPq2Block + 2 + (f & 31)];
+              const float sc = scales[r * nblk + b];
+              const bool finite = (h & 0x7c00u) != 0x7c00u;
+              v = make_float4(pq2_weight(code & 3u, sc, finite), pq2_weight((code >> 2) & 3u, sc, finite),
+                              pq2_weight((code >> 4) & 3u, sc, finite), pq2_weight((code >> 6) & 3u, sc, finite));
+              t = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+            }
+            reinterpret_cast<float4 *>(a.out)[(row0 + r) * n4 + f] = v;
+          }
+          dst[q * kRingStride + r] = t;
+        }
+      }
+    } else if (c > 0 && lane < kFusedRows) {
+      const float4 *src = ring + ((c - 1) & 1) * (kChunkQ * kRingStride);
+#pragma unroll 8
+      for (int q = 0; q < kChunkQ; ++q) {
+        const float4 t = src[q * kRingStride + lane];
+        ss += t.x;
+        ss += t.y;
+        ss += t.z;
+        ss += t.w;
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && lane < kFusedRows) {
+    // src/kernels.rs:69-70: mean = ss / n; scale = 1 / sqrt(mean + eps)
+    row_scale[lane] = 1.0f / sqrtf(ss / static_cast<float>(a.ne0) + a.eps);
+  }
+  __syncthreads();
+
+  const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
+  float4 *on = reinterpret_cast<float4 *>(a.out_norm) + row0 * n4;
+  const int total = nr * n4;
+  for (int i = tid; i < total; i += kFusedThreads) {
+    const int r = i / n4;
+    const int f = i - r * n4;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row_ok[r]) {
+      const uint8_t *rowb = reinterpret_cast<const uint8_t *>(stage + r * rb16);
+      const int b = f >> 5;
+      const uint32_t h = static_cast<uint32_t>(rowb[b * kPq2Block]) |
+                         (static_cast<uint32_t>(rowb[b * kPq2Block + 1]) << 8);
+      const uint32_t code = rowb[b * kPq2Block + 2 + (f & 31)];
+      const float sc = scales[r * nblk + b];
+      const bool finite = (h & 0x7c00u) != 0x7c00u;
+      const float4 v = make_float4(pq2_weight(code & 3u, sc, finite), pq2_weight((code >> 2) & 3u, sc, finite),
+                                   pq2_weight((code >> 4) & 3u, sc, finite), pq2_weight((code >> 6) & 3u, sc, finite));
+      const float4 wv = w4[f];
+      const float rs = row_scale[r];
+      o = make_float4((v.x * rs) * wv.x, (v.y * rs) * wv.y, (v.z * rs) * wv.z, (v.w * rs) * wv.w);
+    }
+    on[i] = o;
+  }
 }
 
 // Decodes float4 f of the packed row at `rowb` straight from global memory
@@ -92,150 +227,8 @@ __device__ __forceinline__ float4 decode4_global(const uint8_t *rowb, int f) {
                      pq2_weight((c >> 6) & 3u, scale, finite));
 }
 
-struct GatherArgs {
-  const uint8_t *table;
-  const uint32_t *ids;
-  float *out;        // embedding rows
-  float *out_norm;   // norm rows
-  const float *w;
-  float *row_scale;  // [n_ids] 1/sqrt(mean(x^2)+eps), written by launch 1
-  uint32_t *bad_id;
-  int row_bytes, ne0, n_ids;
-  uint32_t n_rows;
-  float eps;
-  int n_chain;       // chain blocks in launch 1
-};
-
-// Chain block: rows [row0, row0 + kSeqRows).  The packed rows are staged in
-// LDS together with, per (row, 128-weight block), the four values the
-// reference can add for that block: fl(v * v) for v = (code - 1) * scale,
-// code 0..3 (computed with the same operations, so non-finite scales give
-// the same NaN/inf terms).  Producer waves then turn chunk c (128 columns of
-// every row) into squares by table lookup and write them to an LDS ring laid
-// out column-major; the chain wave (lane = row, alone on its SIMD) adds
-// chunk c-1 in column order (the chain is latency-bound: ~10 cycles per
-// dependent add, ~21 us per 5120-weight row).  Same additions, same order as
-// src/kernels.rs:65-68, so the scale is bit-identical to the CPU's.
-__device__ void chain_block(const GatherArgs &a, int blk, uint4 *smem) {
-  __shared__ int row_ok[kSeqRows];
-  const int rb16 = a.row_bytes >> 4;
-  const int nblk = a.row_bytes / kPq2Block;
-  const int tstride = nblk | 1;
-  uint4 *stage = smem;                                                       // [kSeqRows][rb16]
-  float4 *terms = reinterpret_cast<float4 *>(smem + kSeqRows * rb16);        // [kSeqRows][tstride]
-  float4 *ring = terms + kSeqRows * tstride;                                 // [2][kChunkQ][kRingStride]
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int row0 = blk * kSeqRows;
-  const int nr = (a.n_ids - row0) < kSeqRows ? a.n_ids - row0 : kSeqRows;
-  const int n4 = a.ne0 >> 2;
-
-  if (tid < kSeqRows) row_ok[tid] = tid < nr && a.ids[row0 + tid] < a.n_rows;
-  for (int i = tid; i < nr * rb16; i += kSeqThreads) {
-    const int r = i / rb16;
-    const uint32_t id = a.ids[row0 + r];
-    if (id < a.n_rows)
-      stage[i] = reinterpret_cast<const uint4 *>(a.table + static_cast<size_t>(id) * a.row_bytes)[i - r * rb16];
-  }
-  __syncthreads();
-  for (int i = tid; i < nr * nblk; i += kSeqThreads) {
-    const int r = i / nblk;
-    const int b = i - r * nblk;
-    const uint8_t *bp = reinterpret_cast<const uint8_t *>(stage + r * rb16) + b * kPq2Block;
-    const uint32_t h = static_cast<uint32_t>(bp[0]) | (static_cast<uint32_t>(bp[1]) << 8);
-    const float scale = __uint_as_float(half_bits_to_f32_bits(h));
-    const bool finite = (h & 0x7c00u) != 0x7c00u;
-    float4 t;
-    float v = pq2_weight(0u, scale, finite);
-    t.x = v * v;
-    v = pq2_weight(1u, scale, finite);
-    t.y = v * v;
-    v = pq2_weight(2u, scale, finite);
-    t.z = v * v;
-    v = pq2_weight(3u, scale, finite);
-    t.w = v * v;
-    terms[r * tstride + b] = t;
-  }
-  __syncthreads();
-
-  // The chain is latency-bound and shares CUs with streaming writer blocks:
-  // raise this block's wave priority (wave-level, not the stream's) so writer
-  // waves do not stretch the 5120-add sequence.
-  __builtin_amdgcn_s_setprio(2);
-  const int n_chunks = (n4 + kChunkQ - 1) / kChunkQ;
-  float ss = 0.0f;  // chain lane `lane` accumulates row `lane`
-  for (int c = 0; c <= n_chunks; ++c) {
-    if (wave != 0) {
-      if (c < n_chunks) {
-        float4 *dst = ring + (c & 1) * (kChunkQ * kRingStride);
-        // lanes walk rows fastest: conflict-free ring writes
-        for (int i = tid - 64; i < kSeqRows * kChunkQ; i += kSeqThreads - 64) {
-          const int r = i % kSeqRows;
-          const int q = i / kSeqRows;
-          const int f = c * kChunkQ + q;
-          float4 t = make_float4(0.f, 0.f, 0.f, 0.f);  // adding +0 leaves a sum unchanged
-          if (r < nr && f < n4 && row_ok[r]) {
-            const int b = f >> 5;
-            const uint32_t code =
-                reinterpret_cast<const uint8_t *>(stage + r * rb16)[b * kPq2Block + 2 + (f & 31)];
-            const float *tb = reinterpret_cast<const float *>(terms + r * tstride + b);
-            t = make_float4(tb[code & 3u], tb[(code >> 2) & 3u], tb[(code >> 4) & 3u],
-                            tb[code >> 6]);
-          }
-          dst[q * kRingStride + r] = t;
-        }
-      }
-    } else if (c > 0 && lane < kSeqRows) {
-      const float4 *src = ring + ((c - 1) & 1) * (kChunkQ * kRingStride);
-#pragma unroll 8
-      for (int q = 0; q < kChunkQ; ++q) {
-        const float4 t = src[q * kRingStride + lane];
-        ss += t.x;
-        ss += t.y;
-        ss += t.z;
-        ss += t.w;
-      }
-    }
-    __syncthreads();
-  }
-  if (wave == 0 && lane < nr) {
-    // src/kernels.rs:69-70: mean = ss / n; scale = 1 / sqrt(mean + eps)
-    a.row_scale[row0 + lane] = 1.0f / sqrtf(ss / static_cast<float>(a.ne0) + a.eps);
-  }
-}
-
-// Launch 1: blocks [0, n_chain) are chain blocks (dispatched first, so they
-// start at once and their ~20 us add sequences run under the streaming
-// stores), the rest write the embedding rows, one float4 per lane over the
-// flat [n_ids][ne0/4] range.
-__global__ __launch_bounds__(kSeqThreads) void pq2_gather_rms_pass1_kernel(GatherArgs a) {
-  extern __shared__ uint4 smem[];
-  if (static_cast<int>(blockIdx.x) < a.n_chain) {
-    chain_block(a, blockIdx.x, smem);
-    return;
-  }
-  const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
-  const uint32_t idx = (blockIdx.x - a.n_chain) * static_cast<uint32_t>(kSeqThreads) + threadIdx.x;
-  if (idx >= static_cast<uint32_t>(a.n_ids) * n4) return;
-  const uint32_t t = idx / n4;
-  const uint32_t f = idx - t * n4;
-  const uint32_t id = a.ids[t];
-  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (id < a.n_rows) {
-    v = decode4_global(a.table + static_cast<size_t>(id) * a.row_bytes, f);
-  } else if (f == 0 && a.bad_id != nullptr) {
-    *a.bad_id = id;
-  }
-  reinterpret_cast<float4 *>(a.out)[idx] = v;
-}
-
-// Embedding rows (NORM false) or norm rows (NORM true: (v * scale) * w,
-// src/kernels.rs:71-73, with the row's scale), one float4 per lane over the
-// flat [n_ids][ne0/4] range (fits 32 bits: checked by the host).  One 16-byte
-// store per lane is the store shape that streams best here (measured: four
-// contiguous float4 per lane is 1.5x slower).
-template <bool NORM>
+// Plain gather: one float4 of output per lane over the flat [n_ids][ne0/4]
+// range (fits 32 bits: checked by the host).
 __global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
   const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
   const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
@@ -245,19 +238,11 @@ __global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
   const uint32_t id = a.ids[t];
   float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
   if (id < a.n_rows) {
-    const float4 v = decode4_global(a.table + static_cast<size_t>(id) * a.row_bytes, f);
-    if constexpr (NORM) {
-      const float4 wv = reinterpret_cast<const float4 *>(a.w)[f];
-      const float scale = a.row_scale[t];
-      o = make_float4((v.x * scale) * wv.x, (v.y * scale) * wv.y, (v.z * scale) * wv.z,
-                      (v.w * scale) * wv.w);
-    } else {
-      o = v;
-    }
-  } else if (!NORM && f == 0 && a.bad_id != nullptr) {
+    o = decode4_global(a.table + static_cast<size_t>(id) * a.row_bytes, f);
+  } else if (f == 0 && a.bad_id != nullptr) {
     *a.bad_id = id;
   }
-  reinterpret_cast<float4 *>(NORM ? a.out_norm : a.out)[idx] = o;
+  reinterpret_cast<float4 *>(a.out)[idx] = o;
 }
 
 // Any ne0 / alignment: byte reads straight from the table.
@@ -313,8 +298,8 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
   const size_t row_bytes = bh_pq2_row_bytes(ne0);
   const unsigned grid = static_cast<unsigned>(n_ids);
   const uint32_t nr = static_cast<uint32_t>(n_rows);
-  // row writers: ne0/16 lanes per row, 16-byte stores, halfword table loads;
-  // the chain blocks stage rows with 16-byte loads
+  // writers: one float4 per lane (16-byte stores, halfword table loads); the
+  // fused kernel stages rows with 16-byte loads
   const bool rows_ok = (ne0 % 4 == 0) && n_ids * (ne0 / 4) < 0xffffff00u && aligned16(table) &&
                        aligned16(out) && (!norm || (aligned16(out_norm) && aligned16(w)));
   const unsigned wgrid = static_cast<unsigned>((n_ids * (ne0 / 4) + 255) / 256);
@@ -331,33 +316,18 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
   ga.n_rows = nr;
   ga.eps = eps;
   if (rows_ok && !norm) {
-    BH_LAUNCH((pq2_rows_write_kernel<false>), wgrid, 256, 0, st, ga);
+    BH_LAUNCH(pq2_rows_write_kernel, wgrid, 256, 0, st, ga);
     return ok();
   }
-  if (rows_ok && norm && row_bytes % 16 == 0 && seq_smem_bytes(row_bytes) <= kMaxSeqSmem) {
-    ga.table = table;
-    ga.ids = ids;
-    ga.out = out;
-    ga.out_norm = out_norm;
-    ga.w = w;
-    ga.bad_id = bad_id;
-    ga.row_bytes = static_cast<int>(row_bytes);
-    ga.ne0 = static_cast<int>(ne0);
-    ga.n_ids = static_cast<int>(n_ids);
-    ga.n_rows = nr;
-    ga.eps = eps;
-    ga.n_chain = static_cast<int>((n_ids + kSeqRows - 1) / kSeqRows);
-    ga.row_scale = static_cast<float *>(device_scratch(n_ids * sizeof(float), kScratchGather));
-    if (ga.row_scale == nullptr) return BH_ERR_HIP;
-    const size_t smem = seq_smem_bytes(row_bytes);
-    if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_gather_rms_pass1_kernel),
+  if (rows_ok && norm && row_bytes % 16 == 0 && fused_smem_bytes(row_bytes) <= kMaxSeqSmem) {
+    const size_t smem = fused_smem_bytes(row_bytes);
+    if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_gather_rms_kernel),
                                               hipFuncAttributeMaxDynamicSharedMemorySize,
                                               static_cast<int>(smem)),
                           "hipFuncSetAttribute"))
       return e;
-    const size_t g1 = ga.n_chain + (n_ids * (ne0 / 4) + kSeqThreads - 1) / kSeqThreads;
-    BH_LAUNCH(pq2_gather_rms_pass1_kernel, static_cast<unsigned>(g1), kSeqThreads, smem, st, ga);
-    BH_LAUNCH((pq2_rows_write_kernel<true>), wgrid, 256, 0, st, ga);
+    const unsigned fgrid = static_cast<unsigned>((n_ids + kFusedRows - 1) / kFusedRows);
+    BH_LAUNCH(pq2_gather_rms_kernel, fgrid, kFusedThreads, smem, st, ga);
   } else {
     if (norm) {
       BH_LAUNCH((pq2_gather_loop_kernel<true>), grid, kBlock, 0, st, table, row_bytes,
