@@ -57,14 +57,14 @@ __global__ __launch_bounds__(kBlock) void unary_vec_kernel(const float *a, const
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const size_t i = base + u * kBlock;
-    va[u] = i < n4 ? a4[i] : make_float4(0, 0, 0, 0);
-    if constexpr (BIN) vb[u] = i < n4 ? b4[i] : make_float4(0, 0, 0, 0);
+    va[u] = i < n4 ? load_stream(a4 + i) : make_float4(0, 0, 0, 0);
+    if constexpr (BIN) vb[u] = i < n4 ? load_stream(b4 + i) : make_float4(0, 0, 0, 0);
     else vb[u] = va[u];
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const size_t i = base + u * kBlock;
-    if (i < n4) o4[i] = unary_op4<MODE>(va[u], vb[u]);
+    if (i < n4) store_stream(o4 + i, unary_op4<MODE>(va[u], vb[u]));
   }
   // scalar tail (n % 4 elements), done by the first lanes of block 0
   if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a, int
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int i = (part * kU + u) * kBlock + tid;
-      v[u] = i < n4 ? c4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[u] = i < n4 ? load_stream(c4 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (part == 0)
       for (int h = tid; h < a.n_v_head; h += kBlock) small_gates(a, t * a.n_v_head + h, h);
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a, int
         const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
         s = make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
       }
-      if (i < n4) reinterpret_cast<float4 *>(a.conv_out)[t * n4 + i] = s;
+      if (i < n4) store_stream(reinterpret_cast<float4 *>(a.conv_out) + t * n4 + i, s);
     }
   } else {
     // output gate row: y * act(z)
@@ -189,16 +189,16 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a, int
     for (int u = 0; u < kU; ++u) {
       const int i = ((part - bc) * kU + u) * kBlock + tid;
       if (i < n4) {
-        z[u] = reinterpret_cast<const float4 *>(a.z)[t * n4 + i];
-        y[u] = reinterpret_cast<const float4 *>(a.y)[t * n4 + i];
+        z[u] = load_stream(reinterpret_cast<const float4 *>(a.z) + t * n4 + i);
+        y[u] = load_stream(reinterpret_cast<const float4 *>(a.y) + t * n4 + i);
       }
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int i = ((part - bc) * kU + u) * kBlock + tid;
       if (i < n4) {
-        reinterpret_cast<float4 *>(a.gated_out)[t * n4 + i] =
-            a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(z[u], y[u]) : unary_op4<BH_SILU_MUL>(z[u], y[u]);
+        store_stream(reinterpret_cast<float4 *>(a.gated_out) + t * n4 + i,
+                   a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(z[u], y[u]) : unary_op4<BH_SILU_MUL>(z[u], y[u]));
       }
     }
   }

@@ -118,16 +118,16 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
     if (r < a.n_q) {
       const float4 *src = reinterpret_cast<const float4 *>(a.q + (t * a.n_q + r) * a.q_stride);
 #pragma unroll
-      for (int v = 0; v < V; ++v) x[k][v] = src[gl + v * G];
+      for (int v = 0; v < V; ++v) x[k][v] = load_stream(src + gl + v * G);
       if (a.gate_out != nullptr) {
         const float4 *gs = reinterpret_cast<const float4 *>(a.q + (t * a.n_q + r) * a.q_stride + a.head_dim);
 #pragma unroll
-        for (int v = 0; v < V; ++v) g[k][v] = gs[gl + v * G];
+        for (int v = 0; v < V; ++v) g[k][v] = load_stream(gs + gl + v * G);
       }
     } else if (r < n_rows) {
       const float4 *src = reinterpret_cast<const float4 *>(a.k + (t * a.n_k + (r - a.n_q)) * a.head_dim);
 #pragma unroll
-      for (int v = 0; v < V; ++v) x[k][v] = src[gl + v * G];
+      for (int v = 0; v < V; ++v) x[k][v] = load_stream(src + gl + v * G);
     }
   }
   float4 wq[V], wk[V];
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
     if (is_q) {
       float4 *dst = reinterpret_cast<float4 *>(a.q_out + (t * a.n_q + r) * a.head_dim);
 #pragma unroll
-      for (int v = 0; v < V; ++v) dst[gl + v * G] = vv[v];
+      for (int v = 0; v < V; ++v) store_stream(dst + gl + v * G, vv[v]);
       if (a.gate_out != nullptr) {
         float4 *gd = reinterpret_cast<float4 *>(a.gate_out + (t * a.n_q + r) * a.head_dim);
 #pragma unroll
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
     } else if (r < n_rows) {
       float4 *dst = reinterpret_cast<float4 *>(a.k_out + (t * a.n_k + (r - a.n_q)) * a.head_dim);
 #pragma unroll
-      for (int v = 0; v < V; ++v) dst[gl + v * G] = vv[v];
+      for (int v = 0; v < V; ++v) store_stream(dst + gl + v * G, vv[v]);
     }
   }
 }

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(1024) void rms_rows_kernel(
         v[i].y += a.y;
         v[i].z += a.z;
         v[i].w += a.w;
-        s4[c] = v[i];
+        store_stream(s4 + c, v[i]);
       }
     }
   }
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(1024) void rms_rows_kernel(
       o.y = (v[i].y * scale) * wv.y;
       o.z = (v[i].z * scale) * wv.z;
       o.w = (v[i].w * scale) * wv.w;
-      o4[c] = o;
+      store_stream(o4 + c, o);
     }
   }
 }
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(1024) void l2_rows_kernel(const float *x, float *ou
   for (int i = 0; i < VPT; ++i) {
     const int c = L.gl + i * L.stride;
     if (L.live && c < r4) {
-      o4[c] = make_float4(v[i].x * scale, v[i].y * scale, v[i].z * scale, v[i].w * scale);
+      store_stream(o4 + c, make_float4(v[i].x * scale, v[i].y * scale, v[i].z * scale, v[i].w * scale));
     }
   }
 }
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(const float *x, floa
   for (int i = 0; i < VPT; ++i) {
     const int c = L.gl + i * L.stride;
     if (L.live && c < r4) {
-      o4[c] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+      store_stream(o4 + c, make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv));
     }
   }
 }
@@ -510,9 +510,9 @@ __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float
   const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
   if (c >= r4) return;
   const float2 st = row_stat[r];
-  const float4 v = x[r * r4 + c];
-  out[r * r4 + c] = make_float4(expf(v.x * inv_t - st.x) * st.y, expf(v.y * inv_t - st.x) * st.y,
-                                expf(v.z * inv_t - st.x) * st.y, expf(v.w * inv_t - st.x) * st.y);
+  const float4 v = load_stream(x + r * r4 + c);
+  store_stream(out + r * r4 + c, make_float4(expf(v.x * inv_t - st.x) * st.y, expf(v.y * inv_t - st.x) * st.y,
+                                expf(v.z * inv_t - st.x) * st.y, expf(v.w * inv_t - st.x) * st.y));
 }
 
 // Looped fallback for rows whose length is not a multiple of 4 or whose
