@@ -413,17 +413,16 @@ __device__ __forceinline__ MaxSum ms_merge(MaxSum a, MaxSum b) {
 
 // Split-row pass 1: block (c, r) reduces chunk c of row r (kSplitVPT float4
 // per lane, loaded up front) to (max, sum of expf(y - max)).  The chunk max
-// comes first, so each element costs one expf.  A one-wave-per-row kernel
-// then folds each row's chunk states into (M, 1/(f32)S) for pass 2 (kernel
-// boundaries order the three launches; no block waits for another).
+// comes first, so each element costs one expf.  Pass 2 folds each row's
+// chunk states (the kernel boundary orders the two launches; no block waits
+// for another).
 constexpr int kSplitVPT = 4;
-constexpr size_t kMaxSplitRows = 65535;  // grid.y limit of passes 1 and 3
+constexpr size_t kMaxSplitRows = 65535;  // grid.y limit of both passes
 constexpr size_t kSplitChunk4 = static_cast<size_t>(kBlock) * kSplitVPT;  // float4 per chunk
 
 struct SplitScratch {
-  double *part_s;     // [rows][nch]
-  float *part_m;      // [rows][nch]
-  float2 *row_stat;   // [rows] (M, 1/S)
+  double *part_s;  // [rows][nch]
+  float *part_m;   // [rows][nch]
 };
 
 __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float4 *x, size_t r4,
@@ -483,36 +482,49 @@ __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float
   }
 }
 
-// Fold of a row's chunk states (one wave per row): lane i takes chunks i,
-// i+64, ...; the cross-lane tree is fixed, so results are deterministic.
-__global__ __launch_bounds__(64) void softmax_split_fold_kernel(SplitScratch sc, int nch) {
-  const size_t r = blockIdx.x;
-  const MaxOp mx;
-  const float *pm = sc.part_m + r * nch;
-  const double *ps = sc.part_s + r * nch;
-  float M = -INFINITY;
-  for (int i = threadIdx.x; i < nch; i += 64) M = mx(M, pm[i]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) M = mx(M, __shfl_xor(M, off, 64));
-  double S = 0.0;
-  for (int i = threadIdx.x; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off, 64);
-  if (threadIdx.x == 0) sc.row_stat[r] = make_float2(M, 1.0f / static_cast<float>(S));
-}
-
-// Split-row pass 2: one float4 per lane, expf(y - M) * (1 / (f32)S), the
-// reference's output formula, with the row's (M, 1/S) from pass 1.
+// Split-row pass 2: the block's first wave folds the row's chunk states into
+// (M, 1/(f32)S) while the block's x loads are in flight -- every block of a
+// row folds the same states in the same fixed order (lane i takes chunks i,
+// i+64, ..., then a fixed shuffle tree), so all of them agree bit for bit --
+// then each lane writes expf(y - M) * (1 / (f32)S), the reference's output
+// formula, for its kSplitWV float4.
+constexpr int kSplitWV = 4;  // measured: 17.6 us vs 20.2 (2) and 21.3 (8) on [64, 248320]
 __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float4 *x, float4 *out,
                                                                      size_t r4, float inv_t,
-                                                                     const float2 *row_stat) {
+                                                                     SplitScratch sc, int nch) {
+  __shared__ float2 stat;
   const size_t r = blockIdx.y;
-  const size_t c = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (c >= r4) return;
-  const float2 st = row_stat[r];
-  const float4 v = load_stream(x + r * r4 + c);
-  store_stream(out + r * r4 + c, make_float4(expf(v.x * inv_t - st.x) * st.y, expf(v.y * inv_t - st.x) * st.y,
-                                expf(v.z * inv_t - st.x) * st.y, expf(v.w * inv_t - st.x) * st.y));
+  const size_t c0 = static_cast<size_t>(blockIdx.x) * (kBlock * kSplitWV) + threadIdx.x;
+  float4 v[kSplitWV];
+#pragma unroll
+  for (int i = 0; i < kSplitWV; ++i) {
+    const size_t c = c0 + static_cast<size_t>(i) * kBlock;
+    if (c < r4) v[i] = load_stream(x + r * r4 + c);
+  }
+  if (threadIdx.x < 64) {
+    const MaxOp mx;
+    const float *pm = sc.part_m + r * nch;
+    const double *ps = sc.part_s + r * nch;
+    float M = -INFINITY;
+    for (int i = threadIdx.x; i < nch; i += 64) M = mx(M, pm[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = mx(M, __shfl_xor(M, off, 64));
+    double S = 0.0;
+    for (int i = threadIdx.x; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off, 64);
+    if (threadIdx.x == 0) stat = make_float2(M, 1.0f / static_cast<float>(S));
+  }
+  __syncthreads();
+  const float2 st = stat;
+#pragma unroll
+  for (int i = 0; i < kSplitWV; ++i) {
+    const size_t c = c0 + static_cast<size_t>(i) * kBlock;
+    if (c < r4)
+      store_stream(out + r * r4 + c,
+                   make_float4(expf(v[i].x * inv_t - st.x) * st.y, expf(v[i].y * inv_t - st.x) * st.y,
+                               expf(v[i].z * inv_t - st.x) * st.y, expf(v[i].w * inv_t - st.x) * st.y));
+  }
 }
 
 // Looped fallback for rows whose length is not a multiple of 4 or whose
@@ -624,25 +636,21 @@ int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float
   const size_t nch = (r4 + kSplitChunk4 - 1) / kSplitChunk4;
   if (nch > 65535) return fail(BH_ERR_SHAPE, "softmax_rows: row too long");
   const size_t nparts = rows * nch;
-  // scratch: per-row (M, 1/S), f64 partial sums, f32 partial maxima
-  const size_t off_s = (rows * sizeof(float2) + 15) / 16 * 16;
-  const size_t off_m = off_s + nparts * sizeof(double);
+  // scratch: f64 partial sums, then f32 partial maxima
+  const size_t off_m = nparts * sizeof(double);
   char *scratch = static_cast<char *>(device_scratch(off_m + nparts * sizeof(float), kScratchSoftmax));
   if (scratch == nullptr) return BH_ERR_HIP;
   SplitScratch sc;
-  sc.row_stat = reinterpret_cast<float2 *>(scratch);
-  sc.part_s = reinterpret_cast<double *>(scratch + off_s);
+  sc.part_s = reinterpret_cast<double *>(scratch);
   sc.part_m = reinterpret_cast<float *>(scratch + off_m);
   const float4 *x4 = reinterpret_cast<const float4 *>(x);
   BH_LAUNCH(softmax_split_stats_kernel, dim3(static_cast<unsigned>(nch), static_cast<unsigned>(rows)),
             kBlock, 0, st, x4, r4, inv_t, sc);
-  BH_LAUNCH(softmax_split_fold_kernel, static_cast<unsigned>(rows), 64, 0, st, sc,
-            static_cast<int>(nch));
-  const size_t wblocks = (r4 + kBlock - 1) / kBlock;
+  const size_t wblocks = (r4 + kBlock * kSplitWV - 1) / (kBlock * kSplitWV);
   if (wblocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "softmax_rows: row too long");
   BH_LAUNCH(softmax_split_write_kernel,
             dim3(static_cast<unsigned>(wblocks), static_cast<unsigned>(rows)), kBlock, 0, st, x4,
-            reinterpret_cast<float4 *>(out), r4, inv_t, sc.row_stat);
+            reinterpret_cast<float4 *>(out), r4, inv_t, sc, static_cast<int>(nch));
   return ok();
 }
 

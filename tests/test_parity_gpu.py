@@ -268,7 +268,8 @@ def test_softmax_attention_causal(bh, oracle, synth, dev):
 
 
 @pytest.mark.parametrize("rows,row_len", [(2, 4), (1000, 7), (3, 40000), (5000, 96),
-                                          (7, 16384), (2, 1)])
+                                          (7, 16384), (2, 1), (2, 1000000), (3, 300004),
+                                          (1, 4194304)])
 def test_softmax_shapes(bh, oracle, synth, dev, rows, row_len):
     x = synth.Rng(rows * row_len).normal(rows * row_len, 0.0, 2.0)
     ref = oracle.softmax_rows(x, row_len)
@@ -306,10 +307,10 @@ def test_softmax_nan_and_inf_entries(bh, oracle, synth, dev):
 
 
 def test_softmax_split_repeated_mixed_shapes(bh, oracle, synth, dev):
-    """The wide-row path keeps per-row arrival counters in the library's
-    scratch and re-arms them itself: repeated calls with changing shapes
-    (including ones whose partials overlap earlier counters' neighbours)
-    must all give the oracle's result."""
+    """The wide-row path keeps per-chunk partial states in the library's
+    scratch, reused by every call: repeated calls with changing shapes (whose
+    partials overlap earlier calls' stale ones) must all give the oracle's
+    result."""
     cases = [(64, 248320), (3, 40000), (200, 20480), (3, 40000), (64, 248320), (1, 16384)]
     for i, (rows, row_len) in enumerate(cases):
         x = synth.Rng(500 + i).normal(rows * row_len, 0.0, 3.0)
