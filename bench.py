@@ -234,7 +234,12 @@ def measure(name, wl, steps, warmup, stream, extra=None):
 
 def cpu_baseline(bh, synth, oracle, seconds: float):
     """Time oracle.qk_norm_rope (src/forward.rs:237-270 restated) on the same
-    config, repeating the 2048-token batch until `seconds` have passed."""
+    config, repeating the 2048-token batch until `seconds` have passed: once on
+    one thread (the reference's decode thread), then row-parallel over the
+    host's cores for a quarter of that time (an upper bound for a threaded
+    CPU path; the C call releases the GIL, tokens are split into contiguous
+    slices, one per thread)."""
+    import concurrent.futures
     import numpy as np
     n_tok, nq, nk, hd = 2048, 24, 4, 256
     r = synth.Rng(1)
@@ -243,18 +248,41 @@ def cpu_baseline(bh, synth, oracle, seconds: float):
     wq, wk = r.normal(hd, 1.0, 0.1), r.normal(hd, 1.0, 0.1)
     pos = synth.positions(n_tok)
     nbytes = (q.nbytes + k.nbytes) * 2 + 2 * hd * 4
+
+    def run(lo, hi):
+        oracle.qk_norm_rope(q[lo:hi], k[lo:hi], wq, wk, pos[lo:hi], nq, nk, hd, 64, bh.SECTIONS,
+                            1e7, 1e-6)
+
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.qk_norm_rope(q, k, wq, wk, pos, nq, nk, hd, 64, bh.SECTIONS, 1e7, 1e-6)
+        run(0, n_tok)
         reps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
+    try:
+        n_thr = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n_thr = os.cpu_count() or 1
+    n_thr = max(1, min(n_thr, 16))  # the GPU box's CPU share is 16 cores
+    cuts = [n_tok * i // n_thr for i in range(n_thr + 1)]
+    reps_mt, t1 = 0, time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(n_thr) as pool:
+        while True:
+            list(pool.map(run, cuts[:-1], cuts[1:]))
+            reps_mt += 1
+            el_mt = time.perf_counter() - t1
+            if el_mt >= seconds / 4:
+                break
     return {"value": round(nbytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
             "kind": "port",
             "sample": f"oracle qk_norm_rope on the full config-2 batch (2048 tokens x 28 heads),"
                       f" {reps} repetitions in {el:.1f} s, 1 thread",
-            "rows_per_s": round(n_tok * reps / el, 1)}
+            "rows_per_s": round(n_tok * reps / el, 1),
+            "upper_bound_mt": {"value": round(nbytes * reps_mt / el_mt / 1e9, 4), "unit": "GB/s",
+                               "cores": n_thr,
+                               "sample": f"same batch split over {n_thr} threads by token, "
+                                         f"{reps_mt} repetitions in {el_mt:.1f} s"}}
 
 
 def load_traffic():

@@ -48,8 +48,7 @@ inline int pow2ceil(size_t v) {
 // of the same client on one device must not overlap in time.  Returns
 // nullptr on allocation failure (the status is already recorded).
 constexpr int kScratchSoftmax = 0;  // split-row softmax partials
-constexpr int kScratchGather = 1;   // fused gather + RMSNorm row scales
-constexpr int kScratchSlots = 2;
+constexpr int kScratchSlots = 1;
 void *device_scratch(size_t bytes, int slot);
 
 
