@@ -225,6 +225,32 @@ int bh_pq2_embed_gather_rms(const uint8_t *table, size_t ne0, size_t n_rows,
                             float *out_norm, uint32_t *bad_id, bh_stream stream);
 
 /* ---------------------------------------------------------------------------
+ * PQ2_0 products (matrix cores).  payload is the tensor's whole PQ2_0 data on
+ * the device (payload_len bytes, rows of bh_pq2_row_bytes(ne0) back to back);
+ * the product reads rows base_row .. base_row + n_rows - 1.  Results agree
+ * with the reference's scalar row dot to <= 1e-5 of the output's largest
+ * magnitude (the summation order differs, as the reference's AVX2 path's
+ * does).  Uses the library's per-device scratch (x fragments): calls must
+ * not overlap on one device.
+ * ------------------------------------------------------------------------- */
+
+/* kernels::pq2_matvec_range (src/kernels.rs:283-333):
+ * y[r] = sum_j x[j] * W[base_row + r][j] for r < n_rows.  Errors (text of the
+ * reference): x_len != ne0, y_len < n_rows, byte length overflow, rows past
+ * payload_len. */
+int bh_pq2_matvec_range(const uint8_t *payload, size_t payload_len, size_t ne0,
+                        uint64_t base_row, size_t n_rows, const float *x,
+                        size_t x_len, float *y, size_t y_len, bh_stream stream);
+
+/* kernels::pq2_matmul_n (src/kernels.rs:340-423): x is [n_tok][ne0], y is
+ * [n_tok][n_rows] (token-major), Y[t][r] = sum_j X[t][j] * W[base_row + r][j].
+ * Each weight row is read once for all tokens.  Errors as the reference. */
+int bh_pq2_matmul_n(const uint8_t *payload, size_t payload_len, size_t ne0,
+                    uint64_t base_row, size_t n_rows, const float *x,
+                    size_t x_len, size_t n_tok, float *y, size_t y_len,
+                    bh_stream stream);
+
+/* ---------------------------------------------------------------------------
  * Host-slice mirrors: the Rust signatures, host memory in and out.  Outputs
  * are caller-allocated with the length the Rust function would return.
  * ------------------------------------------------------------------------- */
@@ -257,6 +283,18 @@ int bh_host_decode_pq2_0_row(const uint8_t *raw, size_t raw_len, size_t ne0,
 int bh_host_batch_embed(const uint8_t *payload, size_t payload_len, size_t ne0,
                         size_t n_rows, const uint32_t *tokens, size_t n_tok,
                         float *out);
+/* kernels::dot_pq2_0_row (src/kernels.rs:233-262): *out = row `row` . x. */
+int bh_host_dot_pq2_0_row(const uint8_t *payload, size_t payload_len, size_t ne0,
+                          uint64_t row, const float *x, size_t x_len, float *out);
+/* kernels::pq2_matvec_range (src/kernels.rs:283-333), host slices; y has
+ * y_len entries of which the first n_rows are written. */
+int bh_host_pq2_matvec_range(const uint8_t *payload, size_t payload_len, size_t ne0,
+                             uint64_t base_row, size_t n_rows, const float *x,
+                             size_t x_len, float *y, size_t y_len);
+/* kernels::pq2_matmul_n (src/kernels.rs:340-423), host slices. */
+int bh_host_pq2_matmul_n(const uint8_t *payload, size_t payload_len, size_t ne0,
+                         uint64_t base_row, size_t n_rows, const float *x,
+                         size_t x_len, size_t n_tok, float *y, size_t y_len);
 
 #ifdef __cplusplus
 }

@@ -309,6 +309,39 @@ int or_embed_gather(const uint8_t *payload, size_t ne0, size_t n_rows, const uin
   return OR_OK;
 }
 
+/* ---- PQ2_0 products (src/kernels.rs:233-423) ------------------------------ */
+
+/* row_dot_scalar, src/kernels.rs:633-653: per 128-block an f32 sum of
+ * x[j] * (code - 1) in column order, then acc += scale * block_acc. */
+float or_pq2_row_dot(const uint8_t *raw, size_t ne0, const float *x) {
+  size_t n_blocks = (ne0 + 127) / 128;
+  float acc = 0.0f;
+  for (size_t block = 0; block < n_blocks; ++block) {
+    size_t b = block * 34;
+    float scale = or_half_to_f32((uint16_t)(raw[b] | (raw[b + 1] << 8)));
+    const uint8_t *qs = raw + b + 2;
+    size_t start = block * 128, end = start + 128 < ne0 ? start + 128 : ne0;
+    float block_acc = 0.0f;
+    for (size_t j = start; j < end; ++j) {
+      uint8_t code = (uint8_t)((qs[(j - start) / 4] >> (((j - start) % 4) * 2)) & 0x03);
+      block_acc += x[j] * (float)((int32_t)code - 1);
+    }
+    acc += scale * block_acc;
+  }
+  return acc;
+}
+
+/* pq2_matmul_n, src/kernels.rs:340-423 (and pq2_matvec_range when n_tok is
+ * 1): y[t][r] = row_dot(W[base_row + r], x[t]); y is [n_tok][n_rows].  The
+ * caller has checked the payload length. */
+void or_pq2_matmul_n(const uint8_t *payload, size_t ne0, uint64_t base_row, size_t n_rows,
+                     const float *x, size_t n_tok, float *y) {
+  size_t rb = or_pq2_row_bytes(ne0);
+  for (size_t r = 0; r < n_rows; ++r)
+    for (size_t t = 0; t < n_tok; ++t)
+      y[t * n_rows + r] = or_pq2_row_dot(payload + ((size_t)base_row + r) * rb, ne0, x + t * ne0);
+}
+
 /* ---- GDN gate prep (src/forward.rs:497-507, 524, 539-540) ---------------- */
 
 void or_gdn_gate_prep(const float *alpha_raw, const float *dt_bias, const float *ssm_a,

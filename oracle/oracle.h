@@ -84,6 +84,12 @@ void or_gdn_gate_prep(const float *alpha_raw, const float *dt_bias, const float 
 int or_silu_l2_part(const float *conv, size_t n_tok, size_t conv_dim, size_t l2_dim,
                     size_t head_dim, float eps, float *conv_out);
 
+/* src/kernels.rs:633-653 (row_dot_scalar) */
+float or_pq2_row_dot(const uint8_t *raw, size_t ne0, const float *x);
+/* src/kernels.rs:340-423 / :283-333: y [n_tok][n_rows] */
+void or_pq2_matmul_n(const uint8_t *payload, size_t ne0, uint64_t base_row, size_t n_rows,
+                     const float *x, size_t n_tok, float *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -44,6 +44,8 @@ _SIG = {
     "or_embed_gather": (ctypes.c_int, [_vp, _sz, _sz, _vp, _sz, _vp, _f, _vp, _vp, _vp]),
     "or_gdn_gate_prep": (None, [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp]),
     "or_silu_l2_part": (ctypes.c_int, [_vp, _sz, _sz, _sz, _sz, _f, _vp]),
+    "or_pq2_row_dot": (_f, [_vp, _sz, _vp]),
+    "or_pq2_matmul_n": (None, [_vp, _sz, ctypes.c_uint64, _sz, _vp, _sz, _vp]),
 }
 
 _LIB = None
@@ -207,6 +209,29 @@ def embed_gather(table, ne0: int, n_rows: int, tokens, w=None, eps: float = 1e-6
                               _p(out), _p(out_norm), _p(bad)),
         f"row {int(bad[0])} out of range (n_rows {n_rows})")
     return (out, out_norm) if w is not None else out
+
+
+def pq2_row_dot(raw, ne0: int, x) -> float:
+    """row_dot_scalar (src/kernels.rs:633-653) of one packed row with x."""
+    raw, x = _c(raw, np.uint8), _c(x)
+    if raw.size < pq2_row_bytes(ne0) or x.size != ne0:
+        raise OracleShapeError("pq2_row_dot shape")
+    return float(lib().or_pq2_row_dot(_p(raw), ne0, _p(x)))
+
+
+def pq2_matmul_n(payload, ne0: int, n_rows: int, x, base_row: int = 0) -> np.ndarray:
+    """pq2_matmul_n (src/kernels.rs:340-423): x [n_tok][ne0] -> y [n_tok][n_rows];
+    a 1-D x gives pq2_matvec_range's y [n_rows]."""
+    payload = _c(payload, np.uint8)
+    x = _c(x)
+    one = x.ndim == 1
+    x2 = x.reshape(1, -1) if one else x
+    n_tok = x2.shape[0]
+    if x2.shape[1] != ne0 or payload.size < (base_row + n_rows) * pq2_row_bytes(ne0):
+        raise OracleShapeError("pq2_matmul_n shape")
+    y = np.empty((n_tok, n_rows), np.float32)
+    lib().or_pq2_matmul_n(_p(payload), ne0, base_row, n_rows, _p(x2), n_tok, _p(y))
+    return y[0] if one else y
 
 
 def gdn_gate_prep(alpha_raw, dt_bias, ssm_a, beta_raw):

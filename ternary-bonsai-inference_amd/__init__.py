@@ -117,6 +117,16 @@ _SIGNATURES = {
                                      ctypes.POINTER(ctypes.c_int32), _c_float]),
     "bh_host_decode_pq2_0_row": (_c_int, [_vp, _c_size, _c_size, _vp]),
     "bh_host_batch_embed": (_c_int, [_vp, _c_size, _c_size, _c_size, _vp, _c_size, _vp]),
+    "bh_pq2_matvec_range": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp,
+                                     _c_size, _vp, _c_size, _vp]),
+    "bh_pq2_matmul_n": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp, _c_size,
+                                 _c_size, _vp, _c_size, _vp]),
+    "bh_host_dot_pq2_0_row": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _vp, _c_size,
+                                       _vp]),
+    "bh_host_pq2_matvec_range": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp,
+                                          _c_size, _vp, _c_size]),
+    "bh_host_pq2_matmul_n": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp,
+                                      _c_size, _c_size, _vp, _c_size]),
 }
 
 _LIB = None
@@ -292,6 +302,25 @@ def pq2_embed_gather(table, ne0: int, n_rows: int, ids, out=None, w=None, eps: f
                                         w.data_ptr(), w.numel(), eps, out.data_ptr(),
                                         out_norm.data_ptr(), _ptr(bad_id), _stream(stream)))
     return out, out_norm
+
+
+def pq2_matmul_n(payload, ne0: int, n_rows: int, x, base_row: int = 0, out=None, stream=None):
+    """kernels::pq2_matmul_n (src/kernels.rs:340-423) on device tensors:
+    payload uint8 (the tensor's whole PQ2_0 data), x [n_tok, ne0] f32 ->
+    y [n_tok, n_rows]; a 1-D x runs pq2_matvec_range and returns y [n_rows]."""
+    import torch
+    if x.dim() == 1:
+        y = torch.empty(n_rows, dtype=torch.float32, device=x.device) if out is None else out
+        check(lib().bh_pq2_matvec_range(payload.data_ptr(), payload.numel(), ne0, base_row,
+                                        n_rows, x.data_ptr(), x.numel(), y.data_ptr(),
+                                        y.numel(), _stream(stream)))
+        return y
+    n_tok = x.shape[0]
+    y = torch.empty((n_tok, n_rows), dtype=torch.float32, device=x.device) if out is None else out
+    check(lib().bh_pq2_matmul_n(payload.data_ptr(), payload.numel(), ne0, base_row, n_rows,
+                                x.data_ptr(), x.numel(), n_tok, y.data_ptr(), y.numel(),
+                                _stream(stream)))
+    return y
 
 
 def env_info() -> dict:

@@ -48,7 +48,8 @@ inline int pow2ceil(size_t v) {
 // of the same client on one device must not overlap in time.  Returns
 // nullptr on allocation failure (the status is already recorded).
 constexpr int kScratchSoftmax = 0;  // split-row softmax partials
-constexpr int kScratchSlots = 1;
+constexpr int kScratchMatmul = 1;   // PQ2_0 product: f16 x fragments, token scales
+constexpr int kScratchSlots = 2;
 void *device_scratch(size_t bytes, int slot);
 
 

@@ -235,3 +235,85 @@ extern "C" int bh_host_batch_embed(const uint8_t *payload, size_t payload_len, s
   if (int e = download(out, dout, n_tok * ne0 * 4, s.get())) return e;
   return ok();
 }
+
+namespace {
+// Uploads rows [base_row, base_row + n_rows) of a host payload and runs
+// bh_pq2_matmul_n on them; the caller has done the reference's checks.
+int host_matmul_rows(const uint8_t *payload, size_t ne0, uint64_t base_row, size_t n_rows,
+                     const float *x, size_t n_tok, float *y) {
+  if (n_rows == 0 || n_tok == 0) return ok();
+  const size_t rb = bh_pq2_row_bytes(ne0);
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dw, dx, dy;
+  if (int e = upload(dw, payload + base_row * rb, n_rows * rb, s.get())) return e;
+  if (int e = upload(dx, x, n_tok * ne0 * 4, s.get())) return e;
+  if (int e = dy.alloc(n_tok * n_rows * 4)) return e;
+  if (int e = bh_pq2_matmul_n(dw.as<uint8_t>(), n_rows * rb, ne0, 0, n_rows, dx.as<float>(),
+                              n_tok * ne0, n_tok, dy.as<float>(), n_tok * n_rows, s.handle()))
+    return e;
+  return download(y, dy, n_tok * n_rows * 4, s.get());
+}
+
+bool rows_end_bytes(uint64_t base_row, size_t n_rows, size_t rb, size_t *out) {
+  const unsigned __int128 v = (static_cast<unsigned __int128>(base_row) + n_rows) * rb;
+  if (v > static_cast<unsigned __int128>(SIZE_MAX)) return false;
+  *out = static_cast<size_t>(v);
+  return true;
+}
+}  // namespace
+
+extern "C" int bh_host_dot_pq2_0_row(const uint8_t *payload, size_t payload_len, size_t ne0,
+                                     uint64_t row, const float *x, size_t x_len, float *out) {
+  // src/kernels.rs:239-256
+  if (x_len != ne0)
+    return fail(BH_ERR_SHAPE, "dot_pq2_0_row: x length " + std::to_string(x_len) + " != ne0 " +
+                                  std::to_string(ne0));
+  const size_t rb = bh_pq2_row_bytes(ne0);
+  const size_t start = static_cast<size_t>(row) * rb, end = start + rb;
+  if (end > payload_len)
+    return fail(BH_ERR_SHAPE, "dot_pq2_0_row: row " + std::to_string(row) + " needs bytes " +
+                                  std::to_string(start) + ".." + std::to_string(end) +
+                                  ", payload is " + std::to_string(payload_len));
+  if (ne0 == 0) {
+    *out = 0.0f;
+    return ok();
+  }
+  return host_matmul_rows(payload, ne0, row, 1, x, 1, out);
+}
+
+extern "C" int bh_host_pq2_matvec_range(const uint8_t *payload, size_t payload_len, size_t ne0,
+                                        uint64_t base_row, size_t n_rows, const float *x,
+                                        size_t x_len, float *y, size_t y_len) {
+  // src/kernels.rs:291-307
+  if (x_len != ne0)
+    return fail(BH_ERR_SHAPE, "pq2_matvec_range: x length " + std::to_string(x_len) +
+                                  " != ne0 " + std::to_string(ne0));
+  if (y_len < n_rows) return fail(BH_ERR_SHAPE, "pq2_matvec_range: y too small");
+  const size_t rb = bh_pq2_row_bytes(ne0);
+  size_t byte_len = 0;
+  if (!rows_end_bytes(base_row, n_rows, rb, &byte_len))
+    return fail(BH_ERR_SHAPE, "pq2_matvec_range: row range byte length overflows");
+  if (byte_len > payload_len)
+    return fail(BH_ERR_SHAPE, "pq2_matvec_range: rows " + std::to_string(base_row) + ".." +
+                                  std::to_string(base_row + n_rows) + " need " +
+                                  std::to_string(byte_len) + " bytes, payload is " +
+                                  std::to_string(payload_len));
+  return host_matmul_rows(payload, ne0, base_row, n_rows, x, 1, y);
+}
+
+extern "C" int bh_host_pq2_matmul_n(const uint8_t *payload, size_t payload_len, size_t ne0,
+                                    uint64_t base_row, size_t n_rows, const float *x,
+                                    size_t x_len, size_t n_tok, float *y, size_t y_len) {
+  // src/kernels.rs:349-364
+  if (x_len != n_tok * ne0)
+    return fail(BH_ERR_SHAPE, "pq2_matmul_n: x length " + std::to_string(x_len) + " != n_tok " +
+                                  std::to_string(n_tok) + " * ne0 " + std::to_string(ne0));
+  if (y_len < n_tok * n_rows) return fail(BH_ERR_SHAPE, "pq2_matmul_n: y too small");
+  const size_t rb = bh_pq2_row_bytes(ne0);
+  size_t need = 0;
+  if (!rows_end_bytes(base_row, n_rows, rb, &need))
+    return fail(BH_ERR_SHAPE, "pq2_matmul_n: overflow");
+  if (need > payload_len) return fail(BH_ERR_SHAPE, "pq2_matmul_n: row range exceeds payload");
+  return host_matmul_rows(payload, ne0, base_row, n_rows, x, n_tok, y);
+}

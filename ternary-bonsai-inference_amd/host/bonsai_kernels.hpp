@@ -16,6 +16,9 @@
 //   kernels::softmax_rows(x, row_len)           -> Result<std::vector<float>>
 //   kernels::pq2_row_bytes(ne0)                 -> size_t
 //   kernels::decode_pq2_0_row(raw, ne0)         -> std::vector<float>
+//   kernels::dot_pq2_0_row(payload, ne0, row, x)            -> Result<float>
+//   kernels::pq2_matvec_range(payload, ne0, base, n, x, y)  -> Result<void>
+//   kernels::pq2_matmul_n(payload, ne0, base, n, x, n_tok, y) -> Result<void>
 //   rope::rope_imrope(head, p_t, p_h, p_w, p_e, n_dims, sections, freq_base)
 //   prefill::batch_embed(payload, ne0, n_rows, tokens) -> Result<std::vector<float>>
 //
@@ -134,6 +137,37 @@ inline std::vector<float> decode_pq2_0_row(const std::vector<uint8_t> &raw, size
   std::vector<float> out(ne0);
   detail::check_or_throw(bh_host_decode_pq2_0_row(raw.data(), raw.size(), ne0, out.data()));
   return out;
+}
+
+// src/kernels.rs:233-262
+inline Result<float> dot_pq2_0_row(const std::vector<uint8_t> &payload, size_t ne0, uint64_t row,
+                                   const std::vector<float> &x) {
+  float out = 0.0f;
+  const int st = bh_host_dot_pq2_0_row(payload.data(), payload.size(), ne0, row, x.data(),
+                                       x.size(), &out);
+  if (st != BH_OK) return Result<float>::err(bh_last_error());
+  return Result<float>::ok(out);
+}
+
+// src/kernels.rs:283-333: y[r] = row(base_row + r) . x for r < n_rows (y may
+// be longer; only the first n_rows entries are written)
+inline Result<bool> pq2_matvec_range(const std::vector<uint8_t> &payload, size_t ne0,
+                                     uint64_t base_row, size_t n_rows,
+                                     const std::vector<float> &x, std::vector<float> &y) {
+  const int st = bh_host_pq2_matvec_range(payload.data(), payload.size(), ne0, base_row, n_rows,
+                                          x.data(), x.size(), y.data(), y.size());
+  if (st != BH_OK) return Result<bool>::err(bh_last_error());
+  return Result<bool>::ok(true);
+}
+
+// src/kernels.rs:340-423: x [n_tok][ne0], y [n_tok][n_rows]
+inline Result<bool> pq2_matmul_n(const std::vector<uint8_t> &payload, size_t ne0,
+                                 uint64_t base_row, size_t n_rows, const std::vector<float> &x,
+                                 size_t n_tok, std::vector<float> &y) {
+  const int st = bh_host_pq2_matmul_n(payload.data(), payload.size(), ne0, base_row, n_rows,
+                                      x.data(), x.size(), n_tok, y.data(), y.size());
+  if (st != BH_OK) return Result<bool>::err(bh_last_error());
+  return Result<bool>::ok(true);
 }
 
 }  // namespace kernels

@@ -189,6 +189,84 @@ int main() {
     CHECK(bad.error() == "Weights: row_f32(token_embd.weight): row 6 out of range (n_rows 6)");
   });
 
+  // src/kernels.rs:857-907 (avx2_row_dot_matches_scalar): the reference
+  // compares two CPU dot orders to 1e-4 relative; here the mirror's device
+  // dot is held to the same bound against a double-precision dot of the
+  // same decoded rows.
+  run("avx2_row_dot_matches_scalar", [] {
+    const size_t ne0 = 5120, n_rows = 8, row_bytes = kernels::pq2_row_bytes(ne0);
+    std::vector<uint8_t> raw(row_bytes * n_rows, 0);
+    uint64_t s = 0x123456789abcdef0ull;
+    auto next = [&s] {
+      s ^= s << 13;
+      s ^= s >> 7;
+      s ^= s << 17;
+      return s;
+    };
+    auto f16 = [](float v) -> uint16_t {  // the test's own truncating converter
+      uint32_t b;
+      std::memcpy(&b, &v, 4);
+      const uint16_t sign = static_cast<uint16_t>((b >> 16) & 0x8000);
+      const int exp = static_cast<int>((b >> 23) & 0xff) - 127 + 15;
+      const uint32_t mant = (b & 0x7fffff) >> 13;
+      return static_cast<uint16_t>(sign | ((static_cast<uint16_t>(exp) << 10) | mant));
+    };
+    for (size_t r = 0; r < n_rows; ++r)
+      for (size_t b = 0; b < ne0 / 128; ++b) {
+        const size_t base = r * row_bytes + b * 34;
+        const float sc = 0.5f + static_cast<float>((next() >> 8) % 1000) / 1000.0f;
+        const uint16_t h = f16(sc);
+        raw[base] = static_cast<uint8_t>(h & 0xff);
+        raw[base + 1] = static_cast<uint8_t>(h >> 8);
+        for (int k = 0; k < 32; ++k) raw[base + 2 + k] = static_cast<uint8_t>(next() % 256);
+      }
+    std::vector<float> x(ne0);
+    for (auto &v : x) v = (static_cast<float>(next() % 2001) - 1000.0f) / 500.0f;
+    for (size_t r = 0; r < n_rows; ++r) {
+      const std::vector<uint8_t> row(raw.begin() + r * row_bytes, raw.begin() + (r + 1) * row_bytes);
+      const std::vector<float> w = kernels::decode_pq2_0_row(row, ne0);
+      double exact = 0.0;
+      for (size_t j = 0; j < ne0; ++j) exact += static_cast<double>(x[j]) * w[j];
+      const float dev = kernels::dot_pq2_0_row(raw, ne0, r, x).unwrap();
+      const double scale = std::fmax(std::fabs(exact), 1e-6);
+      CHECK(std::fabs(exact - dev) / scale < 1e-4);
+    }
+  });
+
+  // src/kernels.rs:910-946
+  run("pq2_matmul_n_matches_per_token_matvec", [] {
+    const size_t ne0 = 256, n_rows = 12, n_tok = 3, rb = kernels::pq2_row_bytes(ne0);
+    uint32_t seed = 0x12345678u;
+    auto next = [&seed] {
+      seed ^= seed << 13;
+      seed ^= seed >> 17;
+      seed ^= seed << 5;
+      return seed;
+    };
+    std::vector<uint8_t> payload(n_rows * rb, 0);
+    for (size_t r = 0; r < n_rows; ++r)
+      for (size_t blk = 0; blk < ne0 / 128; ++blk) {
+        const size_t base = r * rb + blk * 34;
+        // gguf::f32_to_half: round to nearest even (these are normal-range values)
+        const _Float16 hv = static_cast<_Float16>(static_cast<float>(next() % 500) / 250.0f + 0.01f);
+        uint16_t h;
+        std::memcpy(&h, &hv, 2);
+        payload[base] = static_cast<uint8_t>(h & 0xff);
+        payload[base + 1] = static_cast<uint8_t>(h >> 8);
+        for (int k = 0; k < 32; ++k) payload[base + 2 + k] = static_cast<uint8_t>(next() % 256);
+      }
+    std::vector<float> x(n_tok * ne0);
+    for (auto &v : x) v = (static_cast<float>(next() % 2001) - 1000.0f) / 500.0f;
+    std::vector<float> y_n(n_tok * n_rows, 0.0f);
+    CHECK(kernels::pq2_matmul_n(payload, ne0, 0, n_rows, x, n_tok, y_n).is_ok());
+    for (size_t t = 0; t < n_tok; ++t) {
+      std::vector<float> y1(n_rows, 0.0f);
+      const std::vector<float> xt(x.begin() + t * ne0, x.begin() + (t + 1) * ne0);
+      CHECK(kernels::pq2_matvec_range(payload, ne0, 0, n_rows, xt, y1).is_ok());
+      for (size_t r = 0; r < n_rows; ++r) CHECK(y_n[t * n_rows + r] == y1[r]);
+    }
+  });
+
   std::printf("%s: %d failed checks\n", g_fail ? "FAILED" : "OK", g_fail);
   return g_fail ? 1 : 0;
 }

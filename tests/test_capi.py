@@ -13,7 +13,7 @@ import pytest
 def test_library_exports_every_header_symbol(bh):
     lib = bh.lib()
     names = bh.header_symbols()
-    assert len(names) == 24
+    assert len(names) == 29
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     # and the Python binding declares a signature for each of them
@@ -110,6 +110,57 @@ def test_batch_embed_range_error_text(bh, synth):
                                "(n_rows 4)")
     assert lib.bh_host_decode_pq2_0_row(table.ctypes.data, 10, 256, out.ctypes.data) == \
         bh.BH_ERR_SHAPE
+
+
+def test_pq2_product_shape_errors(bh):
+    """src/kernels.rs:239-256, 291-307, 349-364: the reference's Err texts,
+    returned before any device work (the pointers are never read)."""
+    lib = bh.lib()
+    dummy = ctypes.c_void_p(16)
+    # device entry points
+    assert lib.bh_pq2_matvec_range(dummy, 1360, 5120, 0, 1, dummy, 5119, dummy, 1, None) == \
+        bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matvec_range: x length 5119 != ne0 5120"
+    assert lib.bh_pq2_matvec_range(dummy, 1360 * 4, 5120, 0, 4, dummy, 5120, dummy, 3, None) == \
+        bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matvec_range: y too small"
+    assert lib.bh_pq2_matvec_range(dummy, 1360 * 4, 5120, 2, 3, dummy, 5120, dummy, 3, None) == \
+        bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matvec_range: rows 2..5 need 6800 bytes, payload is 5440"
+    assert lib.bh_pq2_matvec_range(dummy, 1360, 5120, 2**63, 2**62, dummy, 5120, dummy,
+                                   2**62, None) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matvec_range: row range byte length overflows"
+    assert lib.bh_pq2_matmul_n(dummy, 68 * 12, 256, 0, 12, dummy, 767, 3, dummy, 36, None) == \
+        bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matmul_n: x length 767 != n_tok 3 * ne0 256"
+    assert lib.bh_pq2_matmul_n(dummy, 68 * 12, 256, 0, 12, dummy, 768, 3, dummy, 35, None) == \
+        bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matmul_n: y too small"
+    assert lib.bh_pq2_matmul_n(dummy, 68 * 12, 256, 1, 12, dummy, 768, 3, dummy, 36, None) == \
+        bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matmul_n: row range exceeds payload"
+    assert lib.bh_pq2_matmul_n(dummy, 68, 256, 2**63, 2**62, dummy, 256, 1, dummy, 2**62,
+                               None) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matmul_n: overflow"
+    # empty ranges succeed without touching anything
+    assert lib.bh_pq2_matvec_range(None, 0, 5120, 0, 0, None, 5120, None, 0, None) == bh.BH_OK
+    assert lib.bh_pq2_matmul_n(None, 0, 256, 0, 0, None, 0, 0, None, 0, None) == bh.BH_OK
+    # host mirrors: same texts, dot_pq2_0_row's own
+    raw = np.zeros(1360 * 2, np.uint8)
+    x = np.zeros(5120, np.float32)
+    out = np.zeros(4, np.float32)
+    assert lib.bh_host_dot_pq2_0_row(raw.ctypes.data, raw.size, 5120, 0, x.ctypes.data, 5000,
+                                     out.ctypes.data) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "dot_pq2_0_row: x length 5000 != ne0 5120"
+    assert lib.bh_host_dot_pq2_0_row(raw.ctypes.data, raw.size, 5120, 2, x.ctypes.data, 5120,
+                                     out.ctypes.data) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "dot_pq2_0_row: row 2 needs bytes 2720..4080, payload is 2720"
+    assert lib.bh_host_pq2_matvec_range(raw.ctypes.data, raw.size, 5120, 1, 2, x.ctypes.data,
+                                        5120, out.ctypes.data, 4) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matvec_range: rows 1..3 need 4080 bytes, payload is 2720"
+    assert lib.bh_host_pq2_matmul_n(raw.ctypes.data, raw.size, 5120, 0, 2, x.ctypes.data, 5120,
+                                    2, out.ctypes.data, 4) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "pq2_matmul_n: x length 5120 != n_tok 2 * ne0 5120"
 
 
 def test_splitmix64_known_vector(synth):

@@ -376,3 +376,74 @@ def test_embed_gather_rms_is_rms_of_rows(oracle, synth):
     ref = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-6) * w
     # the reference sums 5120 squares sequentially in f32: ~1e-5 from exact
     assert rel_err(nrm, ref) < 3e-5
+
+
+# ---------------------------------------------------------------------------
+# PQ2_0 row dot / products (src/kernels.rs:233-423, 633-653)
+# ---------------------------------------------------------------------------
+
+def test_pq2_row_dot_one_hot_is_the_decoded_weight(oracle, synth):
+    """Closed form: x = e_j gives the row's decoded weight j exactly (one
+    non-zero product in one block, every other block adds scale * 0)."""
+    import pq2data
+    ne0, n_rows = 384, 5
+    table = synth.pq2_table(synth.Rng(41), n_rows, ne0).reshape(-1)
+    w = pq2data.decoded(table, ne0, n_rows).astype(np.float32)
+    for j in (0, 1, 127, 128, 200, 383):
+        x = np.zeros(ne0, np.float32)
+        x[j] = 1.0
+        y = oracle.pq2_matmul_n(table, ne0, n_rows, x)
+        assert np.array_equal(y, w[:, j]), j
+        # a power-of-two multiple scales exactly
+        x[j] = 0.25
+        assert np.array_equal(oracle.pq2_matmul_n(table, ne0, n_rows, x), w[:, j] * 0.25)
+
+
+def test_pq2_row_dot_matches_float64_dot(oracle, synth):
+    """The f32 block sums agree with an exact-enough float64 dot of the
+    numpy-decoded rows (a dropped block, a wrong code order or a scale
+    applied to the wrong block fails by orders of magnitude)."""
+    import pq2data
+    ne0, n_rows, n_tok = 1280, 40, 3
+    table = synth.pq2_table(synth.Rng(42), n_rows, ne0).reshape(-1)
+    x = synth.Rng(43).normal(n_tok * ne0).reshape(n_tok, ne0)
+    y = oracle.pq2_matmul_n(table, ne0, n_rows, x)
+    ref = x.astype(np.float64) @ pq2data.decoded(table, ne0, n_rows).T
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-6
+    # partial last block (ne0 not a multiple of 128)
+    ne0 = 300
+    table = synth.pq2_table(synth.Rng(44), 7, ne0).reshape(-1)
+    x = synth.Rng(45).normal(ne0)
+    y = oracle.pq2_matmul_n(table, ne0, 7, x)
+    ref = pq2data.decoded(table, ne0, 7) @ x.astype(np.float64)
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-6
+
+
+def test_pq2_row_dot_reference_avx2_case(oracle):
+    """src/kernels.rs:857-907 restated: the reference checks its AVX2 dot
+    against row_dot_scalar to 1e-4 relative; the oracle (row_dot_scalar)
+    must meet the same bound against the float64 dot of the same rows."""
+    import pq2data
+    raw, x, ne0, n_rows = pq2data.avx2_case()
+    ref = pq2data.decoded(raw, ne0, n_rows) @ x.astype(np.float64)
+    rb = oracle.pq2_row_bytes(ne0)
+    for r in range(n_rows):
+        s = oracle.pq2_row_dot(raw[r * rb:(r + 1) * rb], ne0, x)
+        assert abs(s - ref[r]) / max(abs(s), 1e-6) < 1e-4, r
+    y = oracle.pq2_matmul_n(raw, ne0, n_rows, x)
+    assert np.array_equal(y, np.array([oracle.pq2_row_dot(raw[r * rb:(r + 1) * rb], ne0, x)
+                                       for r in range(n_rows)], np.float32))
+
+
+def test_pq2_matmul_n_reference_case(oracle, synth):
+    """src/kernels.rs:910-946 restated: pq2_matmul_n equals the per-token
+    matvec exactly; base_row selects the rows of the range."""
+    import pq2data
+    payload, x, ne0, n_rows, n_tok = pq2data.matmul_case(synth.f32_to_half)
+    y = oracle.pq2_matmul_n(payload, ne0, n_rows, x)
+    for t in range(n_tok):
+        assert np.array_equal(y[t], oracle.pq2_matmul_n(payload, ne0, n_rows, x[t]))
+    ref = x.astype(np.float64) @ pq2data.decoded(payload, ne0, n_rows).T
+    assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-6
+    tail = oracle.pq2_matmul_n(payload, ne0, 5, x, base_row=7)
+    assert np.array_equal(tail, y[:, 7:12])
