@@ -29,6 +29,7 @@ from pathlib import Path
 
 REPO = Path(__file__).resolve().parent
 PKG_DIR = REPO / "ternary-bonsai-inference_amd"
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16/bf16 MFMA
 HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 600 * 2**20  # > 2x the 256 MB MALL
 
@@ -213,6 +214,49 @@ def wl_gather_rms(bh, synth, dev, stream, n_tok=8192, vocab=248320, ne0=5120):
     return launch, len(sets), bytes_per, n_tok, (table, w, sets)
 
 
+def wl_pq2_matmul(bh, synth, dev, stream, n_rows, ne0, n_tok):
+    """kernels::pq2_matmul_n / pq2_matvec_range (src/kernels.rs:283-423):
+    Y[n_tok][n_rows] = X[n_tok][ne0] * W^T over a PQ2_0 weight tensor.  Each
+    rotating set has its own weight tensor, so the weights stream from HBM
+    (a decode step reads every matrix once).  Algorithmic bytes: the packed
+    weights once, x and y once."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    rb = bh.pq2_row_bytes(ne0)
+    bytes_per = n_rows * rb + n_tok * ne0 * 4 + n_tok * n_rows * 4
+    sets = []
+    for _ in range(n_sets(bytes_per)):
+        table = synth.torch_pq2_table(n_rows, ne0, dev, generator=g).reshape(-1)
+        x = torch.randn((n_tok, ne0), device=dev, generator=g)
+        sets.append((table, x, torch.empty((n_tok, n_rows), device=dev)))
+    lib, sh = bh.lib(), stream.cuda_stream
+
+    def launch(i):
+        table, x, y = sets[i]
+        if n_tok == 1:
+            st = lib.bh_pq2_matvec_range(table.data_ptr(), table.numel(), ne0, 0, n_rows,
+                                         x.data_ptr(), ne0, y.data_ptr(), n_rows, sh)
+        else:
+            st = lib.bh_pq2_matmul_n(table.data_ptr(), table.numel(), ne0, 0, n_rows,
+                                     x.data_ptr(), x.numel(), n_tok, y.data_ptr(), y.numel(), sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, n_rows, sets
+
+
+def measure_mm(name, n_rows, ne0, n_tok, bh, synth, dev, stream, steps, warmup):
+    """A product entry: HBM GB/s as every entry, plus useful TFLOP/s (2 flops
+    per weight and token) against the dense f16 MFMA peak; the x side runs
+    as two f16 MFMAs (hi, lo), so half that peak is the useful ceiling."""
+    rec = measure(name, wl_pq2_matmul(bh, synth, dev, stream, n_rows, ne0, n_tok), steps,
+                  warmup, stream)
+    tflops = 2.0 * n_tok * n_rows * ne0 / (rec["ms"] * 1e-3) / 1e12
+    rec.update({"tokens": n_tok, "TFLOPs": round(tflops, 2),
+                "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)})
+    return rec
+
+
 def measure(name, wl, steps, warmup, stream, extra=None):
     import torch
     launch, n_rot, nbytes, rows, keep = wl
@@ -360,6 +404,16 @@ def main() -> int:
                         ksteps, args.warmup, stream),
                 measure("pq2_gather_rms T=8192", wl_gather_rms(bh, synth, dev, stream), ksteps,
                         args.warmup, stream),
+                measure_mm("pq2_matvec LM head [248320x5120] N=1", 248320, 5120, 1, bh, synth,
+                           dev, stream, ksteps, args.warmup),
+                measure_mm("pq2_matvec ffn_up [17408x5120] N=1", 17408, 5120, 1, bh, synth,
+                           dev, stream, ksteps, args.warmup),
+                measure_mm("pq2_matvec ffn_down [5120x17408] N=1", 5120, 17408, 1, bh, synth,
+                           dev, stream, ksteps, args.warmup),
+                measure_mm("pq2_matmul_n ffn_up [17408x5120] N=64", 17408, 5120, 64, bh, synth,
+                           dev, stream, ksteps, args.warmup),
+                measure_mm("pq2_matmul_n LM head [248320x5120] N=16", 248320, 5120, 16, bh,
+                           synth, dev, stream, ksteps, args.warmup),
             ]
 
     cpu = None

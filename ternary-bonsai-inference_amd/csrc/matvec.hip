@@ -53,73 +53,69 @@ __host__ __device__ constexpr int mm_column(int i, int g, int j, int h) {
 }
 
 // ---------------------------------------------------------------------------
-// Prepare: per-token power-of-two scale and the hi/lo f16 A fragments.
-// afrag layout: [tile][kstep][piece (hi, lo)][64 lanes] x 16 bytes.
+// Prepare: the hi/lo f16 A fragments, with a power of two per (token,
+// 128-block) chosen so the block's largest |x| lands in [2^14, 2^15): hi
+// never overflows f16 and lo keeps 11 more bits.  The power of two comes
+// back out in the product kernel's per-block f32 step (exact).
+//   afrag: [tile][kstep][piece (hi, lo)][64 lanes] x 16 bytes, written only
+//          for real tokens (the product kernel zero-fills the others);
+//   binv:  [tile][block][lane group g] float4 = 2^-e of tokens 4g .. 4g+3.
 // ---------------------------------------------------------------------------
 struct PrepArgs {
-  const float *x;     // [n_tok][ne0]
+  const float *x;  // [n_tok][ne0]
   uint4 *afrag;
-  float *tok_scale;   // [n_tok]: 2^e of each token
-  float *tok_inv;     // [n_tok]: 2^-e
-  int ne0, n_tok, n_ksteps, n_tiles;
+  float *binv;
+  int ne0, n_tok, nblk, n_ksteps;
 };
 
-// One block per token: the power of two that puts the token's largest |x|
-// in [2^14, 2^15), so hi never overflows f16 and lo keeps 11 more bits.
-__global__ __launch_bounds__(kMmThreads) void pq2_mm_scale_kernel(PrepArgs a) {
-  __shared__ float part[kMmThreads / 64];
-  const int m = blockIdx.x;
-  const float *xr = a.x + static_cast<size_t>(m) * a.ne0;
-  float mx = 0.0f;
-  for (int j = threadIdx.x; j < a.ne0; j += kMmThreads) mx = fmaxf(mx, fabsf(xr[j]));  // NaN ignored
-  mx = group_reduce<kMmThreads>(mx, MaxOp{}, part);
-  if (threadIdx.x == 0) {
-    int e = 0;
-    if (mx > 0.0f && mx <= 3.4e38f) {
-      int k;
-      (void)frexpf(mx, &k);  // mx = f * 2^k, f in [0.5, 1): mx * 2^(15-k) in [2^14, 2^15)
-      e = 15 - k;
-      e = e < -126 ? -126 : (e > 126 ? 126 : e);  // 2^e and 2^-e stay normal f32
-    }
-    a.tok_scale[m] = ldexpf(1.0f, e);
-    a.tok_inv[m] = ldexpf(1.0f, -e);
-  }
-}
-
+// One lane per (token, block): 128 columns, one max, 32 fragment halves.
 __global__ __launch_bounds__(kMmThreads) void pq2_mm_prep_kernel(PrepArgs a) {
-  const int tile = blockIdx.x;
-  const int n_items = a.n_ksteps * 64;
-  for (int item = blockIdx.y * kMmThreads + threadIdx.x; item < n_items;
-       item += gridDim.y * kMmThreads) {
-    const int ks = item >> 6, l = item & 63;
-    const int ml = l & 15, g = l >> 4, i = ks & 3, blk = ks >> 2;
-    const int m = 16 * tile + ml;
-    h8 hi, lo;
+  const int item = blockIdx.x * kMmThreads + threadIdx.x;
+  if (item >= a.n_tok * a.nblk) return;
+  const int m = item / a.nblk, blk = item - m * a.nblk;
+  const float4 *xr = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(m) * a.ne0 + 128 * blk);
+  float4 v[32];
+  float mx = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      hi[e] = static_cast<_Float16>(0.0f);
-      lo[e] = static_cast<_Float16>(0.0f);
-    }
-    if (m < a.n_tok) {
-      const float s = a.tok_scale[m];
-      const float *xr = a.x + static_cast<size_t>(m) * a.ne0 + 128 * blk;
-      const float4 p0 = *reinterpret_cast<const float4 *>(xr + mm_column(i, g, 0, 0));
-      const float4 p1 = *reinterpret_cast<const float4 *>(xr + mm_column(i, g, 0, 1));
-      const float v[8] = {p0.x * s, p1.x * s, p0.y * s, p1.y * s,
-                          p0.z * s, p1.z * s, p0.w * s, p1.w * s};  // element 2j + h
+  for (int c = 0; c < 32; ++c) {
+    v[c] = xr[c];
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+  }
+  int e = 0;  // NaN is ignored by fmaxf; an all-zero or non-finite block keeps 2^0
+  if (mx > 0.0f && mx <= 3.4e38f) {
+    int k;
+    (void)frexpf(mx, &k);  // mx = f * 2^k, f in [0.5, 1): mx * 2^(15-k) in [2^14, 2^15)
+    e = 15 - k;
+    e = e < -126 ? -126 : (e > 126 ? 126 : e);  // 2^e and 2^-e stay normal f32
+  }
+  const float s = ldexpf(1.0f, e);
+  const int tile = m >> 4, ml = m & 15;
+  a.binv[((static_cast<size_t>(tile) * a.nblk + blk) * 4 + (ml >> 2)) * 4 + (ml & 3)] = ldexpf(1.0f, -e);
+  uint4 *frag = a.afrag + static_cast<size_t>(tile) * a.n_ksteps * 2 * 64;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const _Float16 h = static_cast<_Float16>(v[e]);
-        hi[e] = h;
-        // an infinite x keeps lo = 0 (inf - inf would turn the term into NaN)
-        lo[e] = __builtin_isinf(static_cast<float>(h))
-                    ? static_cast<_Float16>(0.0f)
-                    : static_cast<_Float16>(v[e] - static_cast<float>(h));
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      h8 hi, lo;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // columns mm_column(i, g, j, h), j = 0..3: float4 number c
+        const float4 q = v[8 * g + 4 * (i >> 1) + 2 * h + (i & 1)];
+        const float f[4] = {q.x * s, q.y * s, q.z * s, q.w * s};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const _Float16 hv = static_cast<_Float16>(f[j]);
+          hi[2 * j + h] = hv;
+          // an infinite x keeps lo = 0 (inf - inf would turn the term into NaN)
+          lo[2 * j + h] = __builtin_isinf(static_cast<float>(hv))
+                              ? static_cast<_Float16>(0.0f)
+                              : static_cast<_Float16>(f[j] - static_cast<float>(hv));
+        }
       }
+      uint4 *dst = frag + static_cast<size_t>(4 * blk + i) * 2 * 64 + 16 * g + ml;
+      dst[0] = __builtin_bit_cast(uint4, hi);
+      dst[64] = __builtin_bit_cast(uint4, lo);
     }
-    uint4 *dst = a.afrag + (static_cast<size_t>(tile) * a.n_ksteps + ks) * 2 * 64 + l;
-    dst[0] = __builtin_bit_cast(uint4, hi);
-    dst[64] = __builtin_bit_cast(uint4, lo);
   }
 }
 
@@ -127,24 +123,39 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_prep_kernel(PrepArgs a) {
 // Main product.  Block = 4 waves; a wave owns NT 16-row weight tiles and the
 // block's MT token tiles.  Lane l: row n = l & 15 of each weight tile, lane
 // group g = l >> 4 (code bytes 8g..8g+7 of every block).
+//
+// Weights are read two blocks (68 bytes, 17 dwords) at a time: with 4-byte
+// aligned rows the pair starts on a dword, its odd block's codes are
+// dword-aligned and its even block's are 2 bytes off, so every lane reads
+// whole dwords inside the pair (dwordx3 + dwordx2 + the two scale dwords)
+// and realigns with a funnel shift -- no read ever leaves the pair.
 // ---------------------------------------------------------------------------
 struct MmArgs {
-  const uint8_t *w;      // first row of the range (payload + base_row * row_bytes)
+  const uint8_t *w;    // first row of the range (payload + base_row * row_bytes)
   const uint4 *afrag;
-  const float *tok_inv;
-  float *y;              // [n_tok][y_stride]
+  const float4 *binv;
+  float *y;            // [n_tok][y_stride]
   size_t row_bytes;
   int n_rows, nblk, n_ksteps, n_tok, y_stride;
 };
 
+// (t & mask) | (b & ~mask) in one instruction (gfx9's three-operand
+// encodings take no literal, so the compiler would split it in two).
+__device__ __forceinline__ uint32_t bit_select(uint32_t mask, uint32_t t, uint32_t b) {
+  uint32_t r;
+  __asm__("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(t), "v"(b));
+  return r;
+}
+
 // f16 pairs (code_lo - 1, code_hi - 1) of the codes at bits (2j, 2j + 16)
-// of t, for j = 0..3, as the 8 halves of a B fragment.
-__device__ __forceinline__ h8 decode_codes(uint32_t t) {
+// of t, for j = 0..3, as the 8 halves of a B fragment.  `magic` holds
+// 0x64006400 (1024.0 in both halves, no bits in the code positions).
+__device__ __forceinline__ h8 decode_codes(uint32_t t, uint32_t magic) {
   h8 r;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t mask = (3u << (2 * j)) | (3u << (2 * j + 16));
-    const uint32_t bits = (t & mask) | 0x64006400u;  // 1024 + code * 2^(2j), exact
+    const uint32_t bits = bit_select(mask, t, magic);  // 1024 + code * 2^(2j), exact
     const h2 v = __builtin_bit_cast(h2, bits);
     const _Float16 k = static_cast<_Float16>(1.0f / static_cast<float>(1 << (2 * j)));
     const _Float16 c = static_cast<_Float16>(-(1024.0f / static_cast<float>(1 << (2 * j)) + 1.0f));
@@ -156,32 +167,88 @@ __device__ __forceinline__ h8 decode_codes(uint32_t t) {
   return r;
 }
 
-template <int MT, int NT>
+struct PairData {
+  uint32_t e0, e1, e2;  // pair dwords 2g .. 2g+2 (even block's codes, 2 bytes in)
+  uint32_t o0, o1;      // pair dwords 9+2g, 10+2g (odd block's codes)
+  uint32_t s0, s8;      // pair dwords 0 and 8 (the two f16 scales)
+};
+
+__device__ __forceinline__ PairData load_pair(const uint32_t *rp, int g) {
+  PairData d;
+  const uint3 e = *reinterpret_cast<const uint3 *>(rp + 2 * g);
+  const uint2 o = *reinterpret_cast<const uint2 *>(rp + 9 + 2 * g);
+  d.e0 = e.x;
+  d.e1 = e.y;
+  d.e2 = e.z;
+  d.o0 = o.x;
+  d.o1 = o.y;
+  d.s0 = rp[0];
+  d.s8 = rp[8];
+  return d;
+}
+
+// Codes and scale of one block of a pair, ready for the MFMA steps.
+struct BlockCodes {
+  uint32_t cd[2];  // code bytes 8g..8g+3, 8g+4..8g+7
+  float sc;
+};
+
+__device__ __forceinline__ BlockCodes block_codes(const PairData &d, int half) {
+  BlockCodes c;
+  if (half == 0) {
+    c.cd[0] = __builtin_amdgcn_alignbyte(d.e1, d.e0, 2);
+    c.cd[1] = __builtin_amdgcn_alignbyte(d.e2, d.e1, 2);
+    c.sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(d.s0)));
+  } else {
+    c.cd[0] = d.o0;
+    c.cd[1] = d.o1;
+    c.sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(d.s8 >> 16)));
+  }
+  return c;
+}
+
+template <int MT, int NT, bool ALDS>
 __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
+  // ALDS (one token tile of at most kLdsTok tokens): the x side of the whole
+  // product is staged in LDS once, fragments [kstep][piece][token][lane
+  // group] followed by the block factors [block][lane group]
+  extern __shared__ uint4 a_lds[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int row_wave = blockIdx.x * (4 * 16 * NT) + wave * 16 * NT;
   const int tile0 = blockIdx.y * MT;
 
-  const uint16_t *wp[NT];
+  const uint32_t *wp[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     int row = row_wave + 16 * t + n;
     row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
-    wp[t] = reinterpret_cast<const uint16_t *>(a.w + static_cast<size_t>(row) * a.row_bytes);
+    wp[t] = reinterpret_cast<const uint32_t *>(a.w + static_cast<size_t>(row) * a.row_bytes);
   }
-  // halfword index of block b's scale is 17b; its code bytes 8g..8g+7 are
-  // halfwords 17b + 1 + 4g .. +3 (every block and row starts on an even byte)
-  uint32_t nxt_c[NT][4], nxt_s[NT];
-  auto load_block = [&](int b) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const uint16_t *p = wp[t] + 17 * b;
-      nxt_s[t] = p[0];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) nxt_c[t][q] = p[1 + 4 * g + q];
+  // Row m of an MFMA result depends on row m of A only, so the lanes of a
+  // tile's absent tokens may feed any fragment (their rows are never
+  // stored): they read a real token's (ALDS) or unwritten scratch.
+  const uint4 *af = a.afrag + static_cast<size_t>(tile0) * a.n_ksteps * 2 * 64 + lane;
+  const float4 *binv_g = a.binv + static_cast<size_t>(tile0) * a.nblk * 4 + g;
+  const uint4 *al = a_lds;
+  const float4 *binv_l = nullptr;
+  int lds_tok_stride = 0;
+  if constexpr (ALDS) {
+    const int nt = a.n_tok;  // <= kLdsTok: tile 0 only
+    const int total = a.n_ksteps * 2 * nt * 4;
+    for (int i = threadIdx.x; i < total; i += kMmThreads) {
+      const int gq = i & 3, rest = i >> 2;
+      const int m = rest % nt, kp = rest / nt;  // kp = 2 * kstep + piece
+      a_lds[i] = a.afrag[static_cast<size_t>(kp) * 64 + 16 * gq + m];
     }
-  };
+    float4 *bl = reinterpret_cast<float4 *>(a_lds + total);
+    for (int i = threadIdx.x; i < a.nblk * 4; i += kMmThreads) bl[i] = a.binv[i];
+    __syncthreads();
+    al = a_lds + (n < nt ? n : 0) * 4 + g;
+    lds_tok_stride = nt * 4;
+    binv_l = bl + g;
+  }
+  const uint32_t magic = 0x64006400u;
 
   f4v tot[MT][NT];
 #pragma unroll
@@ -189,18 +256,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) tot[mt][t] = f4v{0.f, 0.f, 0.f, 0.f};
 
-  const uint4 *af = a.afrag + static_cast<size_t>(tile0) * a.n_ksteps * 2 * 64 + lane;
-  load_block(0);
-  for (int b = 0; b < a.nblk; ++b) {
-    uint32_t cd[NT][2], sc[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      cd[t][0] = nxt_c[t][0] | (nxt_c[t][1] << 16);  // code bytes 8g .. 8g+3
-      cd[t][1] = nxt_c[t][2] | (nxt_c[t][3] << 16);  // code bytes 8g+4 .. 8g+7
-      sc[t] = nxt_s[t];
-    }
-    if (b + 1 < a.nblk) load_block(b + 1);
-
+  auto do_block = [&](const BlockCodes(&bc)[NT], int b) {
     f4v acc[MT][NT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -212,14 +268,20 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
       h8 ahi[MT], alo[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const uint4 *p = af + (static_cast<size_t>(mt) * a.n_ksteps + ks) * 2 * 64;
-        ahi[mt] = __builtin_bit_cast(h8, p[0]);
-        alo[mt] = __builtin_bit_cast(h8, p[64]);
+        if constexpr (ALDS) {
+          const uint4 *pl = al + (2 * ks) * lds_tok_stride;
+          ahi[mt] = __builtin_bit_cast(h8, pl[0]);
+          alo[mt] = __builtin_bit_cast(h8, pl[lds_tok_stride]);
+        } else {
+          const uint4 *pg = af + (static_cast<size_t>(mt) * a.n_ksteps + ks) * 2 * 64;
+          ahi[mt] = __builtin_bit_cast(h8, pg[0]);
+          alo[mt] = __builtin_bit_cast(h8, pg[64]);
+        }
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const uint32_t d = cd[t][i >> 1];
-        const h8 bf = decode_codes((i & 1) ? (d >> 8) : d);
+        const uint32_t d = bc[t].cd[i >> 1];
+        const h8 bf = decode_codes((i & 1) ? (d >> 8) : d, magic);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[mt], bf, acc[mt][t], 0, 0, 0);
@@ -227,20 +289,56 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
         }
       }
     }
-    // src/kernels.rs:651: acc += scale * block_acc (f32 product, then sum)
+    // src/kernels.rs:651: acc += scale * block_acc -- block_acc arrives
+    // multiplied by the block's 2^e, so the factor is scale * 2^-e (exact)
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const float s = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(sc[t])));
+    for (int mt = 0; mt < MT; ++mt) {
+      float4 bi;
+      if constexpr (ALDS) {
+        bi = binv_l[b * 4];
+      } else {
+        bi = binv_g[(static_cast<size_t>(mt) * a.nblk + b) * 4];
+      }
+      const float inv[4] = {bi.x, bi.y, bi.z, bi.w};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        f4v p;
+      for (int t = 0; t < NT; ++t) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) p[q] = s * acc[mt][t][q];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) tot[mt][t][q] = tot[mt][t][q] + p[q];
+        for (int q = 0; q < 4; ++q) {
+          const float f = bc[t].sc * inv[q];
+          const float prod = f * acc[mt][t][q];
+          tot[mt][t][q] = tot[mt][t][q] + prod;
+        }
       }
     }
+  };
+
+  // weight pairs stream two deep: pair p + 2 is requested while pair p runs
+  const int npairs = a.nblk >> 1;
+  PairData pa[NT], pb[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    pa[t] = load_pair(wp[t], g);
+    if (npairs > 1) pb[t] = load_pair(wp[t] + 17, g);
   }
+  auto run_pair = [&](PairData(&buf)[NT], int p) {
+    BlockCodes b0[NT], b1[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      b0[t] = block_codes(buf[t], 0);
+      b1[t] = block_codes(buf[t], 1);
+    }
+    if (p + 2 < npairs) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) buf[t] = load_pair(wp[t] + 17 * (p + 2), g);
+    }
+    do_block(b0, 2 * p);
+    do_block(b1, 2 * p + 1);
+  };
+  for (int p = 0; p < npairs; p += 2) {
+    run_pair(pa, p);
+    if (p + 1 < npairs) run_pair(pb, p + 1);
+  }
+
   // lane holds tokens 4g..4g+3 of each token tile, row n of each weight tile
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -248,11 +346,10 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
     for (int q = 0; q < 4; ++q) {
       const int m = 16 * (tile0 + mt) + 4 * g + q;
       if (m >= a.n_tok) continue;
-      const float inv = a.tok_inv[m];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int row = row_wave + 16 * t + n;
-        if (row < a.n_rows) a.y[static_cast<size_t>(m) * a.y_stride + row] = tot[mt][t][q] * inv;
+        if (row < a.n_rows) a.y[static_cast<size_t>(m) * a.y_stride + row] = tot[mt][t][q];
       }
     }
   }
@@ -293,11 +390,24 @@ __global__ void fill_zero_kernel(float *y, size_t n) {
   if (i < n) y[i] = 0.0f;
 }
 
-template <int MT, int NT>
+constexpr int kLdsTok = 4;                 // token counts staged whole in LDS
+constexpr size_t kLdsABytes = 80 * 1024;   // their LDS budget
+
+template <int MT, int NT, bool ALDS = false>
 int launch_mm(const MmArgs &a, int n_tiles, hipStream_t st) {
   const unsigned gx = static_cast<unsigned>((a.n_rows + 64 * NT - 1) / (64 * NT));
   const unsigned gy = static_cast<unsigned>((n_tiles + MT - 1) / MT);
-  BH_LAUNCH((pq2_mm_kernel<MT, NT>), dim3(gx, gy), kMmThreads, 0, st, a);
+  size_t lds = 0;
+  if constexpr (ALDS) {
+    lds = static_cast<size_t>(a.n_ksteps) * 2 * a.n_tok * 4 * sizeof(uint4) +
+          static_cast<size_t>(a.nblk) * 4 * sizeof(float4);
+    if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_mm_kernel<MT, NT, true>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              static_cast<int>(kLdsABytes)),
+                          "hipFuncSetAttribute"))
+      return e;
+  }
+  BH_LAUNCH((pq2_mm_kernel<MT, NT, ALDS>), dim3(gx, gy), kMmThreads, lds, st, a);
   return ok();
 }
 
@@ -313,7 +423,11 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
     BH_LAUNCH(fill_zero_kernel, static_cast<unsigned>((total + 255) / 256), 256, 0, st, y, total);
     return ok();
   }
-  const bool fast = ne0 % 128 == 0 && aligned16(x) && (reinterpret_cast<uintptr_t>(w) & 1u) == 0;
+  // fast path: whole 128-blocks, an even block count (rows and block pairs
+  // start on dwords), 16-byte aligned x rows
+  const size_t nblk = ne0 / 128;
+  const bool fast = ne0 % 128 == 0 && nblk % 2 == 0 && aligned16(x) &&
+                    (reinterpret_cast<uintptr_t>(w) & 3u) == 0;
   if (!fast) {
     BH_LAUNCH(pq2_mm_generic_kernel, dim3(static_cast<unsigned>(n_rows), static_cast<unsigned>(n_tok)),
               64, 0, st, w, row_bytes, static_cast<int>(ne0), x, static_cast<int>(n_tok), y,
@@ -324,24 +438,27 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   const int n_tiles = static_cast<int>((n_tok + 15) / 16);
   const int mt = n_tiles >= 4 ? 4 : (n_tiles >= 2 ? 2 : 1);
   const int tiles_padded = (n_tiles + mt - 1) / mt * mt;
-  // scratch: A fragments, then the per-token 2^e and 2^-e
+  // scratch: A fragments, then the per-(token, block) powers of two
   const size_t frag_bytes = static_cast<size_t>(tiles_padded) * n_ksteps * 2 * 64 * sizeof(uint4);
-  const size_t sc_off = (frag_bytes + 255) / 256 * 256;
-  char *scratch =
-      static_cast<char *>(device_scratch(sc_off + 2 * n_tok * sizeof(float), kScratchMatmul));
+  const size_t binv_off = (frag_bytes + 255) / 256 * 256;
+  const size_t binv_bytes = static_cast<size_t>(tiles_padded) * nblk * 4 * sizeof(float4);
+  char *scratch = static_cast<char *>(device_scratch(binv_off + binv_bytes, kScratchMatmul));
   if (scratch == nullptr) return BH_ERR_HIP;
-  PrepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float *>(scratch + sc_off),
-              reinterpret_cast<float *>(scratch + sc_off) + n_tok, static_cast<int>(ne0),
-              static_cast<int>(n_tok), n_ksteps, tiles_padded};
-  BH_LAUNCH(pq2_mm_scale_kernel, static_cast<unsigned>(n_tok), kMmThreads, 0, st, pa);
-  const unsigned splits = static_cast<unsigned>((n_ksteps * 64 + kMmThreads * 4 - 1) / (kMmThreads * 4));
-  BH_LAUNCH(pq2_mm_prep_kernel, dim3(static_cast<unsigned>(tiles_padded), splits), kMmThreads, 0, st, pa);
+  PrepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float *>(scratch + binv_off),
+              static_cast<int>(ne0), static_cast<int>(n_tok), static_cast<int>(nblk), n_ksteps};
+  const size_t items = n_tok * nblk;
+  BH_LAUNCH(pq2_mm_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
+            kMmThreads, 0, st, pa);
 
-  MmArgs a{w, pa.afrag, pa.tok_inv, y, row_bytes, static_cast<int>(n_rows),
-           static_cast<int>(ne0 / 128), n_ksteps, static_cast<int>(n_tok),
+  MmArgs a{w, pa.afrag, reinterpret_cast<const float4 *>(pa.binv), y, row_bytes,
+           static_cast<int>(n_rows), static_cast<int>(nblk), n_ksteps, static_cast<int>(n_tok),
            static_cast<int>(n_rows)};
   // a wave takes 4 row tiles when that still leaves >= 2 blocks per CU
   const bool wide = n_rows >= static_cast<size_t>(256) * 2 * 256;
+  const bool a_in_lds = n_tok <= kLdsTok && static_cast<size_t>(n_ksteps) * 2 * n_tok * 4 * sizeof(uint4) +
+                                                 nblk * 4 * sizeof(float4) <= kLdsABytes;
+  if (a_in_lds)
+    return wide ? launch_mm<1, 4, true>(a, n_tiles, st) : launch_mm<1, 1, true>(a, n_tiles, st);
   switch (mt) {
     case 4: return wide ? launch_mm<4, 4>(a, n_tiles, st) : launch_mm<4, 1>(a, n_tiles, st);
     case 2: return wide ? launch_mm<2, 4>(a, n_tiles, st) : launch_mm<2, 1>(a, n_tiles, st);
