@@ -10,24 +10,21 @@
 // with MFMA tiles, in a different summation order (max relative difference
 // well below 1e-5 of the output's largest magnitude).
 //
-// Mapping onto v_mfma_f32_16x16x32_f16 (D = A * B + C, 16x16 output tile):
+// Mapping onto v_mfma_f32_16x16x32_f16 (D = A * B + C, 16x16 output tile;
+// lane l holds A[l % 16][8 (l / 16) .. +7], B[8 (l / 16) .. +7][l % 16],
+// D[4 (l / 16) .. +3][l % 16]):
 //   M (A rows)    = tokens, 16 per tile (padded with zero tokens);
 //   N (B columns) = weight rows, 16 per tile;
 //   K             = columns of one 128-weight block, 4 MFMA steps of 32.
-// The 2-bit codes become exact f16 values (code - 1) in {-1, 0, 1, 2}: the
-// code lands in the mantissa of 1024.0 (bit pattern 0x6400 | code << p) and
-// one packed f16 FMA maps 1024 + code * 2^p to code - 1 exactly.  The x side
-// needs more than f16's 11 bits for a 1e-5 result, so every x value is
-// scaled by a per-token power of two (largest |x| of the token in
-// [2^14, 2^15)) and split into hi = f16(x') and lo = f16(x' - hi): hi + lo
-// carries 22 significant bits, and two MFMAs (hi, lo) per weight tile
-// accumulate it in f32.  Each block's f32 tile sum is then multiplied by
-// the block's f32 scale and added to the row total, as the reference does;
-// the power of two is removed at the end (exact).
-//
-// K order: the MFMA sums its 32 k-slots in any order, so lanes may take
-// them in whatever order the codes unpack fastest; the A fragments are
-// written in that same order by the prepare kernel (mm_column()).
+// The 2-bit codes become exact f16 values (code - 1) in {-1, 0, 1, 2}
+// through a 256-entry LDS table (one code byte -> four halves), so a lane's
+// B fragment is two table reads.  The x side needs more than f16's 11 bits
+// for a 1e-5 result, so each (token, 128-block) of x is scaled by a power of
+// two (its largest |x| in [2^14, 2^15)) and split into hi = f16(x') and
+// lo = f16(x' - hi): hi + lo carries 22 significant bits, and two MFMAs (hi,
+// lo) per weight tile accumulate it in f32.  Each block's f32 tile sum is
+// then multiplied by the block's f32 scale times 2^-e (exact) and added to
+// the row total, as the reference adds scale * block_sum.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -43,13 +40,20 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// Block column (0..127) of element e (= 2j + h) of lane group g's A/B
-// fragment in MFMA step i (0..3) of a block.  Lane group g owns code bytes
-// [8g, 8g + 8) of the block, i.e. columns [32g, 32g + 32); step i uses the
-// dword of code bytes 8g + 4(i >> 1) .. +3; half h of pair j takes code j of
-// byte 2h + (i & 1) of that dword.
-__host__ __device__ constexpr int mm_column(int i, int g, int j, int h) {
-  return 32 * g + 16 * (i >> 1) + 4 * (2 * h + (i & 1)) + j;
+// Block column (0..127) of element e (0..7) of lane group g's A/B fragment
+// in MFMA step i (0..3) of a block: lane group g owns code bytes [8g, 8g + 8)
+// of the block, step i takes bytes 8g + 2i and 8g + 2i + 1, i.e. the eight
+// consecutive columns 32g + 8i .. +7 in their natural order.
+#ifndef MM_DEC
+#define MM_DEC 2
+#endif
+// MM_DEC 0 (bit select): element e = 2j + h is code j of byte 2h + (i & 1)
+// of the step's code dword; 1 (table): 8 consecutive columns; 2 (fp4
+// convert): element e is code 2 (e & 1) + (i & 1) of byte e >> 1.
+__host__ __device__ constexpr int mm_column(int i, int g, int e) {
+  return MM_DEC == 1   ? 32 * g + 8 * i + e
+         : MM_DEC == 0 ? 32 * g + 16 * (i >> 1) + 4 * (2 * (e & 1) + (i & 1)) + (e >> 1)
+                       : 32 * g + 16 * (i >> 1) + 4 * (e >> 1) + 2 * (e & 1) + (i & 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -59,7 +63,8 @@ __host__ __device__ constexpr int mm_column(int i, int g, int j, int h) {
 // back out in the product kernel's per-block f32 step (exact).
 //   afrag: [tile][kstep][piece (hi, lo)][64 lanes] x 16 bytes, written only
 //          for real tokens (the product kernel zero-fills the others);
-//   binv:  [tile][block][lane group g] float4 = 2^-e of tokens 4g .. 4g+3.
+//   binv:  [tile][block][lane group g] two float4: 2^-e and sum(hi + lo) of
+//          tokens 4g .. 4g+3.
 // ---------------------------------------------------------------------------
 struct PrepArgs {
   const float *x;  // [n_tok][ne0]
@@ -68,54 +73,57 @@ struct PrepArgs {
   int ne0, n_tok, nblk, n_ksteps;
 };
 
-// One lane per (token, block): 128 columns, one max, 32 fragment halves.
+// 16 consecutive lanes per (token, block); lane (i, g) builds the hi/lo
+// fragments of MFMA step i, lane group g (8 columns).  The block's largest
+// |x| and its sum of hi + lo are reduced across the 16 lanes.
 __global__ __launch_bounds__(kMmThreads) void pq2_mm_prep_kernel(PrepArgs a) {
   const int item = blockIdx.x * kMmThreads + threadIdx.x;
-  if (item >= a.n_tok * a.nblk) return;
-  const int m = item / a.nblk, blk = item - m * a.nblk;
-  const float4 *xr = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(m) * a.ne0 + 128 * blk);
-  float4 v[32];
+  const int mb = item >> 4, sub = item & 15;  // the 16 lanes of a group share mb
+  const bool live = mb < a.n_tok * a.nblk;
+  const int m = live ? mb / a.nblk : 0, blk = live ? mb - m * a.nblk : 0;
+  const int i = sub >> 2, g = sub & 3;
+  const float *xr = a.x + static_cast<size_t>(m) * a.ne0 + 128 * blk;
+  float f[8];
   float mx = 0.0f;
 #pragma unroll
-  for (int c = 0; c < 32; ++c) {
-    v[c] = xr[c];
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[c].x), fabsf(v[c].y)), fmaxf(fabsf(v[c].z), fabsf(v[c].w))));
+  for (int e = 0; e < 8; ++e) {
+    f[e] = live ? xr[mm_column(i, g, e)] : 0.0f;
+    mx = fmaxf(mx, fabsf(f[e]));  // NaN is ignored
   }
-  int e = 0;  // NaN is ignored by fmaxf; an all-zero or non-finite block keeps 2^0
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  int ex = 0;  // an all-zero or non-finite block keeps 2^0
   if (mx > 0.0f && mx <= 3.4e38f) {
     int k;
     (void)frexpf(mx, &k);  // mx = f * 2^k, f in [0.5, 1): mx * 2^(15-k) in [2^14, 2^15)
-    e = 15 - k;
-    e = e < -126 ? -126 : (e > 126 ? 126 : e);  // 2^e and 2^-e stay normal f32
+    ex = 15 - k;
+    ex = ex < -126 ? -126 : (ex > 126 ? 126 : ex);  // 2^e and 2^-e stay normal f32
   }
-  const float s = ldexpf(1.0f, e);
+  const float s = ldexpf(1.0f, ex);
+  h8 hi, lo;
+  float bsum = 0.0f;  // sum of hi + lo over the block (the "- 1" of the fp4 decode)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = f[e] * s;
+    const _Float16 hv = static_cast<_Float16>(v);
+    hi[e] = hv;
+    // an infinite x keeps lo = 0 (inf - inf would turn the term into NaN)
+    lo[e] = __builtin_isinf(static_cast<float>(hv)) ? static_cast<_Float16>(0.0f)
+                                                   : static_cast<_Float16>(v - static_cast<float>(hv));
+    bsum += static_cast<float>(hi[e]) + static_cast<float>(lo[e]);
+  }
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) bsum += __shfl_xor(bsum, off, 64);
+  if (!live) return;
   const int tile = m >> 4, ml = m & 15;
-  a.binv[((static_cast<size_t>(tile) * a.nblk + blk) * 4 + (ml >> 2)) * 4 + (ml & 3)] = ldexpf(1.0f, -e);
-  uint4 *frag = a.afrag + static_cast<size_t>(tile) * a.n_ksteps * 2 * 64;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      h8 hi, lo;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        // columns mm_column(i, g, j, h), j = 0..3: float4 number c
-        const float4 q = v[8 * g + 4 * (i >> 1) + 2 * h + (i & 1)];
-        const float f[4] = {q.x * s, q.y * s, q.z * s, q.w * s};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const _Float16 hv = static_cast<_Float16>(f[j]);
-          hi[2 * j + h] = hv;
-          // an infinite x keeps lo = 0 (inf - inf would turn the term into NaN)
-          lo[2 * j + h] = __builtin_isinf(static_cast<float>(hv))
-                              ? static_cast<_Float16>(0.0f)
-                              : static_cast<_Float16>(f[j] - static_cast<float>(hv));
-        }
-      }
-      uint4 *dst = frag + static_cast<size_t>(4 * blk + i) * 2 * 64 + 16 * g + ml;
-      dst[0] = __builtin_bit_cast(uint4, hi);
-      dst[64] = __builtin_bit_cast(uint4, lo);
-    }
+  uint4 *dst = a.afrag + (static_cast<size_t>(tile) * a.n_ksteps + 4 * blk + i) * 2 * 64 + 16 * g + ml;
+  dst[0] = __builtin_bit_cast(uint4, hi);
+  dst[64] = __builtin_bit_cast(uint4, lo);
+  if (sub == 0) {
+    // block factors: [tile][block][token group][inv, sum] x float4 (token & 3)
+    float *bx = a.binv + (((static_cast<size_t>(tile) * a.nblk + blk) * 4 + (ml >> 2)) * 2) * 4 + (ml & 3);
+    bx[0] = ldexpf(1.0f, -ex);
+    bx[4] = bsum;
   }
 }
 
@@ -139,6 +147,15 @@ struct MmArgs {
   int n_rows, nblk, n_ksteps, n_tok, y_stride;
 };
 
+// Code-byte table: entry b holds the f16 values (code - 1) of the four codes
+// of byte b (LSB first), exact small integers; 256 x 8 bytes in LDS.
+__device__ __forceinline__ void fill_code_lut(uint2 *lut) {
+  constexpr uint32_t kF16[4] = {0xBC00u, 0x0000u, 0x3C00u, 0x4000u};  // -1, 0, 1, 2
+  for (int b = threadIdx.x; b < 256; b += blockDim.x)
+    lut[b] = make_uint2(kF16[b & 3] | (kF16[(b >> 2) & 3] << 16),
+                        kF16[(b >> 4) & 3] | (kF16[(b >> 6) & 3] << 16));
+}
+
 // (t & mask) | (b & ~mask) in one instruction (gfx9's three-operand
 // encodings take no literal, so the compiler would split it in two).
 __device__ __forceinline__ uint32_t bit_select(uint32_t mask, uint32_t t, uint32_t b) {
@@ -148,23 +165,45 @@ __device__ __forceinline__ uint32_t bit_select(uint32_t mask, uint32_t t, uint32
 }
 
 // f16 pairs (code_lo - 1, code_hi - 1) of the codes at bits (2j, 2j + 16)
-// of t, for j = 0..3, as the 8 halves of a B fragment.  `magic` holds
-// 0x64006400 (1024.0 in both halves, no bits in the code positions).
-__device__ __forceinline__ h8 decode_codes(uint32_t t, uint32_t magic) {
+// of t, for j = 0..3: the code lands in the mantissa of 1024.0 (0x6400 |
+// code << 2j) and one packed FMA maps 1024 + code * 4^j to code - 1, exactly.
+__device__ __forceinline__ h8 decode_bits(uint32_t t) {
+  const uint32_t magic = 0x64006400u;  // no bits in the code positions
   h8 r;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t mask = (3u << (2 * j)) | (3u << (2 * j + 16));
-    const uint32_t bits = bit_select(mask, t, magic);  // 1024 + code * 2^(2j), exact
-    const h2 v = __builtin_bit_cast(h2, bits);
+    const h2 v = __builtin_bit_cast(h2, bit_select(mask, t, magic));
     const _Float16 k = static_cast<_Float16>(1.0f / static_cast<float>(1 << (2 * j)));
     const _Float16 c = static_cast<_Float16>(-(1024.0f / static_cast<float>(1 << (2 * j)) + 1.0f));
     const h2 kk = {k, k}, cc = {c, c};
-    const h2 w = __builtin_elementwise_fma(v, kk, cc);  // exact: a small integer
+    const h2 w = __builtin_elementwise_fma(v, kk, cc);
     r[2 * j] = w[0];
     r[2 * j + 1] = w[1];
   }
   return r;
+}
+
+// B fragment of step i from its code dword d as the codes themselves (0..3,
+// exact f16): a 2-bit code in the low bits of a nibble reads as the FP4
+// (e2m1) value code / 2, so with the codes spread one per nibble a packed
+// FP4 -> f16 conversion scaled by 2 yields two codes per instruction.  The
+// missing "- 1" of (code - 1) is applied per block as - sum(x).
+__device__ __forceinline__ h8 decode_fp4(uint32_t d, int i) {
+  const uint32_t t = (i & 1) ? ((d >> 2) & 0x33333333u) : (d & 0x33333333u);
+  const h2 p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(t, 2.0f, 0);
+  const h2 p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(t, 2.0f, 1);
+  const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(t, 2.0f, 2);
+  const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(t, 2.0f, 3);
+  return h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// B fragment of bytes k0 and k0 + 1 of the code dword d: 8 halves, columns
+// in order (the layout mm_column() gives the A side).
+__device__ __forceinline__ h8 decode_lut(const uint2 *lut, uint32_t d, int k0) {
+  const uint2 lo = lut[(d >> (8 * k0)) & 0xffu];
+  const uint2 hi = lut[(d >> (8 * k0 + 8)) & 0xffu];
+  return __builtin_bit_cast(h8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
 struct PairData {
@@ -213,6 +252,8 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
   // product is staged in LDS once, fragments [kstep][piece][token][lane
   // group] followed by the block factors [block][lane group]
   extern __shared__ uint4 a_lds[];
+  __shared__ uint2 code_lut[256];
+  fill_code_lut(code_lut);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int row_wave = blockIdx.x * (4 * 16 * NT) + wave * 16 * NT;
@@ -229,7 +270,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
   // tile's absent tokens may feed any fragment (their rows are never
   // stored): they read a real token's (ALDS) or unwritten scratch.
   const uint4 *af = a.afrag + static_cast<size_t>(tile0) * a.n_ksteps * 2 * 64 + lane;
-  const float4 *binv_g = a.binv + static_cast<size_t>(tile0) * a.nblk * 4 + g;
+  const float4 *binv_g = a.binv + (static_cast<size_t>(tile0) * a.nblk * 4 + g) * 2;
   const uint4 *al = a_lds;
   const float4 *binv_l = nullptr;
   int lds_tok_stride = 0;
@@ -242,13 +283,12 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
       a_lds[i] = a.afrag[static_cast<size_t>(kp) * 64 + 16 * gq + m];
     }
     float4 *bl = reinterpret_cast<float4 *>(a_lds + total);
-    for (int i = threadIdx.x; i < a.nblk * 4; i += kMmThreads) bl[i] = a.binv[i];
-    __syncthreads();
+    for (int i = threadIdx.x; i < a.nblk * 8; i += kMmThreads) bl[i] = a.binv[i];
     al = a_lds + (n < nt ? n : 0) * 4 + g;
     lds_tok_stride = nt * 4;
-    binv_l = bl + g;
+    binv_l = bl + 2 * g;
   }
-  const uint32_t magic = 0x64006400u;
+  __syncthreads();  // code table (and x staging) visible to every wave
 
   f4v tot[MT][NT];
 #pragma unroll
@@ -257,11 +297,11 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
     for (int t = 0; t < NT; ++t) tot[mt][t] = f4v{0.f, 0.f, 0.f, 0.f};
 
   auto do_block = [&](const BlockCodes(&bc)[NT], int b) {
-    f4v acc[MT][NT];
+    f4v acc[MT][NT], acc_lo[MT][NT];  // hi and lo pieces: two independent MFMA chains
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) acc[mt][t] = f4v{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < NT; ++t) acc[mt][t] = acc_lo[mt][t] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ks = 4 * b + i;
@@ -281,31 +321,43 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const uint32_t d = bc[t].cd[i >> 1];
-        const h8 bf = decode_codes((i & 1) ? (d >> 8) : d, magic);
+        const h8 bf = MM_DEC == 2 ? decode_fp4(d, i)
+                      : MM_DEC == 1 ? decode_lut(code_lut, d, 2 * (i & 1))
+                                    : decode_bits((i & 1) ? (d >> 8) : d);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[mt], bf, acc[mt][t], 0, 0, 0);
-          acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[mt], bf, acc[mt][t], 0, 0, 0);
+          acc_lo[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[mt], bf, acc_lo[mt][t], 0, 0, 0);
         }
       }
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[mt][t][q] = acc[mt][t][q] + acc_lo[mt][t][q];
     // src/kernels.rs:651: acc += scale * block_acc -- block_acc arrives
     // multiplied by the block's 2^e, so the factor is scale * 2^-e (exact)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      float4 bi;
+      float4 bi, bs;
       if constexpr (ALDS) {
-        bi = binv_l[b * 4];
+        bi = binv_l[b * 8];
+        bs = binv_l[b * 8 + 1];
       } else {
-        bi = binv_g[(static_cast<size_t>(mt) * a.nblk + b) * 4];
+        bi = binv_g[(static_cast<size_t>(mt) * a.nblk + b) * 8];
+        bs = binv_g[(static_cast<size_t>(mt) * a.nblk + b) * 8 + 1];
       }
       const float inv[4] = {bi.x, bi.y, bi.z, bi.w};
+      const float xs[4] = {bs.x, bs.y, bs.z, bs.w};
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float f = bc[t].sc * inv[q];
-          const float prod = f * acc[mt][t][q];
+          const float blk = MM_DEC == 2 ? acc[mt][t][q] - xs[q] : acc[mt][t][q];
+          const float prod = f * blk;
           tot[mt][t][q] = tot[mt][t][q] + prod;
         }
       }
@@ -355,6 +407,174 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Staged product (16-byte aligned rows, block count a multiple of 8): each
+// wave streams its 16 rows through LDS in chunks of 8 blocks (272 bytes per
+// row, 17 dwordx4 loads per row, so consecutive lanes read consecutive 16
+// bytes of a row), then every lane reads its fragment codes from LDS.  One
+// chunk is in flight in registers while the previous one is consumed; the
+// stage is private to the wave (in-order LDS, no block barrier).
+// ---------------------------------------------------------------------------
+constexpr int kStageBlocks = 8;
+constexpr int kStageRowBytes = kPq2Blk * kStageBlocks;          // 272
+constexpr int kStageStride = 280;  // LDS bytes per staged row: 8-aligned, spreads the banks
+constexpr int kStageF4 = kStageRowBytes / 16;                   // 17
+constexpr int kStageLoads = (16 * kStageF4 + 63) / 64;          // 5 per lane
+constexpr size_t kStageWaveBytes = 16 * kStageStride;           // 4480
+
+__device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) {
+  return *reinterpret_cast<const uint32_t *>(p);
+}
+
+// TOKQ: accumulator elements per lane that can hold a real token (the tile
+// has at most 4 * TOKQ ... lanes of groups g >= 1 hold tokens >= 4, so with
+// n_tok <= TOKQ only elements q < TOKQ of group 0 carry results).
+template <bool ALDS, int TOKQ>
+__global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
+  extern __shared__ uint4 smem[];
+  __shared__ uint2 code_lut[256];
+  fill_code_lut(code_lut);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int row_wave = blockIdx.x * 64 + wave * 16;
+
+  // x side: whole product in LDS (ALDS) or fragments from global
+  const uint4 *af = a.afrag + lane;
+  const uint4 *al = smem;
+  const float4 *binv_l = nullptr;
+  int lds_tok_stride = 0;
+  size_t a_words = 0;  // uint4 slots used by the ALDS area
+  if constexpr (ALDS) {
+    const int nt = a.n_tok;
+    const int total = a.n_ksteps * 2 * nt * 4;
+    for (int i = threadIdx.x; i < total; i += kMmThreads) {
+      const int gq = i & 3, rest = i >> 2;
+      const int m = rest % nt, kp = rest / nt;
+      smem[i] = a.afrag[static_cast<size_t>(kp) * 64 + 16 * gq + m];
+    }
+    float4 *bl = reinterpret_cast<float4 *>(smem + total);
+    for (int i = threadIdx.x; i < a.nblk * 8; i += kMmThreads) bl[i] = a.binv[i];
+    al = smem + (n < nt ? n : 0) * 4 + g;
+    lds_tok_stride = nt * 4;
+    binv_l = bl + 2 * g;
+    a_words = static_cast<size_t>(total) + static_cast<size_t>(a.nblk) * 8;
+  }
+  uint8_t *stage = reinterpret_cast<uint8_t *>(smem + a_words) + wave * kStageWaveBytes;
+
+  // this lane's share of a chunk: float4 slot k covers row r_k, piece c_k
+  const uint8_t *src[kStageLoads];
+  int dst[kStageLoads];
+  bool live[kStageLoads];
+#pragma unroll
+  for (int k = 0; k < kStageLoads; ++k) {
+    const int idx = lane + 64 * k;
+    live[k] = idx < 16 * kStageF4;
+    const int r = live[k] ? idx / kStageF4 : 0, c16 = live[k] ? idx % kStageF4 : 0;
+    int row = row_wave + r;
+    row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
+    src[k] = a.w + static_cast<size_t>(row) * a.row_bytes + 16 * c16;
+    dst[k] = r * kStageStride + 16 * c16;
+  }
+  uint4 regs[kStageLoads];
+  auto gload = [&](int chunk) {
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k)
+      if (live[k]) regs[k] = *reinterpret_cast<const uint4 *>(src[k] + static_cast<size_t>(chunk) * kStageRowBytes);
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k) {
+      if (live[k]) {
+        uint2 *d = reinterpret_cast<uint2 *>(stage + dst[k]);  // 8-byte aligned
+        d[0] = make_uint2(regs[k].x, regs[k].y);
+        d[1] = make_uint2(regs[k].z, regs[k].w);
+      }
+    }
+  };
+  f4v tot = f4v{0.f, 0.f, 0.f, 0.f};
+
+  const int n_chunks = a.nblk / kStageBlocks;
+  gload(0);
+  __syncthreads();  // code table (and x staging) visible to every wave
+  lstore();
+  if (n_chunks > 1) gload(1);
+  for (int c = 0; c < n_chunks; ++c) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint8_t *rowp = stage + n * kStageStride;
+#pragma unroll 2
+    for (int bb = 0; bb < kStageBlocks; ++bb) {
+      const int b = c * kStageBlocks + bb;
+      const uint8_t *blk = rowp + kPq2Blk * bb;
+      BlockCodes bc;
+      if ((bb & 1) == 0) {  // block starts on a dword: codes are 2 bytes in
+        const uint32_t e0 = lds_u32(blk + 8 * g), e1 = lds_u32(blk + 8 * g + 4),
+                       e2 = lds_u32(blk + 8 * g + 8);
+        bc.cd[0] = __builtin_amdgcn_alignbyte(e1, e0, 2);
+        bc.cd[1] = __builtin_amdgcn_alignbyte(e2, e1, 2);
+        bc.sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk))));
+      } else {  // block starts 2 bytes into a dword: codes are dword-aligned
+        bc.cd[0] = lds_u32(blk + 2 + 8 * g);
+        bc.cd[1] = lds_u32(blk + 6 + 8 * g);
+        bc.sc = static_cast<float>(
+            __builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk - 2) >> 16)));
+      }
+      f4v acc = f4v{0.f, 0.f, 0.f, 0.f}, acc_lo = acc;  // two independent MFMA chains
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ks = 4 * b + i;
+        h8 ahi, alo;
+        if constexpr (ALDS) {
+          const uint4 *pl = al + (2 * ks) * lds_tok_stride;
+          ahi = __builtin_bit_cast(h8, pl[0]);
+          alo = __builtin_bit_cast(h8, pl[lds_tok_stride]);
+        } else {
+          const uint4 *pg = af + static_cast<size_t>(ks) * 2 * 64;
+          ahi = __builtin_bit_cast(h8, pg[0]);
+          alo = __builtin_bit_cast(h8, pg[64]);
+        }
+        const uint32_t d = bc.cd[i >> 1];
+        const h8 bf = MM_DEC == 2 ? decode_fp4(d, i)
+                      : MM_DEC == 1 ? decode_lut(code_lut, d, 2 * (i & 1))
+                                    : decode_bits((i & 1) ? (d >> 8) : d);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc, 0, 0, 0);
+        acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc_lo, 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < TOKQ; ++q) acc[q] = acc[q] + acc_lo[q];
+      float4 bi, bs;
+      if constexpr (ALDS) {
+        bi = binv_l[b * 8];
+        bs = binv_l[b * 8 + 1];
+      } else {
+        bi = a.binv[(static_cast<size_t>(b) * 4 + g) * 2];
+        bs = a.binv[(static_cast<size_t>(b) * 4 + g) * 2 + 1];
+      }
+      const float inv[4] = {bi.x, bi.y, bi.z, bi.w};
+      const float xs[4] = {bs.x, bs.y, bs.z, bs.w};
+#pragma unroll
+      for (int q = 0; q < TOKQ; ++q) {
+        const float f = bc.sc * inv[q];  // src/kernels.rs:651, block scale * 2^-e
+        const float blk = MM_DEC == 2 ? acc[q] - xs[q] : acc[q];
+        const float prod = f * blk;
+        tot[q] = tot[q] + prod;
+      }
+    }
+    if (c + 1 < n_chunks) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      lstore();  // chunk c + 1 replaces chunk c (this wave finished reading it)
+      if (c + 2 < n_chunks) gload(c + 2);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < TOKQ; ++q) {
+    const int m = 4 * g + q;
+    const int row = row_wave + n;
+    if (m < a.n_tok && row < a.n_rows) a.y[static_cast<size_t>(m) * a.y_stride + row] = tot[q];
+  }
+}
+
 // Any ne0 or alignment: the scalar reference loop (src/kernels.rs:633-653),
 // one wave per (row, token), lanes over blocks, block sums in order, then a
 // fixed-order reduction of the lanes' scale * block_sum terms.
@@ -391,7 +611,7 @@ __global__ void fill_zero_kernel(float *y, size_t n) {
 }
 
 constexpr int kLdsTok = 4;                 // token counts staged whole in LDS
-constexpr size_t kLdsABytes = 80 * 1024;   // their LDS budget
+constexpr size_t kLdsABytes = 104 * 1024;  // their LDS budget (with 4 wave stages: 121 KB)
 
 template <int MT, int NT, bool ALDS = false>
 int launch_mm(const MmArgs &a, int n_tiles, hipStream_t st) {
@@ -400,7 +620,7 @@ int launch_mm(const MmArgs &a, int n_tiles, hipStream_t st) {
   size_t lds = 0;
   if constexpr (ALDS) {
     lds = static_cast<size_t>(a.n_ksteps) * 2 * a.n_tok * 4 * sizeof(uint4) +
-          static_cast<size_t>(a.nblk) * 4 * sizeof(float4);
+          static_cast<size_t>(a.nblk) * 8 * sizeof(float4);
     if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_mm_kernel<MT, NT, true>),
                                               hipFuncAttributeMaxDynamicSharedMemorySize,
                                               static_cast<int>(kLdsABytes)),
@@ -408,6 +628,22 @@ int launch_mm(const MmArgs &a, int n_tiles, hipStream_t st) {
       return e;
   }
   BH_LAUNCH((pq2_mm_kernel<MT, NT, ALDS>), dim3(gx, gy), kMmThreads, lds, st, a);
+  return ok();
+}
+
+template <bool ALDS, int TOKQ>
+int launch_staged(const MmArgs &a, hipStream_t st) {
+  const unsigned gx = static_cast<unsigned>((a.n_rows + 63) / 64);
+  size_t lds = 4 * kStageWaveBytes;
+  if constexpr (ALDS)
+    lds += static_cast<size_t>(a.n_ksteps) * 2 * a.n_tok * 4 * sizeof(uint4) +
+           static_cast<size_t>(a.nblk) * 8 * sizeof(float4);
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_mm_staged_kernel<ALDS, TOKQ>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(kLdsABytes + 4 * kStageWaveBytes)),
+                        "hipFuncSetAttribute"))
+    return e;
+  BH_LAUNCH((pq2_mm_staged_kernel<ALDS, TOKQ>), gx, kMmThreads, lds, st, a);
   return ok();
 }
 
@@ -441,12 +677,12 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   // scratch: A fragments, then the per-(token, block) powers of two
   const size_t frag_bytes = static_cast<size_t>(tiles_padded) * n_ksteps * 2 * 64 * sizeof(uint4);
   const size_t binv_off = (frag_bytes + 255) / 256 * 256;
-  const size_t binv_bytes = static_cast<size_t>(tiles_padded) * nblk * 4 * sizeof(float4);
+  const size_t binv_bytes = static_cast<size_t>(tiles_padded) * nblk * 8 * sizeof(float4);
   char *scratch = static_cast<char *>(device_scratch(binv_off + binv_bytes, kScratchMatmul));
   if (scratch == nullptr) return BH_ERR_HIP;
   PrepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float *>(scratch + binv_off),
               static_cast<int>(ne0), static_cast<int>(n_tok), static_cast<int>(nblk), n_ksteps};
-  const size_t items = n_tok * nblk;
+  const size_t items = n_tok * nblk * 16;
   BH_LAUNCH(pq2_mm_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
             kMmThreads, 0, st, pa);
 
@@ -455,8 +691,14 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
            static_cast<int>(n_rows)};
   // a wave takes 4 row tiles when that still leaves >= 2 blocks per CU
   const bool wide = n_rows >= static_cast<size_t>(256) * 2 * 256;
+  const bool staged = nblk % kStageBlocks == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+                      row_bytes % 16 == 0 && n_tiles == 1;
   const bool a_in_lds = n_tok <= kLdsTok && static_cast<size_t>(n_ksteps) * 2 * n_tok * 4 * sizeof(uint4) +
-                                                 nblk * 4 * sizeof(float4) <= kLdsABytes;
+                                                 nblk * 8 * sizeof(float4) <= kLdsABytes;
+  if (staged) {
+    if (a_in_lds) return n_tok == 1 ? launch_staged<true, 1>(a, st) : launch_staged<true, 4>(a, st);
+    return launch_staged<false, 4>(a, st);
+  }
   if (a_in_lds)
     return wide ? launch_mm<1, 4, true>(a, n_tiles, st) : launch_mm<1, 1, true>(a, n_tiles, st);
   switch (mt) {
