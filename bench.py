@@ -348,6 +348,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline kernel (profiling runs)")
+    ap.add_argument("--only", default="",
+                    help="after the headline, time only the entries whose name contains this")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="length of the CPU-baseline sample (0 disables)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -386,35 +388,34 @@ def main() -> int:
         kernels = [head]
         if not args.headline_only:
             ksteps = max(10, args.steps // 4)
-            kernels += [
-                measure("rms_norm_rows T=512", wl_rms_rows(bh, synth, dev, stream, 512),
-                        ksteps, args.warmup, stream),
-                measure("rms_norm_rows T=2048", wl_rms_rows(bh, synth, dev, stream, 2048),
-                        ksteps, args.warmup, stream),
-                measure("rms_norm_rows T=8192", wl_rms_rows(bh, synth, dev, stream, 8192),
-                        ksteps, args.warmup, stream),
-                measure("gdn_prep_fused T=4096", wl_gdn_prep(bh, synth, dev, stream), ksteps,
-                        args.warmup, stream),
-                measure("softmax vocab [64,248320] temp 0.7",
-                        wl_softmax(bh, synth, dev, stream, 64, 248320,
-                                   float(1 / __import__("numpy").float32(0.7)), spikes=True),
-                        ksteps, args.warmup, stream),
-                measure("softmax causal [24*2048,2048]",
-                        wl_softmax(bh, synth, dev, stream, 24 * 2048, 2048, 1.0, causal=True),
-                        ksteps, args.warmup, stream),
-                measure("pq2_gather_rms T=8192", wl_gather_rms(bh, synth, dev, stream), ksteps,
-                        args.warmup, stream),
-                measure_mm("pq2_matvec LM head [248320x5120] N=1", 248320, 5120, 1, bh, synth,
-                           dev, stream, ksteps, args.warmup),
-                measure_mm("pq2_matvec ffn_up [17408x5120] N=1", 17408, 5120, 1, bh, synth,
-                           dev, stream, ksteps, args.warmup),
-                measure_mm("pq2_matvec ffn_down [5120x17408] N=1", 5120, 17408, 1, bh, synth,
-                           dev, stream, ksteps, args.warmup),
-                measure_mm("pq2_matmul_n ffn_up [17408x5120] N=64", 17408, 5120, 64, bh, synth,
-                           dev, stream, ksteps, args.warmup),
-                measure_mm("pq2_matmul_n LM head [248320x5120] N=16", 248320, 5120, 16, bh,
-                           synth, dev, stream, ksteps, args.warmup),
+            np32 = __import__("numpy").float32
+            rows_wl = {T: (lambda T=T: wl_rms_rows(bh, synth, dev, stream, T)) for T in (512, 2048, 8192)}
+            entries = [
+                ("rms_norm_rows T=512", rows_wl[512]),
+                ("rms_norm_rows T=2048", rows_wl[2048]),
+                ("rms_norm_rows T=8192", rows_wl[8192]),
+                ("gdn_prep_fused T=4096", lambda: wl_gdn_prep(bh, synth, dev, stream)),
+                ("softmax vocab [64,248320] temp 0.7",
+                 lambda: wl_softmax(bh, synth, dev, stream, 64, 248320, float(1 / np32(0.7)),
+                                    spikes=True)),
+                ("softmax causal [24*2048,2048]",
+                 lambda: wl_softmax(bh, synth, dev, stream, 24 * 2048, 2048, 1.0, causal=True)),
+                ("pq2_gather_rms T=8192", lambda: wl_gather_rms(bh, synth, dev, stream)),
             ]
+            products = [  # (name, rows, ne0, tokens): decode matvecs and batched products
+                ("pq2_matvec LM head [248320x5120] N=1", 248320, 5120, 1),
+                ("pq2_matvec ffn_up [17408x5120] N=1", 17408, 5120, 1),
+                ("pq2_matvec ffn_down [5120x17408] N=1", 5120, 17408, 1),
+                ("pq2_matmul_n ffn_up [17408x5120] N=64", 17408, 5120, 64),
+                ("pq2_matmul_n LM head [248320x5120] N=16", 248320, 5120, 16),
+            ]
+            for name, wl in entries:
+                if args.only in name:
+                    kernels.append(measure(name, wl(), ksteps, args.warmup, stream))
+            for name, rows, ne0, n_tok in products:
+                if args.only in name:
+                    kernels.append(measure_mm(name, rows, ne0, n_tok, bh, synth, dev, stream,
+                                              ksteps, args.warmup))
 
     cpu = None
     if args.cpu_seconds > 0:

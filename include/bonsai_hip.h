@@ -25,8 +25,9 @@
  * expf/logf/sinf/cosf, no FMA contraction.  The PQ2_0 decode is bit-exact.
  *
  * Threading: every device entry point is re-entrant per stream, except
- * bh_softmax_rows on rows too wide for one workgroup, which uses a per-device
- * scratch buffer and must not run concurrently with itself on one device.
+ * bh_softmax_rows on rows too wide for one workgroup and the PQ2_0 products
+ * (bh_pq2_matvec_range, bh_pq2_matmul_n), which use per-device scratch
+ * buffers: each must not run concurrently with itself on one device.
  */
 #ifndef BONSAI_HIP_H
 #define BONSAI_HIP_H

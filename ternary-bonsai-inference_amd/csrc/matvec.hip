@@ -16,15 +16,18 @@
 //   M (A rows)    = tokens, 16 per tile (padded with zero tokens);
 //   N (B columns) = weight rows, 16 per tile;
 //   K             = columns of one 128-weight block, 4 MFMA steps of 32.
-// The 2-bit codes become exact f16 values (code - 1) in {-1, 0, 1, 2}
-// through a 256-entry LDS table (one code byte -> four halves), so a lane's
-// B fragment is two table reads.  The x side needs more than f16's 11 bits
-// for a 1e-5 result, so each (token, 128-block) of x is scaled by a power of
-// two (its largest |x| in [2^14, 2^15)) and split into hi = f16(x') and
-// lo = f16(x' - hi): hi + lo carries 22 significant bits, and two MFMAs (hi,
-// lo) per weight tile accumulate it in f32.  Each block's f32 tile sum is
-// then multiplied by the block's f32 scale times 2^-e (exact) and added to
-// the row total, as the reference adds scale * block_sum.
+// B fragments hold the codes themselves (0..3, exact in f16): a 2-bit code
+// in the low bits of a nibble reads as the FP4 (e2m1) value code / 2, so
+// with the codes spread one per nibble one packed FP4 -> f16 conversion
+// (scale 2) decodes two weights; sum(x * (code - 1)) is then the MFMA's
+// sum(x * code) minus the block's sum(x), precomputed per (token, block).
+// The x side needs more than f16's 11 bits for a 1e-5 result, so each
+// (token, 128-block) of x is scaled by a power of two (its largest |x| in
+// [2^14, 2^15)) and split into hi = f16(x') and lo = f16(x' - hi): hi + lo
+// carries 22 significant bits, and two MFMAs (hi, lo) per weight tile
+// accumulate it in f32.  Each block's f32 tile sum is then multiplied by the
+// block's f32 scale times 2^-e (exact) and added to the row total, as the
+// reference adds scale * block_sum.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -41,19 +44,13 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 // Block column (0..127) of element e (0..7) of lane group g's A/B fragment
-// in MFMA step i (0..3) of a block: lane group g owns code bytes [8g, 8g + 8)
-// of the block, step i takes bytes 8g + 2i and 8g + 2i + 1, i.e. the eight
-// consecutive columns 32g + 8i .. +7 in their natural order.
-#ifndef MM_DEC
-#define MM_DEC 2
-#endif
-// MM_DEC 0 (bit select): element e = 2j + h is code j of byte 2h + (i & 1)
-// of the step's code dword; 1 (table): 8 consecutive columns; 2 (fp4
-// convert): element e is code 2 (e & 1) + (i & 1) of byte e >> 1.
+// in MFMA step i (0..3) of a block.  Lane group g owns code bytes [8g, 8g+8)
+// of the block (columns [32g, 32g + 32)); step i uses the dword of code bytes
+// 8g + 4 (i >> 1) .. +3, spread one code per nibble (the codes of parity
+// i & 1), and element e is code 2 (e & 1) + (i & 1) of byte e >> 1.  The MFMA
+// sums its k-slots in any order, so only A and B have to agree.
 __host__ __device__ constexpr int mm_column(int i, int g, int e) {
-  return MM_DEC == 1   ? 32 * g + 8 * i + e
-         : MM_DEC == 0 ? 32 * g + 16 * (i >> 1) + 4 * (2 * (e & 1) + (i & 1)) + (e >> 1)
-                       : 32 * g + 16 * (i >> 1) + 4 * (e >> 1) + 2 * (e & 1) + (i & 1);
+  return 32 * g + 16 * (i >> 1) + 4 * (e >> 1) + 2 * (e & 1) + (i & 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -62,7 +59,8 @@ __host__ __device__ constexpr int mm_column(int i, int g, int e) {
 // never overflows f16 and lo keeps 11 more bits.  The power of two comes
 // back out in the product kernel's per-block f32 step (exact).
 //   afrag: [tile][kstep][piece (hi, lo)][64 lanes] x 16 bytes, written only
-//          for real tokens (the product kernel zero-fills the others);
+//          for real tokens (the lanes of absent tokens feed rows that are
+//          never stored);
 //   binv:  [tile][block][lane group g] two float4: 2^-e and sum(hi + lo) of
 //          tokens 4g .. 4g+3.
 // ---------------------------------------------------------------------------
@@ -147,43 +145,6 @@ struct MmArgs {
   int n_rows, nblk, n_ksteps, n_tok, y_stride;
 };
 
-// Code-byte table: entry b holds the f16 values (code - 1) of the four codes
-// of byte b (LSB first), exact small integers; 256 x 8 bytes in LDS.
-__device__ __forceinline__ void fill_code_lut(uint2 *lut) {
-  constexpr uint32_t kF16[4] = {0xBC00u, 0x0000u, 0x3C00u, 0x4000u};  // -1, 0, 1, 2
-  for (int b = threadIdx.x; b < 256; b += blockDim.x)
-    lut[b] = make_uint2(kF16[b & 3] | (kF16[(b >> 2) & 3] << 16),
-                        kF16[(b >> 4) & 3] | (kF16[(b >> 6) & 3] << 16));
-}
-
-// (t & mask) | (b & ~mask) in one instruction (gfx9's three-operand
-// encodings take no literal, so the compiler would split it in two).
-__device__ __forceinline__ uint32_t bit_select(uint32_t mask, uint32_t t, uint32_t b) {
-  uint32_t r;
-  __asm__("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(t), "v"(b));
-  return r;
-}
-
-// f16 pairs (code_lo - 1, code_hi - 1) of the codes at bits (2j, 2j + 16)
-// of t, for j = 0..3: the code lands in the mantissa of 1024.0 (0x6400 |
-// code << 2j) and one packed FMA maps 1024 + code * 4^j to code - 1, exactly.
-__device__ __forceinline__ h8 decode_bits(uint32_t t) {
-  const uint32_t magic = 0x64006400u;  // no bits in the code positions
-  h8 r;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t mask = (3u << (2 * j)) | (3u << (2 * j + 16));
-    const h2 v = __builtin_bit_cast(h2, bit_select(mask, t, magic));
-    const _Float16 k = static_cast<_Float16>(1.0f / static_cast<float>(1 << (2 * j)));
-    const _Float16 c = static_cast<_Float16>(-(1024.0f / static_cast<float>(1 << (2 * j)) + 1.0f));
-    const h2 kk = {k, k}, cc = {c, c};
-    const h2 w = __builtin_elementwise_fma(v, kk, cc);
-    r[2 * j] = w[0];
-    r[2 * j + 1] = w[1];
-  }
-  return r;
-}
-
 // B fragment of step i from its code dword d as the codes themselves (0..3,
 // exact f16): a 2-bit code in the low bits of a nibble reads as the FP4
 // (e2m1) value code / 2, so with the codes spread one per nibble a packed
@@ -196,14 +157,6 @@ __device__ __forceinline__ h8 decode_fp4(uint32_t d, int i) {
   const h2 p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(t, 2.0f, 2);
   const h2 p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(t, 2.0f, 3);
   return h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-}
-
-// B fragment of bytes k0 and k0 + 1 of the code dword d: 8 halves, columns
-// in order (the layout mm_column() gives the A side).
-__device__ __forceinline__ h8 decode_lut(const uint2 *lut, uint32_t d, int k0) {
-  const uint2 lo = lut[(d >> (8 * k0)) & 0xffu];
-  const uint2 hi = lut[(d >> (8 * k0 + 8)) & 0xffu];
-  return __builtin_bit_cast(h8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
 struct PairData {
@@ -252,8 +205,6 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
   // product is staged in LDS once, fragments [kstep][piece][token][lane
   // group] followed by the block factors [block][lane group]
   extern __shared__ uint4 a_lds[];
-  __shared__ uint2 code_lut[256];
-  fill_code_lut(code_lut);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int row_wave = blockIdx.x * (4 * 16 * NT) + wave * 16 * NT;
@@ -288,7 +239,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
     lds_tok_stride = nt * 4;
     binv_l = bl + 2 * g;
   }
-  __syncthreads();  // code table (and x staging) visible to every wave
+  if constexpr (ALDS) __syncthreads();  // x staging visible to every wave
 
   f4v tot[MT][NT];
 #pragma unroll
@@ -321,9 +272,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const uint32_t d = bc[t].cd[i >> 1];
-        const h8 bf = MM_DEC == 2 ? decode_fp4(d, i)
-                      : MM_DEC == 1 ? decode_lut(code_lut, d, 2 * (i & 1))
-                                    : decode_bits((i & 1) ? (d >> 8) : d);
+        const h8 bf = decode_fp4(d, i);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[mt], bf, acc[mt][t], 0, 0, 0);
@@ -356,7 +305,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_kernel(MmArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float f = bc[t].sc * inv[q];
-          const float blk = MM_DEC == 2 ? acc[mt][t][q] - xs[q] : acc[mt][t][q];
+          const float blk = acc[mt][t][q] - xs[q];
           const float prod = f * blk;
           tot[mt][t][q] = tot[mt][t][q] + prod;
         }
@@ -432,8 +381,6 @@ __device__ __forceinline__ uint32_t lds_u32(const uint8_t *p) {
 template <bool ALDS, int TOKQ>
 __global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
   extern __shared__ uint4 smem[];
-  __shared__ uint2 code_lut[256];
-  fill_code_lut(code_lut);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int row_wave = blockIdx.x * 64 + wave * 16;
@@ -495,7 +442,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
 
   const int n_chunks = a.nblk / kStageBlocks;
   gload(0);
-  __syncthreads();  // code table (and x staging) visible to every wave
+  if constexpr (ALDS) __syncthreads();  // x staging visible to every wave
   lstore();
   if (n_chunks > 1) gload(1);
   for (int c = 0; c < n_chunks; ++c) {
@@ -534,9 +481,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
           alo = __builtin_bit_cast(h8, pg[64]);
         }
         const uint32_t d = bc.cd[i >> 1];
-        const h8 bf = MM_DEC == 2 ? decode_fp4(d, i)
-                      : MM_DEC == 1 ? decode_lut(code_lut, d, 2 * (i & 1))
-                                    : decode_bits((i & 1) ? (d >> 8) : d);
+        const h8 bf = decode_fp4(d, i);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bf, acc, 0, 0, 0);
         acc_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bf, acc_lo, 0, 0, 0);
       }
@@ -555,7 +500,7 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
 #pragma unroll
       for (int q = 0; q < TOKQ; ++q) {
         const float f = bc.sc * inv[q];  // src/kernels.rs:651, block scale * 2^-e
-        const float blk = MM_DEC == 2 ? acc[q] - xs[q] : acc[q];
+        const float blk = acc[q] - xs[q];
         const float prod = f * blk;
         tot[q] = tot[q] + prod;
       }
