@@ -128,13 +128,19 @@ def wl_rms_rows(bh, synth, dev, stream, rows=512, row_len=5120):
     return launch, len(sets), bytes_per, rows, (sets, w)
 
 
-def wl_gdn_prep(bh, synth, dev, stream, n_tok=4096):
+def wl_gdn_prep(bh, synth, dev, stream, n_tok=4096, with_conv=False):
+    """Config 3; with with_conv the causal conv1d (k = 4) runs in front, from
+    the raw qkv and the cache (src/forward.rs:508-533): the same row bytes
+    plus the taps and the cache read and written."""
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(2)
-    C, H = 6144, 48
+    C, H, K = 6144, 48, 4
     bytes_per = (n_tok * C * 4 * 2 + n_tok * H * 4 * 2 + 2 * H * 4 + n_tok * H * 4 * 2
                  + n_tok * C * 4 * 3)
+    if with_conv:
+        bytes_per += C * K * 4 + 2 * C * (K - 1) * 4
+    taps = 0.5 * torch.randn((C, K), device=dev, generator=g) if with_conv else None
     A = -torch.exp(2 * torch.rand(H, device=dev, generator=g))
     bias = 0.5 * torch.randn(H, device=dev, generator=g)
     sets = []
@@ -146,12 +152,14 @@ def wl_gdn_prep(bh, synth, dev, stream, n_tok=4096):
         beta = torch.randn((n_tok, H), device=dev, generator=g)
         outs = [torch.empty_like(conv), torch.empty_like(z), torch.empty_like(dt),
                 torch.empty_like(beta)]
-        sets.append((conv, z, y, dt, beta, outs))
+        cache = torch.randn((C, K - 1), device=dev, generator=g) if with_conv else None
+        sets.append((conv, z, y, dt, beta, outs, cache))
     args = [bh.make_gdn_args(conv=c, conv_out=o[0], z=z, y=y, gated_out=o[1], alpha_raw=dt,
                              dt_bias=bias, ssm_a=A, beta_raw=b, gate_out=o[2], beta_out=o[3],
                              n_tok=n_tok, conv_dim=C, l2_dim=C, head_dim=128, inner_dim=C,
-                             n_v_head=H, gate_mode=bh.BH_SIGMOID_MUL, eps=1e-6)
-            for c, z, y, dt, b, o in sets]
+                             n_v_head=H, gate_mode=bh.BH_SIGMOID_MUL, eps=1e-6,
+                             conv_w=taps, conv_state=cache, conv_k=K)
+            for c, z, y, dt, b, o, cache in sets]
     import ctypes
     refs = [ctypes.byref(a) for a in args]
     lib, sh = bh.lib(), stream.cuda_stream
@@ -160,7 +168,7 @@ def wl_gdn_prep(bh, synth, dev, stream, n_tok=4096):
         st = lib.bh_gdn_prep_fused(refs[i], sh)
         if st:
             bh.check(st)
-    return launch, len(sets), bytes_per, n_tok, (sets, A, bias, args)
+    return launch, len(sets), bytes_per, n_tok, (sets, A, bias, args, taps)
 
 
 def wl_softmax(bh, synth, dev, stream, rows, row_len, inv_t, causal=False, spikes=False):
@@ -395,6 +403,8 @@ def main() -> int:
                 ("rms_norm_rows T=2048", rows_wl[2048]),
                 ("rms_norm_rows T=8192", rows_wl[8192]),
                 ("gdn_prep_fused T=4096", lambda: wl_gdn_prep(bh, synth, dev, stream)),
+                ("gdn_prep_fused + conv1d T=4096",
+                 lambda: wl_gdn_prep(bh, synth, dev, stream, with_conv=True)),
                 ("softmax vocab [64,248320] temp 0.7",
                  lambda: wl_softmax(bh, synth, dev, stream, 64, 248320, float(1 / np32(0.7)),
                                     spikes=True)),

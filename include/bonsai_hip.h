@@ -144,9 +144,26 @@ typedef struct bh_gdn_prep_args {
   size_t n_v_head;  /* 48 in Ternary-Bonsai-27B                  */
   int gate_mode;    /* BH_SILU_MUL or BH_SIGMOID_MUL             */
   float eps;
+  /* Optional causal conv1d in front (src/forward.rs:508-533): when conv_w is
+   * non-NULL, `conv` holds the raw qkv projections and the channels are
+   * convolved with conv_w [conv_dim][conv_k] over the tokens and the cache
+   * conv_state [conv_dim][conv_k - 1] (oldest first) before the SiLU; the
+   * cache is then advanced by n_tok tokens, in place.  conv_out must not
+   * alias conv in this mode.  Zero these fields to leave it off. */
+  const float *conv_w;
+  float *conv_state;
+  size_t conv_k;
 } bh_gdn_prep_args;
 
 int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream);
+
+/* Causal conv1d + SiLU over n_tok tokens (src/forward.rs:508-533 applied per
+ * token): out[t][c] = silu(sum_j w[c][j] * s_{t-k+1+j}) with s_p = x[p][c]
+ * and, for p < 0, the cache state[c][p + k - 1] (k - 1 inputs per channel,
+ * oldest first); the cache is then advanced by n_tok tokens in place.
+ * x, out: [n_tok][ch] (out must not alias x); w: [ch][k]; 1 <= k <= 64. */
+int bh_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok,
+                   size_t ch, size_t k, float *out, bh_stream stream);
 
 /* ---------------------------------------------------------------------------
  * Softmax (src/kernels.rs:175-202; temperature: src/sampler.rs:85, 110)

@@ -309,6 +309,32 @@ int or_embed_gather(const uint8_t *payload, size_t ne0, size_t n_rows, const uin
   return OR_OK;
 }
 
+/* ---- causal conv1d + SiLU (src/forward.rs:508-533) ------------------------ */
+
+/* Per token, per channel: win = [state[c][0..k-1), x[t][c]] (oldest first),
+ * acc = sum_j w[c*k + j] * win[j] in f32, j ascending, out = silu(acc); then
+ * the state drops its oldest sample and appends x[t][c] (:526-532).  state is
+ * [ch][k-1] and is updated in place; k >= 1. */
+void or_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok, size_t ch,
+                    size_t k, float *out) {
+  size_t n_prev = k - 1;
+  float win[64];
+  for (size_t t = 0; t < n_tok; ++t) {
+    for (size_t c = 0; c < ch; ++c) {
+      for (size_t j = 0; j < n_prev; ++j) win[j] = state[c * n_prev + j];
+      win[n_prev] = x[t * ch + c];
+      float acc = 0.0f;
+      for (size_t j = 0; j < k; ++j) acc += w[c * k + j] * win[j];
+      out[t * ch + c] = or_silu(acc);
+    }
+    for (size_t c = 0; c < ch; ++c) {
+      if (n_prev == 0) continue;
+      for (size_t j = 0; j + 1 < n_prev; ++j) state[c * n_prev + j] = state[c * n_prev + j + 1];
+      state[c * n_prev + n_prev - 1] = x[t * ch + c];
+    }
+  }
+}
+
 /* ---- PQ2_0 products (src/kernels.rs:233-423) ------------------------------ */
 
 /* row_dot_scalar, src/kernels.rs:633-653: per 128-block an f32 sum of

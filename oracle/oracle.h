@@ -90,6 +90,10 @@ float or_pq2_row_dot(const uint8_t *raw, size_t ne0, const float *x);
 void or_pq2_matmul_n(const uint8_t *payload, size_t ne0, uint64_t base_row, size_t n_rows,
                      const float *x, size_t n_tok, float *y);
 
+/* src/forward.rs:508-533, per token in order; state [ch][k-1] in/out, k <= 64 */
+void or_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok, size_t ch,
+                    size_t k, float *out);
+
 #ifdef __cplusplus
 }
 #endif

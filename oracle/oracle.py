@@ -45,6 +45,7 @@ _SIG = {
     "or_gdn_gate_prep": (None, [_vp, _vp, _vp, _vp, _sz, _sz, _vp, _vp]),
     "or_silu_l2_part": (ctypes.c_int, [_vp, _sz, _sz, _sz, _sz, _f, _vp]),
     "or_pq2_row_dot": (_f, [_vp, _sz, _vp]),
+    "or_conv1d_silu": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "or_pq2_matmul_n": (None, [_vp, _sz, ctypes.c_uint64, _sz, _vp, _sz, _vp]),
 }
 
@@ -209,6 +210,20 @@ def embed_gather(table, ne0: int, n_rows: int, tokens, w=None, eps: float = 1e-6
                               _p(out), _p(out_norm), _p(bad)),
         f"row {int(bad[0])} out of range (n_rows {n_rows})")
     return (out, out_norm) if w is not None else out
+
+
+def conv1d_silu(x, state, w):
+    """Causal conv1d + SiLU over tokens (src/forward.rs:508-533): x [n_tok, ch],
+    state [ch, k-1], w [ch, k] -> (out [n_tok, ch], new state)."""
+    x, w = _c(x), _c(w)
+    st = _c(state).copy()
+    n_tok, ch = x.shape
+    k = w.shape[1]
+    if w.shape[0] != ch or st.shape != (ch, k - 1) or k < 1 or k > 64:
+        raise OracleShapeError("conv1d_silu shape")
+    out = np.empty_like(x)
+    lib().or_conv1d_silu(_p(x), _p(st), _p(w), n_tok, ch, k, _p(out))
+    return out, st
 
 
 def pq2_row_dot(raw, ne0: int, x) -> float:

@@ -72,6 +72,7 @@ class GdnPrepArgs(ctypes.Structure):
         ("gate_out", _vp), ("beta_out", _vp),
         ("n_tok", _c_size), ("conv_dim", _c_size), ("l2_dim", _c_size), ("head_dim", _c_size),
         ("inner_dim", _c_size), ("n_v_head", _c_size), ("gate_mode", _c_int), ("eps", _c_float),
+        ("conv_w", _vp), ("conv_state", _vp), ("conv_k", _c_size),
     ]
 
 
@@ -117,6 +118,7 @@ _SIGNATURES = {
                                      ctypes.POINTER(ctypes.c_int32), _c_float]),
     "bh_host_decode_pq2_0_row": (_c_int, [_vp, _c_size, _c_size, _vp]),
     "bh_host_batch_embed": (_c_int, [_vp, _c_size, _c_size, _c_size, _vp, _c_size, _vp]),
+    "bh_conv1d_silu": (_c_int, [_vp, _vp, _vp, _c_size, _c_size, _c_size, _vp, _vp]),
     "bh_pq2_matvec_range": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp,
                                      _c_size, _vp, _c_size, _vp]),
     "bh_pq2_matmul_n": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp, _c_size,
@@ -253,11 +255,15 @@ def gdn_gate_prep(alpha_raw, dt_bias, ssm_a, beta_raw, stream=None):
 def make_gdn_args(conv=None, conv_out=None, z=None, y=None, gated_out=None, alpha_raw=None,
                   dt_bias=None, ssm_a=None, beta_raw=None, gate_out=None, beta_out=None,
                   n_tok=0, conv_dim=0, l2_dim=0, head_dim=GDN_STATE, inner_dim=0,
-                  n_v_head=0, gate_mode=BH_SILU_MUL, eps=EPS) -> GdnPrepArgs:
+                  n_v_head=0, gate_mode=BH_SILU_MUL, eps=EPS, conv_w=None, conv_state=None,
+                  conv_k=0) -> GdnPrepArgs:
+    """With conv_w (and conv_state, conv_k), `conv` is the raw qkv and the
+    causal conv1d runs in front of the SiLU (src/forward.rs:508-533)."""
     return GdnPrepArgs(_ptr(conv), _ptr(conv_out), _ptr(z), _ptr(y), _ptr(gated_out),
                        _ptr(alpha_raw), _ptr(dt_bias), _ptr(ssm_a), _ptr(beta_raw),
                        _ptr(gate_out), _ptr(beta_out), n_tok, conv_dim, l2_dim, head_dim,
-                       inner_dim, n_v_head, gate_mode, eps)
+                       inner_dim, n_v_head, gate_mode, eps, _ptr(conv_w), _ptr(conv_state),
+                       conv_k if conv_w is not None else 0)
 
 
 def gdn_prep_fused(args: GdnPrepArgs, stream=None) -> None:
@@ -302,6 +308,18 @@ def pq2_embed_gather(table, ne0: int, n_rows: int, ids, out=None, w=None, eps: f
                                         w.data_ptr(), w.numel(), eps, out.data_ptr(),
                                         out_norm.data_ptr(), _ptr(bad_id), _stream(stream)))
     return out, out_norm
+
+
+def conv1d_silu(x, state, w, out=None, stream=None):
+    """Causal conv1d + SiLU (src/forward.rs:508-533) over x [n_tok, ch] with
+    the cache state [ch, k-1] (advanced in place) and taps w [ch, k]."""
+    import torch
+    n_tok, ch = x.shape
+    k = w.shape[1]
+    out = torch.empty_like(x) if out is None else out
+    check(lib().bh_conv1d_silu(x.data_ptr(), _ptr(state), w.data_ptr(), n_tok, ch, k,
+                               out.data_ptr(), _stream(stream)))
+    return out
 
 
 def pq2_matmul_n(payload, ne0: int, n_rows: int, x, base_row: int = 0, out=None, stream=None):

@@ -19,6 +19,7 @@
 #include <string>
 
 #include "common.hpp"
+#include "conv.hpp"
 
 namespace bh {
 namespace {
@@ -120,6 +121,7 @@ struct GdnParams {
   int conv_dim, l2_dim, head_dim, inner_dim, n_v_head;
   int sigmoid_gate;  // 1: y * sigmoid(z), 0: y * silu(z)
   float eps;
+  ConvIn cv;         // cv.k > 0: `conv` holds the raw qkv, convolved here first
 };
 
 // src/forward.rs:501-507: beta = sigmoid(beta_raw); gate = softplus(alpha_raw
@@ -204,6 +206,136 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a, int
   }
 }
 
+// Conv mode of the fused prep: a conv block runs kConvTok consecutive tokens
+// over its channels, with the taps loaded once and the 4-row input window
+// kept in registers (one new input row per token); per token it applies the
+// SiLU, the head L2 norm and the store as gdn_prep_fused_kernel does.  The
+// gated-output blocks stay one token each.  Grid: per group of kConvTok
+// tokens, bc conv blocks then kConvTok * bg gated-output blocks.
+constexpr int kConvTok = 4;
+
+template <int G>
+__global__ __launch_bounds__(kBlock) void gdn_prep_conv_kernel(GdnParams a, int bc, int bg,
+                                                               size_t n_tok) {
+  const int per_grp = bc + kConvTok * bg;
+  const size_t grp = blockIdx.x / per_grp;
+  const int part = blockIdx.x % per_grp;
+  const int tid = threadIdx.x;
+  const size_t t0 = grp * kConvTok;
+  const int nt = n_tok - t0 < static_cast<size_t>(kConvTok) ? static_cast<int>(n_tok - t0) : kConvTok;
+
+  if (part < bc) {
+    const int n4 = a.conv_dim >> 2;
+    const int l2_4 = a.l2_dim >> 2;
+    if (part == 0)
+      for (int e = tid; e < nt * a.n_v_head; e += kBlock) {
+        const int tt = e / a.n_v_head, h = e - tt * a.n_v_head;
+        small_gates(a, (t0 + tt) * a.n_v_head + h, h);
+      }
+    float wv[kU][4][4];  // [u][channel q][tap j]
+    float4 win[kU][4];   // [u][tap j]: inputs of the current token's window
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = (part * kU + u) * kBlock + tid;
+      const int c = 4 * (i < n4 ? i : 0);
+      const float4 *w4 = reinterpret_cast<const float4 *>(a.cv.w + static_cast<size_t>(c) * 4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 f = w4[q];
+        wv[u][q][0] = f.x;
+        wv[u][q][1] = f.y;
+        wv[u][q][2] = f.z;
+        wv[u][q][3] = f.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {  // the three inputs before t0
+        const long p = static_cast<long>(t0) - 3 + j;
+        if (p >= 0) {
+          win[u][j] = reinterpret_cast<const float4 *>(a.cv.x + static_cast<size_t>(p) * a.conv_dim)[c / 4];
+        } else {
+          const float *st = a.cv.state + static_cast<size_t>(c) * 3 + (p + 3);
+          win[u][j] = make_float4(st[0], st[3], st[6], st[9]);
+        }
+      }
+    }
+    for (int tt = 0; tt < nt; ++tt) {
+      const size_t t = t0 + tt;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = (part * kU + u) * kBlock + tid;
+        const int c = 4 * (i < n4 ? i : 0);
+        win[u][3] = load_stream(reinterpret_cast<const float4 *>(a.cv.x + t * a.conv_dim) + c / 4);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = (part * kU + u) * kBlock + tid;
+        // src/forward.rs:518-522: acc = sum_j w[c][j] * win[j], j ascending
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc.x += wv[u][0][j] * win[u][j].x;
+          acc.y += wv[u][1][j] * win[u][j].y;
+          acc.z += wv[u][2][j] * win[u][j].z;
+          acc.w += wv[u][3][j] * win[u][j].w;
+        }
+        float4 s = silu4(acc);
+        double ss = static_cast<double>(s.x) * static_cast<double>(s.x);
+        ss += static_cast<double>(s.y) * static_cast<double>(s.y);
+        ss += static_cast<double>(s.z) * static_cast<double>(s.z);
+        ss += static_cast<double>(s.w) * static_cast<double>(s.w);
+#pragma unroll
+        for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (i < l2_4) {
+          const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
+          s = make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
+        }
+        if (i < n4) store_stream(reinterpret_cast<float4 *>(a.conv_out) + t * n4 + i, s);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) win[u][j] = win[u][j + 1];  // slide the window
+      }
+    }
+  } else {
+    const int gp = part - bc;
+    const size_t t = t0 + gp / bg;
+    if (t >= n_tok) return;
+    const int n4 = a.inner_dim >> 2;
+    const int gb = gp % bg;
+    float4 z[kU], y[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = (gb * kU + u) * kBlock + tid;
+      if (i < n4) {
+        z[u] = load_stream(reinterpret_cast<const float4 *>(a.z) + t * n4 + i);
+        y[u] = load_stream(reinterpret_cast<const float4 *>(a.y) + t * n4 + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = (gb * kU + u) * kBlock + tid;
+      if (i < n4)
+        store_stream(reinterpret_cast<float4 *>(a.gated_out) + t * n4 + i,
+                     a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(z[u], y[u])
+                                    : unary_op4<BH_SILU_MUL>(z[u], y[u]));
+    }
+  }
+}
+
+template <int G>
+int launch_fused(const GdnParams &p, bool conv, size_t n_tok, int bc, int bg, hipStream_t st) {
+  if (conv) {
+    const size_t groups = (n_tok + kConvTok - 1) / kConvTok;
+    const size_t blocks = groups * static_cast<size_t>(bc + kConvTok * bg);
+    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: too many blocks");
+    BH_LAUNCH(gdn_prep_conv_kernel<G>, static_cast<unsigned>(blocks), kBlock, 0, st, p, bc, bg,
+              n_tok);
+  } else {
+    const size_t blocks = n_tok * static_cast<size_t>(bc + bg);
+    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: too many blocks");
+    BH_LAUNCH(gdn_prep_fused_kernel<G>, static_cast<unsigned>(blocks), kBlock, 0, st, p, bc, bg);
+  }
+  return ok();
+}
+
 // Scalar gates only (no conv / gated rows requested).
 __global__ __launch_bounds__(kBlock) void gdn_small_gates_kernel(GdnParams a, size_t total) {
   const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -220,20 +352,22 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_loop_kernel(GdnParams a) {
   if (a.conv_out != nullptr) {
     const float *c = a.conv + t * a.conv_dim;
     float *o = a.conv_out + t * a.conv_dim;
+    // channel value before the SiLU: the input, or its causal conv
+    auto pre = [&](int ch) { return a.cv.k > 0 ? conv_at(a.cv, t, ch) : c[ch]; };
     const int n_heads = a.l2_dim / a.head_dim;
     for (int hh = 0; hh < n_heads; ++hh) {
       double ss = 0.0;
       for (int d = tid; d < a.head_dim; d += kBlock) {
-        const float s = silu(c[hh * a.head_dim + d]);
+        const float s = silu(pre(hh * a.head_dim + d));
         ss += static_cast<double>(s) * static_cast<double>(s);
       }
       ss = group_reduce<kBlock>(ss, SumOp{}, lds);
       const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
       for (int d = tid; d < a.head_dim; d += kBlock)
-        o[hh * a.head_dim + d] = silu(c[hh * a.head_dim + d]) * scale;
+        o[hh * a.head_dim + d] = silu(pre(hh * a.head_dim + d)) * scale;
       __syncthreads();  // lds reuse by the next head
     }
-    for (int i = a.l2_dim + tid; i < a.conv_dim; i += kBlock) o[i] = silu(c[i]);
+    for (int i = a.l2_dim + tid; i < a.conv_dim; i += kBlock) o[i] = silu(pre(i));
   }
   if (a.gated_out != nullptr) {
     const size_t off = t * a.inner_dim;
@@ -302,6 +436,18 @@ extern "C" int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream)
                                     std::to_string(g.conv_dim));
     if (!g.conv) return fail(BH_ERR_ARG, "gdn_prep_fused: null conv");
   }
+  const bool conv_in = g.conv_w != nullptr;
+  if (conv_in) {
+    if (g.conv_out == nullptr)
+      return fail(BH_ERR_ARG, "gdn_prep_fused: conv_w needs conv_out (the convolved channels)");
+    if (g.conv_k < 1 || g.conv_k > static_cast<size_t>(kMaxConvK))
+      return fail(BH_ERR_SHAPE, "gdn_prep_fused: conv kernel size " + std::to_string(g.conv_k) +
+                                    " must be in 1.." + std::to_string(kMaxConvK));
+    const ConvIn cv{g.conv, g.conv_state, g.conv_w, static_cast<int>(g.conv_dim),
+                    static_cast<int>(g.conv_k)};
+    if (g.n_tok > 0)
+      if (int e = conv_check(cv, g.conv_out, "gdn_prep_fused")) return e;
+  }
   if (g.gated_out != nullptr && (!g.z || !g.y)) return fail(BH_ERR_ARG, "gdn_prep_fused: null z/y");
   if ((g.gate_out && (!g.alpha_raw || !g.dt_bias || !g.ssm_a)) || (g.beta_out && !g.beta_raw))
     return fail(BH_ERR_ARG, "gdn_prep_fused: null gate input");
@@ -328,12 +474,16 @@ extern "C" int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream)
   p.n_v_head = (g.gate_out || g.beta_out) ? static_cast<int>(g.n_v_head) : 0;
   p.sigmoid_gate = g.gate_mode == BH_SIGMOID_MUL ? 1 : 0;
   p.eps = g.eps;
+  if (conv_in)
+    p.cv = ConvIn{g.conv, g.conv_state, g.conv_w, static_cast<int>(g.conv_dim),
+                  static_cast<int>(g.conv_k)};
   const unsigned grid = static_cast<unsigned>(g.n_tok);
   hipStream_t st = as_stream(stream);
   const size_t hq = g.head_dim / 4;
   const bool conv_fast = g.conv_out == nullptr ||
                          (g.conv_dim % 4 == 0 && g.head_dim % 4 == 0 && hq >= 1 && hq <= 64 &&
-                          (hq & (hq - 1)) == 0 && aligned16(g.conv) && aligned16(g.conv_out));
+                          (hq & (hq - 1)) == 0 && aligned16(g.conv) && aligned16(g.conv_out) &&
+                          (!conv_in || (g.conv_k == 4 && aligned16(g.conv_w))));
   const bool gate_fast = g.gated_out == nullptr ||
                          (g.inner_dim % 4 == 0 && aligned16(g.z) && aligned16(g.y) &&
                           aligned16(g.gated_out));
@@ -350,25 +500,28 @@ extern "C" int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream)
     const int per_block = kBlock * kU;  // float4 per block
     const int bc = g.conv_out ? static_cast<int>((g.conv_dim / 4 + per_block - 1) / per_block) : 1;
     const int bg = g.gated_out ? static_cast<int>((g.inner_dim / 4 + per_block - 1) / per_block) : 0;
-    const size_t blocks = g.n_tok * static_cast<size_t>(bc + bg);
-    if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: too many blocks");
-    const unsigned fgrid = static_cast<unsigned>(blocks);
     if (g.conv_out == nullptr) {
       // conv part disabled: its block only computes the scalar gates
       p.conv_dim = 0;
       p.l2_dim = 0;
     }
+    int e = -999;
     switch (g.conv_out == nullptr ? 64 : hq) {
-      case 1: BH_LAUNCH(gdn_prep_fused_kernel<1>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
-      case 2: BH_LAUNCH(gdn_prep_fused_kernel<2>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
-      case 4: BH_LAUNCH(gdn_prep_fused_kernel<4>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
-      case 8: BH_LAUNCH(gdn_prep_fused_kernel<8>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
-      case 16: BH_LAUNCH(gdn_prep_fused_kernel<16>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
-      case 32: BH_LAUNCH(gdn_prep_fused_kernel<32>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
-      case 64: BH_LAUNCH(gdn_prep_fused_kernel<64>, fgrid, kBlock, 0, st, p, bc, bg); return ok();
+      case 1: e = launch_fused<1>(p, conv_in, g.n_tok, bc, bg, st); break;
+      case 2: e = launch_fused<2>(p, conv_in, g.n_tok, bc, bg, st); break;
+      case 4: e = launch_fused<4>(p, conv_in, g.n_tok, bc, bg, st); break;
+      case 8: e = launch_fused<8>(p, conv_in, g.n_tok, bc, bg, st); break;
+      case 16: e = launch_fused<16>(p, conv_in, g.n_tok, bc, bg, st); break;
+      case 32: e = launch_fused<32>(p, conv_in, g.n_tok, bc, bg, st); break;
+      case 64: e = launch_fused<64>(p, conv_in, g.n_tok, bc, bg, st); break;
       default: break;
+    }
+    if (e != -999) {
+      if (e != BH_OK) return e;
+      // the conv cache shifts only after every token has read it
+      return conv_in ? conv_state_update(p.cv, g.n_tok, st) : ok();
     }
   }
   BH_LAUNCH(gdn_prep_loop_kernel, grid, kBlock, 0, st, p);
-  return ok();
+  return conv_in ? conv_state_update(p.cv, g.n_tok, st) : ok();
 }

@@ -13,7 +13,7 @@ import pytest
 def test_library_exports_every_header_symbol(bh):
     lib = bh.lib()
     names = bh.header_symbols()
-    assert len(names) == 29
+    assert len(names) == 30
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     # and the Python binding declares a signature for each of them
@@ -161,6 +161,20 @@ def test_pq2_product_shape_errors(bh):
     assert lib.bh_host_pq2_matmul_n(raw.ctypes.data, raw.size, 5120, 0, 2, x.ctypes.data, 5120,
                                     2, out.ctypes.data, 4) == bh.BH_ERR_SHAPE
     assert bh.last_error() == "pq2_matmul_n: x length 5120 != n_tok 2 * ne0 5120"
+
+
+def test_conv1d_argument_errors(bh):
+    """bh_conv1d_silu rejects a bad tap count, a missing cache and an output
+    aliasing the input before touching the device."""
+    lib = bh.lib()
+    d = ctypes.c_void_p(64)
+    assert lib.bh_conv1d_silu(d, d, d, 4, 16, 0, ctypes.c_void_p(128), None) == bh.BH_ERR_SHAPE
+    assert "conv kernel size 0" in bh.last_error()
+    assert lib.bh_conv1d_silu(d, d, d, 4, 16, 65, ctypes.c_void_p(128), None) == bh.BH_ERR_SHAPE
+    assert lib.bh_conv1d_silu(d, None, d, 4, 16, 4, ctypes.c_void_p(128), None) == bh.BH_ERR_ARG
+    assert lib.bh_conv1d_silu(d, d, d, 4, 16, 4, d, None) == bh.BH_ERR_ARG
+    assert "must not alias" in bh.last_error()
+    assert lib.bh_conv1d_silu(None, None, None, 0, 16, 4, None, None) == bh.BH_OK
 
 
 def test_splitmix64_known_vector(synth):

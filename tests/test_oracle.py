@@ -447,3 +447,47 @@ def test_pq2_matmul_n_reference_case(oracle, synth):
     assert np.max(np.abs(y - ref)) / np.max(np.abs(ref)) < 1e-6
     tail = oracle.pq2_matmul_n(payload, ne0, 5, x, base_row=7)
     assert np.array_equal(tail, y[:, 7:12])
+
+
+# ---------------------------------------------------------------------------
+# causal conv1d + SiLU (src/forward.rs:508-533)
+# ---------------------------------------------------------------------------
+
+def test_conv1d_unit_taps_and_state(oracle, synth):
+    """Closed form: with tap j set to 1 and the others 0, out[t][c] is
+    silu of the input j - (k-1) steps back (the state for negative times),
+    and the final state holds the last k-1 inputs."""
+    ch, k, n_tok = 12, 4, 6
+    r = synth.Rng(61)
+    x = r.normal(n_tok * ch).reshape(n_tok, ch)
+    st0 = r.normal(ch * (k - 1)).reshape(ch, k - 1)
+    seq = np.concatenate([st0.T, x], axis=0)  # position p -> row p + k - 1
+    for j in range(k):
+        w = np.zeros((ch, k), np.float32)
+        w[:, j] = 1.0
+        out, st = oracle.conv1d_silu(x, st0, w)
+        want = seq[j:j + n_tok]
+        silu = np.array([oracle.silu(float(v)) for v in want.ravel()], np.float32).reshape(want.shape)
+        assert np.array_equal(out, silu), j
+        assert np.array_equal(st, seq[-(k - 1):].T)
+
+
+def test_conv1d_batched_equals_token_steps(oracle, synth):
+    """The reference runs one token at a time with the state threaded
+    through; a batch of tokens must give the same outputs and state."""
+    ch, k, n_tok = 40, 4, 9
+    r = synth.Rng(62)
+    x = r.normal(n_tok * ch).reshape(n_tok, ch)
+    st0 = r.normal(ch * (k - 1)).reshape(ch, k - 1)
+    w = r.normal(ch * k).reshape(ch, k)
+    out, st = oracle.conv1d_silu(x, st0, w)
+    s = st0
+    for t in range(n_tok):
+        o1, s = oracle.conv1d_silu(x[t:t + 1], s, w)
+        assert np.array_equal(o1[0], out[t]), t
+    assert np.array_equal(s, st)
+    # and the pre-activation is the float64 convolution to f32 rounding
+    seq = np.concatenate([st0.T, x], axis=0).astype(np.float64)
+    acc = sum(seq[j:j + n_tok] * w[:, j].astype(np.float64) for j in range(k))
+    silu64 = acc / (1 + np.exp(-acc))
+    assert np.max(np.abs(out - silu64)) / np.max(np.abs(silu64)) < 1e-6
