@@ -171,6 +171,29 @@ def wl_gdn_prep(bh, synth, dev, stream, n_tok=4096, with_conv=False):
     return launch, len(sets), bytes_per, n_tok, (sets, A, bias, args, taps)
 
 
+def wl_conv1d(bh, synth, dev, stream, n_tok=4096, ch=10240, k=4):
+    """Causal conv1d + SiLU (src/forward.rs:508-533) over a prefill batch of
+    the model's qkv width: inputs read once, outputs written once, the taps
+    and the cache (read and written)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    bytes_per = 2 * n_tok * ch * 4 + ch * k * 4 + 2 * ch * (k - 1) * 4
+    w = 0.5 * torch.randn((ch, k), device=dev, generator=g)
+    sets = [(torch.randn((n_tok, ch), device=dev, generator=g),
+             torch.randn((ch, k - 1), device=dev, generator=g),
+             torch.empty((n_tok, ch), device=dev)) for _ in range(n_sets(bytes_per))]
+    lib, sh = bh.lib(), stream.cuda_stream
+
+    def launch(i):
+        x, cache, out = sets[i]
+        st = lib.bh_conv1d_silu(x.data_ptr(), cache.data_ptr(), w.data_ptr(), n_tok, ch, k,
+                                out.data_ptr(), sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, n_tok, (sets, w)
+
+
 def wl_softmax(bh, synth, dev, stream, rows, row_len, inv_t, causal=False, spikes=False):
     import torch
     g = torch.Generator(device=dev)
@@ -405,6 +428,7 @@ def main() -> int:
                 ("gdn_prep_fused T=4096", lambda: wl_gdn_prep(bh, synth, dev, stream)),
                 ("gdn_prep_fused + conv1d T=4096",
                  lambda: wl_gdn_prep(bh, synth, dev, stream, with_conv=True)),
+                ("conv1d_silu [4096,10240] k=4", lambda: wl_conv1d(bh, synth, dev, stream)),
                 ("softmax vocab [64,248320] temp 0.7",
                  lambda: wl_softmax(bh, synth, dev, stream, 64, 248320, float(1 / np32(0.7)),
                                     spikes=True)),

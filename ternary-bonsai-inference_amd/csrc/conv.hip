@@ -24,16 +24,56 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// out[t][c..c+3] for k = 4, channels 16-byte aligned.
+// out[t][c..c+3] for k = 4, channels 16-byte aligned: a lane runs kConvRun
+// consecutive tokens of its 4 channels with the taps and the 4-row input
+// window in registers (one new input row per token).
+constexpr int kConvRun = 8;
+
 __global__ __launch_bounds__(kBlock) void conv1d_silu4_kernel(ConvIn cv, float *out, size_t n4,
-                                                              size_t total) {
+                                                              size_t n_tok) {
   const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
-  if (i >= total) return;
-  const size_t t = i / n4;
-  const int c = static_cast<int>(i - t * n4) * 4;
-  const float4 acc = conv_window4<4>(cv, t, c);
-  store_stream(reinterpret_cast<float4 *>(out + t * cv.ch) + c / 4,
-               make_float4(silu(acc.x), silu(acc.y), silu(acc.z), silu(acc.w)));
+  if (i >= n4) return;
+  const size_t t0 = static_cast<size_t>(blockIdx.y) * kConvRun;
+  const int c = static_cast<int>(i) * 4;
+  float wv[4][4];  // [channel q][tap j]
+  const float4 *w4 = reinterpret_cast<const float4 *>(cv.w + static_cast<size_t>(c) * 4);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 f = w4[q];
+    wv[q][0] = f.x;
+    wv[q][1] = f.y;
+    wv[q][2] = f.z;
+    wv[q][3] = f.w;
+  }
+  float4 win[4];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const long p = static_cast<long>(t0) - 3 + j;
+    if (p >= 0) {
+      win[j] = reinterpret_cast<const float4 *>(cv.x + static_cast<size_t>(p) * cv.ch)[i];
+    } else {
+      const float *st = cv.state + static_cast<size_t>(c) * 3 + (p + 3);
+      win[j] = make_float4(st[0], st[3], st[6], st[9]);
+    }
+  }
+  const int nt = n_tok - t0 < static_cast<size_t>(kConvRun) ? static_cast<int>(n_tok - t0) : kConvRun;
+  for (int tt = 0; tt < nt; ++tt) {
+    const size_t t = t0 + tt;
+    win[3] = load_stream(reinterpret_cast<const float4 *>(cv.x + t * cv.ch) + i);
+    // src/forward.rs:518-522: acc = sum_j w[c][j] * win[j], j ascending
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc.x += wv[0][j] * win[j].x;
+      acc.y += wv[1][j] * win[j].y;
+      acc.z += wv[2][j] * win[j].z;
+      acc.w += wv[3][j] * win[j].w;
+    }
+    store_stream(reinterpret_cast<float4 *>(out + t * cv.ch) + i,
+                 make_float4(silu(acc.x), silu(acc.y), silu(acc.z), silu(acc.w)));
+#pragma unroll
+    for (int j = 0; j < 3; ++j) win[j] = win[j + 1];
+  }
 }
 
 // Any k / layout: one output per lane.
@@ -98,10 +138,12 @@ extern "C" int bh_conv1d_silu(const float *x, float *state, const float *w, size
   if (int e = conv_check(cv, out, "conv1d_silu")) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t total = n_tok * ch;
-  if (k == 4 && ch % 4 == 0 && aligned16(x) && aligned16(out) && aligned16(w)) {
-    const size_t n4 = ch / 4, t4 = n_tok * n4;
-    BH_LAUNCH(conv1d_silu4_kernel, static_cast<unsigned>((t4 + kBlock - 1) / kBlock), kBlock, 0,
-              st, cv, out, n4, t4);
+  const size_t runs = (n_tok + kConvRun - 1) / kConvRun;
+  if (k == 4 && ch % 4 == 0 && aligned16(x) && aligned16(out) && aligned16(w) && runs <= 65535) {
+    const size_t n4 = ch / 4;
+    BH_LAUNCH(conv1d_silu4_kernel, dim3(static_cast<unsigned>((n4 + kBlock - 1) / kBlock),
+                                        static_cast<unsigned>(runs)),
+              kBlock, 0, st, cv, out, n4, n_tok);
   } else {
     if ((total + kBlock - 1) / kBlock > 0x7fffffffu)
       return fail(BH_ERR_SHAPE, "conv1d_silu: too many elements");
