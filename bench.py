@@ -194,6 +194,34 @@ def wl_conv1d(bh, synth, dev, stream, n_tok=4096, ch=10240, k=4):
     return launch, len(sets), bytes_per, n_tok, (sets, w)
 
 
+def wl_gdn_step(bh, synth, dev, stream, n_tok, h_k=16, h_v=48, s=128):
+    """Gated delta-net recurrence (src/gdn.rs:17-77) over n_tok tokens of the
+    model's heads: the state [48,128,128] read and written once, per token
+    q, k [16,128], v, attn [48,128] and gate, beta [48]."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(8)
+    per_tok = (2 * h_k * s + 2 * h_v * s + 2 * h_v) * 4
+    bytes_per = 2 * h_v * s * s * 4 + n_tok * per_tok
+    q = torch.nn.functional.normalize(torch.randn((n_tok, h_k, s), device=dev, generator=g), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn((n_tok, h_k, s), device=dev, generator=g), dim=-1)
+    v = torch.randn((n_tok, h_v, s), device=dev, generator=g)
+    gate = -torch.rand((n_tok, h_v), device=dev, generator=g)
+    beta = torch.rand((n_tok, h_v), device=dev, generator=g)
+    sets = [(0.1 * torch.randn((h_v, s, s), device=dev, generator=g),
+             torch.empty((n_tok, h_v, s), device=dev)) for _ in range(n_sets(bytes_per))]
+    lib, sh = bh.lib(), stream.cuda_stream
+
+    def launch(i):
+        st_, attn = sets[i]
+        rc = lib.bh_gdn_step(q.data_ptr(), k.data_ptr(), v.data_ptr(), gate.data_ptr(),
+                             beta.data_ptr(), st_.data_ptr(), attn.data_ptr(), n_tok, h_k, h_v,
+                             s, sh)
+        if rc:
+            bh.check(rc)
+    return launch, len(sets), bytes_per, n_tok, (sets, q, k, v, gate, beta)
+
+
 def wl_softmax(bh, synth, dev, stream, rows, row_len, inv_t, causal=False, spikes=False):
     import torch
     g = torch.Generator(device=dev)
@@ -435,6 +463,8 @@ def main() -> int:
                 ("softmax causal [24*2048,2048]",
                  lambda: wl_softmax(bh, synth, dev, stream, 24 * 2048, 2048, 1.0, causal=True)),
                 ("pq2_gather_rms T=8192", lambda: wl_gather_rms(bh, synth, dev, stream)),
+                ("gdn_step decode T=1", lambda: wl_gdn_step(bh, synth, dev, stream, 1)),
+                ("gdn_step T=256", lambda: wl_gdn_step(bh, synth, dev, stream, 256)),
             ]
             products = [  # (name, rows, ne0, tokens): decode matvecs and batched products
                 ("pq2_matvec LM head [248320x5120] N=1", 248320, 5120, 1),

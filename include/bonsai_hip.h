@@ -165,6 +165,17 @@ int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream);
 int bh_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok,
                    size_t ch, size_t k, float *out, bh_stream stream);
 
+/* Gated delta-net recurrence over n_tok tokens (src/gdn.rs:17-77, gdn_step,
+ * applied per token; the reference fixes s = 128, h_k = 16, h_v = 48).  Per
+ * token t and v-head h (q/k head h % h_k), with M = state[h] (s x s, row j
+ * contiguous): M *= expf(gate[t][h]); delta[j] = (v[t][h][j] - M[j].k) *
+ * beta[t][h]; M[j] += k * delta[j]; attn[t][h][j] = (M[j].q) / sqrtf(s).
+ * q, k: [n_tok][h_k][s]; v, attn: [n_tok][h_v][s]; gate, beta: [n_tok][h_v];
+ * state: [h_v][s][s], updated in place.  n_tok = 0 is a no-op. */
+int bh_gdn_step(const float *q, const float *k, const float *v, const float *gate,
+                const float *beta, float *state, float *attn, size_t n_tok, size_t h_k,
+                size_t h_v, size_t s, bh_stream stream);
+
 /* ---------------------------------------------------------------------------
  * Softmax (src/kernels.rs:175-202; temperature: src/sampler.rs:85, 110)
  * ------------------------------------------------------------------------- */
@@ -313,6 +324,16 @@ int bh_host_pq2_matvec_range(const uint8_t *payload, size_t payload_len, size_t 
 int bh_host_pq2_matmul_n(const uint8_t *payload, size_t payload_len, size_t ne0,
                          uint64_t base_row, size_t n_rows, const float *x,
                          size_t x_len, size_t n_tok, float *y, size_t y_len);
+
+/* gdn_step, src/gdn.rs:17-77, with its fixed shape (s = 128, h_k = 16,
+ * h_v = 48) and one token: q, k [16*128], v [48*128], gate, beta [48],
+ * state [48*128*128] (advanced in place), attn [48*128] (written).  A slice
+ * shorter than that is an error "gdn_step: <name> len L < N" (the
+ * reference's indexing would panic). */
+int bh_host_gdn_step(const float *q, size_t q_len, const float *k, size_t k_len, const float *v,
+                     size_t v_len, const float *gate, size_t gate_len, const float *beta,
+                     size_t beta_len, float *state, size_t state_len, float *attn,
+                     size_t attn_len);
 
 #ifdef __cplusplus
 }

@@ -335,6 +335,46 @@ void or_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok, 
   }
 }
 
+/* ---- gated delta-net recurrence (src/gdn.rs:17-77) ------------------------- */
+
+/* gdn_step applied to n_tok tokens in order.  Per token t and v-head h (k/q
+ * head h % h_k): M = state[h] (s x s, row j contiguous) *= expf(gate);
+ * delta[j] = (v[j] - sum_i M[j][i] k[i]) * beta; M[j][i] += k[i] * delta[j];
+ * attn[j] = (sum_i M[j][i] q[i]) * (1 / sqrtf(s)); sums in f32, i ascending.
+ * q, k: [n_tok][h_k][s]; v, attn: [n_tok][h_v][s]; gate, beta: [n_tok][h_v];
+ * state: [h_v][s][s], updated in place. */
+void or_gdn_step(const float *q, const float *k, const float *v, const float *gate,
+                 const float *beta, float *state, float *attn, size_t n_tok, size_t h_k,
+                 size_t h_v, size_t s) {
+  float scale = 1.0f / sqrtf((float)s);
+  float *delta = (float *)malloc(s * sizeof(float));
+  if (delta == NULL) return;
+  for (size_t t = 0; t < n_tok; ++t) {
+    for (size_t h = 0; h < h_v; ++h) {
+      const float *qv = q + (t * h_k + h % h_k) * s;
+      const float *kv = k + (t * h_k + h % h_k) * s;
+      const float *vv = v + (t * h_v + h) * s;
+      float *m = state + h * s * s;
+      float eg = expf(gate[t * h_v + h]);
+      for (size_t x = 0; x < s * s; ++x) m[x] *= eg;
+      for (size_t j = 0; j < s; ++j) {
+        float sum = 0.0f;
+        for (size_t i = 0; i < s; ++i) sum += m[j * s + i] * kv[i];
+        delta[j] = (vv[j] - sum) * beta[t * h_v + h];
+      }
+      for (size_t j = 0; j < s; ++j)
+        for (size_t i = 0; i < s; ++i) m[j * s + i] += kv[i] * delta[j];
+      float *out = attn + (t * h_v + h) * s;
+      for (size_t j = 0; j < s; ++j) {
+        float sum = 0.0f;
+        for (size_t i = 0; i < s; ++i) sum += m[j * s + i] * qv[i];
+        out[j] = sum * scale;
+      }
+    }
+  }
+  free(delta);
+}
+
 /* ---- PQ2_0 products (src/kernels.rs:233-423) ------------------------------ */
 
 /* row_dot_scalar, src/kernels.rs:633-653: per 128-block an f32 sum of

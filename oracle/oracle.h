@@ -94,6 +94,11 @@ void or_pq2_matmul_n(const uint8_t *payload, size_t ne0, uint64_t base_row, size
 void or_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok, size_t ch,
                     size_t k, float *out);
 
+/* src/gdn.rs:17-77 over n_tok tokens; state [h_v][s][s] in/out */
+void or_gdn_step(const float *q, const float *k, const float *v, const float *gate,
+                 const float *beta, float *state, float *attn, size_t n_tok, size_t h_k,
+                 size_t h_v, size_t s);
+
 #ifdef __cplusplus
 }
 #endif

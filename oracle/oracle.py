@@ -46,6 +46,7 @@ _SIG = {
     "or_silu_l2_part": (ctypes.c_int, [_vp, _sz, _sz, _sz, _sz, _f, _vp]),
     "or_pq2_row_dot": (_f, [_vp, _sz, _vp]),
     "or_conv1d_silu": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "or_gdn_step": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz]),
     "or_pq2_matmul_n": (None, [_vp, _sz, ctypes.c_uint64, _sz, _vp, _sz, _vp]),
 }
 
@@ -224,6 +225,23 @@ def conv1d_silu(x, state, w):
     out = np.empty_like(x)
     lib().or_conv1d_silu(_p(x), _p(st), _p(w), n_tok, ch, k, _p(out))
     return out, st
+
+
+def gdn_step(q, k, v, gate, beta, state):
+    """gdn_step (src/gdn.rs:17-77) over tokens: q, k [n_tok, h_k, s]; v
+    [n_tok, h_v, s]; gate, beta [n_tok, h_v]; state [h_v, s, s] ->
+    (attn [n_tok, h_v, s], new state)."""
+    q, k, v, gate, beta = map(_c, (q, k, v, gate, beta))
+    st = _c(state).copy()
+    n_tok, h_k, s = q.shape
+    h_v = v.shape[1]
+    if k.shape != q.shape or v.shape != (n_tok, h_v, s) or gate.shape != (n_tok, h_v) or \
+            beta.shape != (n_tok, h_v) or st.shape != (h_v, s, s):
+        raise OracleShapeError("gdn_step shape")
+    attn = np.empty_like(v)
+    lib().or_gdn_step(_p(q), _p(k), _p(v), _p(gate), _p(beta), _p(st), _p(attn), n_tok, h_k,
+                      h_v, s)
+    return attn, st
 
 
 def pq2_row_dot(raw, ne0: int, x) -> float:

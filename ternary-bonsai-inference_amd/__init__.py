@@ -119,6 +119,10 @@ _SIGNATURES = {
     "bh_host_decode_pq2_0_row": (_c_int, [_vp, _c_size, _c_size, _vp]),
     "bh_host_batch_embed": (_c_int, [_vp, _c_size, _c_size, _c_size, _vp, _c_size, _vp]),
     "bh_conv1d_silu": (_c_int, [_vp, _vp, _vp, _c_size, _c_size, _c_size, _vp, _vp]),
+    "bh_host_gdn_step": (_c_int, [_vp, _c_size, _vp, _c_size, _vp, _c_size, _vp, _c_size, _vp,
+                                  _c_size, _vp, _c_size, _vp, _c_size]),
+    "bh_gdn_step": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_size, _c_size,
+                             _c_size, _vp]),
     "bh_pq2_matvec_range": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp,
                                      _c_size, _vp, _c_size, _vp]),
     "bh_pq2_matmul_n": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp, _c_size,
@@ -320,6 +324,20 @@ def conv1d_silu(x, state, w, out=None, stream=None):
     check(lib().bh_conv1d_silu(x.data_ptr(), _ptr(state), w.data_ptr(), n_tok, ch, k,
                                out.data_ptr(), _stream(stream)))
     return out
+
+
+def gdn_step(q, k, v, gate, beta, state, attn=None, stream=None):
+    """Gated delta-net recurrence (src/gdn.rs:17-77 per token) over device
+    tensors q, k [n_tok, h_k, s], v [n_tok, h_v, s], gate, beta [n_tok, h_v];
+    state [h_v, s, s] is advanced in place; returns attn [n_tok, h_v, s]."""
+    import torch
+    n_tok, h_k, s = q.shape
+    h_v = v.shape[1]
+    attn = torch.empty_like(v) if attn is None else attn
+    check(lib().bh_gdn_step(q.data_ptr(), k.data_ptr(), v.data_ptr(), gate.data_ptr(),
+                            beta.data_ptr(), state.data_ptr(), attn.data_ptr(), n_tok, h_k, h_v,
+                            s, _stream(stream)))
+    return attn
 
 
 def pq2_matmul_n(payload, ne0: int, n_rows: int, x, base_row: int = 0, out=None, stream=None):

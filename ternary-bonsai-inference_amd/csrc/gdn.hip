@@ -1,0 +1,383 @@
+// Gated delta-net recurrence over a batch of tokens.
+//
+// Reference: gdn_step, src/gdn.rs:17-77 (one token): for every v-head h
+// (q/k head h % h_k) with state M = state[h] (s x s, row j contiguous):
+//   M *= expf(gate[h]);
+//   delta[j] = (v[j] - dot(M[j], k)) * beta[h];
+//   M[j] += k * delta[j];
+//   attn[j] = dot(M[j], q) * (1 / sqrtf(s)).
+// Each row M[j] only ever meets its own delta[j] and the head's vectors, so
+// the h_v * s rows are independent recurrences of s floats.  The fast path
+// (s = 128) gives a row to 16 lanes, 8 floats each, held in registers for
+// the whole token batch: per token the lanes take both row dots from the
+// state before the token (a depth-3 tree in the lane, then a DPP tree over
+// the 16 lanes; see token_step for the algebra), update the row and store
+// one output; the state is read and written once per call.
+// A block's 16 rows share one head, so a block stages the token inputs (q
+// and k of the head, v of its rows, gate, beta) 32 tokens at a time in LDS.
+// The reference sums the 128 products of a dot in index order; the tree
+// order and the regrouping differ by rounding only (outputs and state within
+// 1e-5 of the reference's scale).
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "common.hpp"
+
+namespace bh {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kLanesPerRow = 16;
+constexpr int kRowsPerBlock = kBlock / kLanesPerRow;  // 16, never straddling a head
+constexpr int kFast = 128;                            // s of the fast path
+constexpr int kPerLane = kFast / kLanesPerRow;        // 8 state floats per lane
+
+struct GdnStepArgs {
+  const float *q, *k, *v, *gate, *beta;
+  float *state, *attn;
+  size_t n_tok;
+  int h_k, h_v, s;
+  float scale;
+};
+
+// Sum over the 16 lanes of a row group (lanes 16r .. 16r+15), every lane
+// receiving the same total: DPP swaps within quads (xor 1, xor 2), then
+// row_half_mirror (quad pairs) and row_mirror (half rows).  fp addition is
+// commutative, so both partners of each swap hold the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  x += dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+// In-lane part of a dot over the lane's 8 elements, as a depth-3 tree.
+__device__ __forceinline__ float part8(const float (&m)[kPerLane], const float4 a, const float4 b) {
+  const float s0 = m[0] * a.x + m[1] * a.y, s1 = m[2] * a.z + m[3] * a.w;
+  const float s2 = m[4] * b.x + m[5] * b.y, s3 = m[6] * b.z + m[7] * b.w;
+  return (s0 + s1) + (s2 + s3);
+}
+
+// One token on the lane's 8 state floats; returns the row's attn value
+// (valid in every lane of the group).  With d_k = M.k and d_q = M.q on the
+// state before the token, the reference's sequence (decay, delta from the
+// decayed row, outer update, readout from the updated row) is
+//   delta = (v - eg d_k) beta,  M' = eg M + k delta,
+//   M'.q  = eg d_q + delta (k.q),
+// so both row dots come from the old state at once and k.q does not depend
+// on the state (rounding differs from the reference's order only).
+__device__ __forceinline__ float token_step(float (&m)[kPerLane], const float4 k0, const float4 k1,
+                                            const float4 q0, const float4 q1, float v, float g,
+                                            float beta, float scale) {
+  const float eg = expf(g);
+  const float kq = row16_sum(part8({k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w}, q0, q1));
+  const float dk = row16_sum(part8(m, k0, k1));
+  const float dq = row16_sum(part8(m, q0, q1));
+  const float delta = (v - eg * dk) * beta;
+  m[0] = eg * m[0] + k0.x * delta; m[1] = eg * m[1] + k0.y * delta;
+  m[2] = eg * m[2] + k0.z * delta; m[3] = eg * m[3] + k0.w * delta;
+  m[4] = eg * m[4] + k1.x * delta; m[5] = eg * m[5] + k1.y * delta;
+  m[6] = eg * m[6] + k1.z * delta; m[7] = eg * m[7] + k1.w * delta;
+  return (eg * dq + delta * kq) * scale;
+}
+
+__device__ __forceinline__ void load_state(const float *mp, float (&m)[kPerLane]) {
+  const float4 x = reinterpret_cast<const float4 *>(mp)[0];
+  const float4 y = reinterpret_cast<const float4 *>(mp)[1];
+  m[0] = x.x; m[1] = x.y; m[2] = x.z; m[3] = x.w;
+  m[4] = y.x; m[5] = y.y; m[6] = y.z; m[7] = y.w;
+}
+
+__device__ __forceinline__ void store_state(float *mp, const float (&m)[kPerLane]) {
+  float4 *d = reinterpret_cast<float4 *>(mp);
+  d[0] = make_float4(m[0], m[1], m[2], m[3]);
+  d[1] = make_float4(m[4], m[5], m[6], m[7]);
+}
+
+// Few tokens (decode): each lane loads its token inputs straight from
+// global memory, the next token's while the current one computes.
+__global__ __launch_bounds__(kBlock) void gdn_step128_direct_kernel(GdnStepArgs a) {
+  const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;  // h * 128 + j
+  const int sub = threadIdx.x % kLanesPerRow;
+  const int h = row / kFast, j = row % kFast;
+  const int kh = h % a.h_k;
+  float *mp = a.state + static_cast<size_t>(row) * kFast + kPerLane * sub;
+  float m[kPerLane];
+  load_state(mp, m);
+  float4 k0, k1, q0, q1;
+  float v, g, b;
+  auto load_tok = [&](size_t t) {
+    const float4 *kp = reinterpret_cast<const float4 *>(a.k + (t * a.h_k + kh) * kFast) + 2 * sub;
+    const float4 *qp = reinterpret_cast<const float4 *>(a.q + (t * a.h_k + kh) * kFast) + 2 * sub;
+    k0 = kp[0]; k1 = kp[1]; q0 = qp[0]; q1 = qp[1];
+    v = a.v[(t * a.h_v + h) * kFast + j];
+    g = a.gate[t * a.h_v + h];
+    b = a.beta[t * a.h_v + h];
+  };
+  load_tok(0);
+  for (size_t t = 0; t < a.n_tok; ++t) {
+    const float4 ck0 = k0, ck1 = k1, cq0 = q0, cq1 = q1;
+    const float cv = v, cg = g, cb = b;
+    if (t + 1 < a.n_tok) load_tok(t + 1);
+    const float out = token_step(m, ck0, ck1, cq0, cq1, cv, cg, cb, a.scale);
+    if (sub == 0) a.attn[(t * a.h_v + h) * kFast + j] = out;
+  }
+  store_state(mp, m);
+}
+
+// Batches: the token inputs are staged per chunk in LDS (q and k rows of
+// the block's k-head, v of its rows, gate and beta of its v-head, plus
+// expf(gate) and k.q once per token).  Chunk c + 1 is loaded into
+// registers while chunk c runs from LDS, so HBM latency is paid once per
+// chunk.  The loads clamp the token index to the batch (a short last chunk
+// re-reads its last token; those LDS entries are never used), so they need
+// no branches.  A row goes to L lanes of 128 / L floats: L = 16 gives 1536
+// waves for the model's 6144 rows (two waves on the busiest SIMDs hide each
+// other's latency); L = 8 halves the cross-lane work but leaves one wave
+// per SIMD with its dependency chain exposed.
+constexpr int kChunk = 32;
+constexpr size_t kDirectMax = 4;  // token counts that skip the LDS staging
+constexpr int kStagedLanes = 16;  // measured faster than 8 on MI355X
+constexpr int kQkVec = kChunk * 2 * (kFast / 4);  // float4s of q and k per chunk
+constexpr int kQkPerThread = kQkVec / kBlock;     // 8
+constexpr int kDotLanes = kBlock / kChunk;        // 8 lanes per token for k.q
+static_assert(kQkVec % kBlock == 0, "chunk split");
+static_assert(kDotLanes == 8, "k.q is an 8-lane DPP tree");
+
+// Sum over the L lanes of a row (lanes L*r .. L*r + L-1), every lane
+// receiving the same total.
+template <int L>
+__device__ __forceinline__ float row_sum(float x) {
+  static_assert(L == 8 || L == 16, "row sums over 8 or 16 lanes");
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  if (L == 16) x += dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+template <int L>
+struct StagedShape {
+  static constexpr int kPer = kFast / L;        // state floats per lane
+  static constexpr int kVec = kPer / 4;         // float4s per lane
+  static constexpr int kRows = kBlock / L;      // rows per block, one head
+  static constexpr int kVPerThread = kChunk * kRows / kBlock;
+  static_assert((kChunk * kRows) % kBlock == 0 && kFast % kRows == 0, "staged shape");
+};
+
+template <int ROWS>
+struct ChunkLds {
+  float4 qk[kChunk][2][kFast / 4];  // [token][q, k][col4]
+  float v[kChunk][ROWS];
+  float gb[2][kChunk];  // gate, beta as loaded
+  float eg[kChunk];     // expf(gate)
+  float kq[kChunk];     // k . q
+};
+
+template <int ROWS, int VPT>
+__device__ __forceinline__ void load_chunk(const GdnStepArgs &a, f32x4 (&rqk)[kQkPerThread],
+                                           float (&rv)[VPT], float &rgb, size_t t0, int nt, int h,
+                                           int kh, int j0) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < kQkPerThread; ++i) {
+    const int f = tid + kBlock * i;
+    const int tok = min(f / (2 * kFast / 4), nt - 1);
+    const int part = (f / (kFast / 4)) & 1, c4 = f % (kFast / 4);
+    const float *src = (part ? a.k : a.q) + ((t0 + tok) * a.h_k + kh) * kFast;
+    rqk[i] = reinterpret_cast<const f32x4 *>(src)[c4];
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = tid + kBlock * i;
+    const int tok = min(e / ROWS, nt - 1), rr = e % ROWS;
+    rv[i] = a.v[((t0 + tok) * a.h_v + h) * kFast + j0 + rr];
+  }
+  const int tok = min(tid % kChunk, nt - 1);
+  rgb = ((tid / kChunk) & 1 ? a.beta : a.gate)[(t0 + tok) * a.h_v + h];
+}
+
+template <int ROWS, int VPT>
+__device__ __forceinline__ void store_chunk(ChunkLds<ROWS> &l, const f32x4 (&rqk)[kQkPerThread],
+                                            const float (&rv)[VPT], float rgb) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < kQkPerThread; ++i)
+    reinterpret_cast<f32x4 *>(&l.qk[0][0][0])[tid + kBlock * i] = rqk[i];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) (&l.v[0][0])[tid + kBlock * i] = rv[i];
+  if (tid < 2 * kChunk) (&l.gb[0][0])[tid] = rgb;
+}
+
+// Per-token constants of a staged chunk: 8 lanes per token sum 16 products
+// of k.q each, then an 8-lane DPP tree; lane 0 of the 8 also takes expf.
+template <int ROWS>
+__device__ __forceinline__ void chunk_constants(ChunkLds<ROWS> &l) {
+  const int tid = threadIdx.x;
+  const int t = tid / kDotLanes, part = tid % kDotLanes;
+  const float4 *q = l.qk[t][0] + 4 * part;
+  const float4 *k = l.qk[t][1] + 4 * part;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 a = q[i], b = k[i];
+    s += (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w);
+  }
+  s = row_sum<8>(s);
+  if (part == 0) {
+    l.kq[t] = s;
+    l.eg[t] = expf(l.gb[0][t]);
+  }
+}
+
+// In-lane part of a row dot over the lane's 4 * N floats, as a tree.
+template <int N>
+__device__ __forceinline__ float part_dot(const float (&m)[4 * N], const f32x4 (&x)[N]) {
+  float p[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const f32x4 v = x[i];
+    p[i] = (m[4 * i] * v.x + m[4 * i + 1] * v.y) + (m[4 * i + 2] * v.z + m[4 * i + 3] * v.w);
+  }
+#pragma unroll
+  for (int w = 1; w < N; w *= 2)
+#pragma unroll
+    for (int i = 0; i + w < N; i += 2 * w) p[i] += p[i + w];
+  return p[0];
+}
+
+template <int L>
+__global__ __launch_bounds__(kBlock) void gdn_step128_kernel(GdnStepArgs a) {
+  using S = StagedShape<L>;
+  __shared__ ChunkLds<S::kRows> lds;
+  const int row0 = blockIdx.x * S::kRows;  // h * 128 + j0
+  const int rl = threadIdx.x / L;
+  const int sub = threadIdx.x % L;
+  const int h = row0 / kFast, j0 = row0 % kFast;
+  const int kh = h % a.h_k;
+  float *mp = a.state + static_cast<size_t>(row0 + rl) * kFast + S::kPer * sub;
+  float m[S::kPer];
+#pragma unroll
+  for (int i = 0; i < S::kVec; ++i) {
+    const f32x4 x = reinterpret_cast<const f32x4 *>(mp)[i];
+    m[4 * i] = x.x; m[4 * i + 1] = x.y; m[4 * i + 2] = x.z; m[4 * i + 3] = x.w;
+  }
+  f32x4 rqk[kQkPerThread];
+  float rv[S::kVPerThread], rgb;
+  const int n_chunks = static_cast<int>((a.n_tok + kChunk - 1) / kChunk);
+  const int last_len = static_cast<int>(a.n_tok - static_cast<size_t>(n_chunks - 1) * kChunk);
+  load_chunk<S::kRows>(a, rqk, rv, rgb, 0, n_chunks > 1 ? kChunk : last_len, h, kh, j0);
+  for (int c = 0; c < n_chunks; ++c) {
+    const int nt = c + 1 < n_chunks ? kChunk : last_len;
+    __syncthreads();  // the previous chunk's LDS reads are done
+    store_chunk(lds, rqk, rv, rgb);
+    __syncthreads();
+    if (c + 1 < n_chunks)
+      load_chunk<S::kRows>(a, rqk, rv, rgb, static_cast<size_t>(c + 1) * kChunk,
+                           c + 2 < n_chunks ? kChunk : last_len, h, kh, j0);
+    chunk_constants(lds);
+    __syncthreads();
+    float *attn = a.attn + (static_cast<size_t>(c) * kChunk * a.h_v + h) * kFast + j0 + rl;
+    // one token: the algebra of token_step on the lane's floats
+    auto step = [&](int t) {
+      f32x4 kc[S::kVec], qc[S::kVec];
+      const f32x4 *kp = reinterpret_cast<const f32x4 *>(lds.qk[t][1]) + S::kVec * sub;
+      const f32x4 *qp = reinterpret_cast<const f32x4 *>(lds.qk[t][0]) + S::kVec * sub;
+#pragma unroll
+      for (int i = 0; i < S::kVec; ++i) {
+        kc[i] = kp[i];
+        qc[i] = qp[i];
+      }
+      const float eg = lds.eg[t], kq = lds.kq[t], beta = lds.gb[1][t], v = lds.v[t][rl];
+      const float dk = row_sum<L>(part_dot<S::kVec>(m, kc));
+      const float dq = row_sum<L>(part_dot<S::kVec>(m, qc));
+      const float delta = (v - eg * dk) * beta;
+#pragma unroll
+      for (int i = 0; i < S::kVec; ++i) {
+        m[4 * i] = eg * m[4 * i] + kc[i].x * delta;
+        m[4 * i + 1] = eg * m[4 * i + 1] + kc[i].y * delta;
+        m[4 * i + 2] = eg * m[4 * i + 2] + kc[i].z * delta;
+        m[4 * i + 3] = eg * m[4 * i + 3] + kc[i].w * delta;
+      }
+      const float out = (eg * dq + delta * kq) * a.scale;
+      if (sub == 0) attn[static_cast<size_t>(t) * a.h_v * kFast] = out;
+    };
+    // two tokens per pass: the state stays in the same registers
+    for (int t = 0; t < nt; t += 2) {
+      step(t);
+      if (t + 1 < nt) step(t + 1);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < S::kVec; ++i)
+    reinterpret_cast<f32x4 *>(mp)[i] = f32x4{m[4 * i], m[4 * i + 1], m[4 * i + 2], m[4 * i + 3]};
+}
+
+// Any s: one lane per row, the row updated in place in memory, sums in
+// index order as the reference.
+__global__ __launch_bounds__(kBlock) void gdn_step_generic_kernel(GdnStepArgs a) {
+  const int row = blockIdx.x * kBlock + threadIdx.x;
+  if (row >= a.h_v * a.s) return;
+  const int h = row / a.s, j = row % a.s;
+  const int kh = h % a.h_k;
+  float *mr = a.state + static_cast<size_t>(row) * a.s;
+  for (size_t t = 0; t < a.n_tok; ++t) {
+    const float *kv = a.k + (t * a.h_k + kh) * a.s;
+    const float *qv = a.q + (t * a.h_k + kh) * a.s;
+    const float eg = expf(a.gate[t * a.h_v + h]);
+    float sum = 0.0f;
+    for (int i = 0; i < a.s; ++i) {
+      mr[i] *= eg;
+      sum += mr[i] * kv[i];
+    }
+    const float delta = (a.v[(t * a.h_v + h) * a.s + j] - sum) * a.beta[t * a.h_v + h];
+    float so = 0.0f;
+    for (int i = 0; i < a.s; ++i) {
+      mr[i] += kv[i] * delta;
+      so += mr[i] * qv[i];
+    }
+    a.attn[(t * a.h_v + h) * a.s + j] = so * a.scale;
+  }
+}
+
+}  // namespace
+}  // namespace bh
+
+using namespace bh;
+
+extern "C" int bh_gdn_step(const float *q, const float *k, const float *v, const float *gate,
+                           const float *beta, float *state, float *attn, size_t n_tok,
+                           size_t h_k, size_t h_v, size_t s, bh_stream stream) {
+  if (h_k == 0 || h_v == 0 || s == 0)
+    return fail(BH_ERR_SHAPE, "gdn_step: h_k, h_v and s must be positive");
+  if (h_v * s > 0x7fffffffu || h_k * s > 0x7fffffffu)
+    return fail(BH_ERR_SHAPE, "gdn_step: state too large");
+  if (n_tok == 0) return ok();
+  if (!q || !k || !v || !gate || !beta || !state || !attn)
+    return fail(BH_ERR_ARG, "gdn_step: null pointer");
+  GdnStepArgs a{q, k, v, gate, beta, state, attn, n_tok, static_cast<int>(h_k),
+                static_cast<int>(h_v), static_cast<int>(s),
+                1.0f / sqrtf(static_cast<float>(s))};  // src/gdn.rs:31, f32 on the host
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool fast =
+      s == static_cast<size_t>(kFast) && aligned16(q) && aligned16(k) && aligned16(state);
+  if (fast) {
+    const unsigned grid = static_cast<unsigned>(h_v * s / kRowsPerBlock);
+    if (n_tok <= kDirectMax)
+      BH_LAUNCH(gdn_step128_direct_kernel, grid, kBlock, 0, st, a);
+    else
+      BH_LAUNCH(gdn_step128_kernel<kStagedLanes>,
+                static_cast<unsigned>(h_v * s / StagedShape<kStagedLanes>::kRows), kBlock, 0, st, a);
+  } else {
+    const unsigned grid = static_cast<unsigned>((h_v * s + kBlock - 1) / kBlock);
+    BH_LAUNCH(gdn_step_generic_kernel, grid, kBlock, 0, st, a);
+  }
+  return ok();
+}

@@ -317,3 +317,43 @@ extern "C" int bh_host_pq2_matmul_n(const uint8_t *payload, size_t payload_len, 
   if (need > payload_len) return fail(BH_ERR_SHAPE, "pq2_matmul_n: row range exceeds payload");
   return host_matmul_rows(payload, ne0, base_row, n_rows, x, n_tok, y);
 }
+
+extern "C" int bh_host_gdn_step(const float *q, size_t q_len, const float *k, size_t k_len,
+                                const float *v, size_t v_len, const float *gate, size_t gate_len,
+                                const float *beta, size_t beta_len, float *state, size_t state_len,
+                                float *attn, size_t attn_len) {
+  // src/gdn.rs:26-28 fixes the shape; the reference indexes its slices
+  // (panicking when one is short), this entry point reports it instead
+  constexpr size_t S = 128, HK = 16, HV = 48;
+  const struct {
+    const char *name;
+    size_t len, need;
+  } args[] = {{"q", q_len, HK * S},
+              {"k", k_len, HK * S},
+              {"v", v_len, HV * S},
+              {"gate", gate_len, HV},
+              {"beta", beta_len, HV},
+              {"state", state_len, HV * S * S},
+              {"attn", attn_len, HV * S}};
+  for (const auto &a : args)
+    if (a.len < a.need)
+      return fail(BH_ERR_SHAPE, std::string("gdn_step: ") + a.name + " len " +
+                                    std::to_string(a.len) + " < " + std::to_string(a.need));
+  Stream s;
+  if (s.status()) return s.status();
+  DevBuf dq, dk, dv, dg, db, dst, dattn;
+  if (int e = upload(dq, q, HK * S * 4, s.get())) return e;
+  if (int e = upload(dk, k, HK * S * 4, s.get())) return e;
+  if (int e = upload(dv, v, HV * S * 4, s.get())) return e;
+  if (int e = upload(dg, gate, HV * 4, s.get())) return e;
+  if (int e = upload(db, beta, HV * 4, s.get())) return e;
+  if (int e = upload(dst, state, HV * S * S * 4, s.get())) return e;
+  if (int e = dattn.alloc(HV * S * 4)) return e;
+  if (int e = bh_gdn_step(dq.as<float>(), dk.as<float>(), dv.as<float>(), dg.as<float>(),
+                          db.as<float>(), dst.as<float>(), dattn.as<float>(), 1, HK, HV, S,
+                          s.handle()))
+    return e;
+  if (int e = download(state, dst, HV * S * S * 4, s.get())) return e;
+  if (int e = download(attn, dattn, HV * S * 4, s.get())) return e;
+  return ok();
+}

@@ -21,6 +21,8 @@
 //   kernels::pq2_matmul_n(payload, ne0, base, n, x, n_tok, y) -> Result<void>
 //   rope::rope_imrope(head, p_t, p_h, p_w, p_e, n_dims, sections, freq_base)
 //   prefill::batch_embed(payload, ne0, n_rows, tokens) -> Result<std::vector<float>>
+//   gdn::gdn_step(q, k, v, gate, beta, state, attn)
+//   gdn::zero_state()                                  -> std::vector<float>
 //
 // Every call runs on the current HIP device (host memory in, host memory
 // out, synchronous), through the bh_host_* entry points.  A HIP failure is
@@ -198,5 +200,26 @@ inline Result<std::vector<float>> batch_embed(const std::vector<uint8_t> &payloa
 }
 
 }  // namespace prefill
+
+namespace gdn {
+
+// src/gdn.rs:17 (s = 128, h_k = 16, h_v = 48; one token): state advanced in
+// place, attn written.  The reference indexes its slices; a short one throws
+// std::out_of_range here.
+inline void gdn_step(const std::vector<float> &q, const std::vector<float> &k,
+                     const std::vector<float> &v, const std::vector<float> &gate,
+                     const std::vector<float> &beta, std::vector<float> &state,
+                     std::vector<float> &attn) {
+  const int st = bh_host_gdn_step(q.data(), q.size(), k.data(), k.size(), v.data(), v.size(),
+                                  gate.data(), gate.size(), beta.data(), beta.size(),
+                                  state.data(), state.size(), attn.data(), attn.size());
+  if (st == BH_ERR_SHAPE) throw std::out_of_range(bh_last_error());
+  detail::check_or_throw(st);
+}
+
+// src/gdn.rs:80
+inline std::vector<float> zero_state() { return std::vector<float>(48 * 128 * 128, 0.0f); }
+
+}  // namespace gdn
 
 }  // namespace bonsai

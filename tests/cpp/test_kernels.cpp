@@ -267,6 +267,46 @@ int main() {
     }
   });
 
+  // src/gdn.rs has no #[test]; closed forms of gdn_step (src/gdn.rs:17-77):
+  // from zero_state() with gate 0, beta 1 and k = e_i, the update writes v
+  // into column i of each head's state and attn[j] = v[j] q[i] / sqrt(128);
+  // a second step with beta 0 only decays the state by expf(gate)
+  run("gdn_step_closed_forms", [] {
+    const size_t S = 128, HK = 16, HV = 48, i = 7;
+    std::vector<float> q(HK * S), k(HK * S, 0.0f), v(HV * S), gate(HV, 0.0f), beta(HV, 1.0f);
+    for (size_t n = 0; n < q.size(); ++n) q[n] = std::sin(0.37f * n);
+    for (size_t n = 0; n < v.size(); ++n) v[n] = std::cos(0.11f * n);
+    for (size_t h = 0; h < HK; ++h) k[h * S + i] = 1.0f;
+    auto state = gdn::zero_state();
+    std::vector<float> attn(HV * S);
+    gdn::gdn_step(q, k, v, gate, beta, state, attn);
+    const float scale = 1.0f / std::sqrt(128.0f);
+    for (size_t h = 0; h < HV; ++h)
+      for (size_t j = 0; j < S; ++j) {
+        CHECK(state[(h * S + j) * S + i] == v[h * S + j]);
+        CHECK(state[(h * S + j) * S + (i + 1) % S] == 0.0f);
+        CHECK(std::fabs(attn[h * S + j] - v[h * S + j] * q[(h % HK) * S + i] * scale) < 1e-6f);
+      }
+    const auto before = state;
+    for (size_t h = 0; h < HV; ++h) gate[h] = -0.01f * static_cast<float>(h);
+    std::vector<float> zero(HV, 0.0f);
+    gdn::gdn_step(q, k, v, gate, zero, state, attn);
+    for (size_t h = 0; h < HV; ++h)
+      for (size_t j = 0; j < S; ++j) {
+        const float want = before[(h * S + j) * S + i] * std::exp(gate[h]);
+        CHECK(std::fabs(state[(h * S + j) * S + i] - want) <= 1e-6f * std::fabs(want) + 1e-30f);
+      }
+    // a short slice: the reference would panic on its index; here it throws
+    bool threw = false;
+    std::vector<float> short_v(HV * S - 1);
+    try {
+      gdn::gdn_step(q, k, short_v, gate, beta, state, attn);
+    } catch (const std::out_of_range &) {
+      threw = true;
+    }
+    CHECK(threw);
+  });
+
   std::printf("%s: %d failed checks\n", g_fail ? "FAILED" : "OK", g_fail);
   return g_fail ? 1 : 0;
 }

@@ -13,7 +13,7 @@ import pytest
 def test_library_exports_every_header_symbol(bh):
     lib = bh.lib()
     names = bh.header_symbols()
-    assert len(names) == 30
+    assert len(names) == 32
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     # and the Python binding declares a signature for each of them
@@ -214,3 +214,29 @@ def test_pq2_table_distribution(oracle, synth):
     frac = [(codes == c).mean() for c in (0, 1, 2)]
     assert all(abs(f - p) < 0.01 for f, p in zip(frac, (0.3, 0.4, 0.3)))
     assert abs(np.abs(sc).mean() - 0.02 * np.sqrt(2 / np.pi)) < 5e-4
+
+
+def test_gdn_step_argument_errors(bh):
+    """bh_gdn_step checks shapes and pointers before touching the device;
+    zero tokens is a no-op."""
+    lib = bh.lib()
+    assert lib.bh_gdn_step(None, None, None, None, None, None, None, 0, 16, 48, 128, None) == 0
+    assert lib.bh_gdn_step(None, None, None, None, None, None, None, 1, 0, 48, 128,
+                           None) == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "gdn_step: h_k, h_v and s must be positive"
+    assert lib.bh_gdn_step(None, None, None, None, None, None, None, 1, 16, 48, 128,
+                           None) == bh.BH_ERR_ARG
+    assert bh.last_error() == "gdn_step: null pointer"
+
+
+def test_host_gdn_step_short_slices(bh):
+    """bh_host_gdn_step names the first short slice before any device work."""
+    lib = bh.lib()
+    need = dict(q=2048, k=2048, v=6144, gate=48, beta=48, state=48 * 128 * 128, attn=6144)
+    for short in need:
+        lens = [need[n] - (n == short) for n in need]
+        args = []
+        for ln in lens:
+            args += [None, ln]
+        assert lib.bh_host_gdn_step(*args) == bh.BH_ERR_SHAPE
+        assert bh.last_error() == f"gdn_step: {short} len {need[short] - 1} < {need[short]}"

@@ -16,7 +16,7 @@ def test_reference_unit_tests_through_cpp_mirror(dev):
     res = subprocess.run([str(BIN)], capture_output=True, text=True, timeout=120)
     print(res.stdout)
     assert res.returncode == 0, res.stdout + res.stderr
-    assert res.stdout.count("PASS ") == 13 and "FAIL" not in res.stdout
+    assert res.stdout.count("PASS ") == 14 and "FAIL" not in res.stdout
 
 
 def test_cpp_mirror_program_is_built():

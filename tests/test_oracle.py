@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 
 from conftest import rel_err
+from gdndata import gdn_case
 
 
 # --- src/kernels.rs:761-772 rms_norm_matches_reference ----------------------
@@ -491,3 +492,50 @@ def test_conv1d_batched_equals_token_steps(oracle, synth):
     acc = sum(seq[j:j + n_tok] * w[:, j].astype(np.float64) for j in range(k))
     silu64 = acc / (1 + np.exp(-acc))
     assert np.max(np.abs(out - silu64)) / np.max(np.abs(silu64)) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# gated delta-net recurrence (src/gdn.rs:17-77)
+# ---------------------------------------------------------------------------
+
+def test_gdn_step_closed_forms(oracle, synth):
+    """beta = 0: the state only decays, attn = expf(gate) M q / sqrt(s);
+    a zero state, gate 0, beta 1 and k = e_i writes v into column i, so
+    attn[j] = v[j] q[i] / sqrt(s)."""
+    h_k, h_v, s = 2, 4, 16
+    q, k, v, gate, beta, st = gdn_case(synth, 1, h_k, h_v, s, 80)
+    zero = np.zeros_like(beta)
+    attn, st1 = oracle.gdn_step(q, k, v, gate, zero, st)
+    for h in range(h_v):
+        m = (st[h] * np.float32(np.exp(np.float32(gate[0, h])))).astype(np.float64)
+        want = m @ q[0, h % h_k].astype(np.float64) / np.sqrt(s)
+        assert np.allclose(attn[0, h], want, rtol=1e-5, atol=1e-6)
+    assert np.allclose(st1, st * np.exp(gate[0])[:, None, None].astype(np.float32), rtol=1e-6)
+    i = 5
+    k1 = np.zeros_like(k)
+    k1[0, :, i] = 1.0
+    attn, st1 = oracle.gdn_step(q, k1, v, np.zeros_like(gate), np.ones_like(beta),
+                                np.zeros_like(st))
+    for h in range(h_v):
+        assert np.array_equal(st1[h][:, i], v[0, h])
+        assert np.allclose(attn[0, h], v[0, h] * q[0, h % h_k, i] / np.float32(np.sqrt(s)),
+                           rtol=1e-6)
+
+
+def test_gdn_step_matches_float64_recurrence(oracle, synth):
+    """Several tokens: the f32 restatement tracks a float64 evaluation of the
+    same recurrence (a wrong head mapping, a missing decay or a transposed
+    update fails by orders of magnitude)."""
+    n_tok, h_k, h_v, s = 6, 2, 4, 32
+    q, k, v, gate, beta, st = gdn_case(synth, n_tok, h_k, h_v, s, 81)
+    attn, st_new = oracle.gdn_step(q, k, v, gate, beta, st)
+    m = st.astype(np.float64)
+    for t in range(n_tok):
+        for h in range(h_v):
+            kk, qq = k[t, h % h_k].astype(np.float64), q[t, h % h_k].astype(np.float64)
+            m[h] *= np.exp(np.float64(gate[t, h]))
+            delta = (v[t, h] - m[h] @ kk) * beta[t, h]
+            m[h] += np.outer(delta, kk)
+            want = m[h] @ qq / np.sqrt(s)
+            assert np.max(np.abs(attn[t, h] - want)) <= 1e-5 * max(1.0, np.max(np.abs(want)))
+    assert np.max(np.abs(st_new - m)) <= 1e-5 * np.max(np.abs(m))
