@@ -165,6 +165,30 @@ int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream);
 int bh_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok,
                    size_t ch, size_t k, float *out, bh_stream stream);
 
+/* KV cache storage types of bh_kv_store / bh_attention. */
+#define BH_KV_F32 0 /* f32 cache (AttnCache::k / v)                          */
+#define BH_KV_F16 1 /* f16 bits (AttnCache::k16 / v16, BONSAI_KV=f16)        */
+
+/* AttnCache::append / append_f16 (src/forward.rs:90-95, 120-125) for n_tok
+ * tokens: rows k, v [n_tok][n_kv_elems] (f32) are written at positions
+ * pos0 .. pos0 + n_tok - 1 of the caches [cap][n_kv_elems], as f32 or as
+ * gguf::f32_to_half bits (src/gguf.rs:914-944, bit for bit). */
+int bh_kv_store(const float *k, const float *v, size_t n_tok, size_t n_kv_elems,
+                void *k_cache, void *v_cache, size_t pos0, int kv_dtype, bh_stream stream);
+
+/* The GQA block of full_attention_layer (src/forward.rs:282-375) for n_q
+ * query tokens at positions pos0 .. pos0 + n_q - 1: query i, head hq reads
+ * kv head hq / (n_head / n_kv) over cache positions 0 .. pos0 + i;
+ * scores = q.k / sqrtf(hd), probs = softmax_rows(scores), out = probs . V.
+ * q, out: [n_q][n_head][hd] f32; caches [>= pos0 + n_q][n_kv * hd] of
+ * kv_dtype, the query tokens' own rows already stored.  hd = 256 with
+ * n_head / n_kv in {1, 2, 3, 4, 6, 8} and 16-byte aligned pointers takes the
+ * split-position kernels; anything else a per-head kernel with the
+ * reference's softmax sequence.  Uses library scratch. */
+int bh_attention(const float *q, size_t n_q, size_t pos0, const void *k_cache,
+                 const void *v_cache, int kv_dtype, size_t n_head, size_t n_kv, size_t hd,
+                 float *out, bh_stream stream);
+
 /* Gated delta-net recurrence over n_tok tokens (src/gdn.rs:17-77, gdn_step,
  * applied per token; the reference fixes s = 128, h_k = 16, h_v = 48).  Per
  * token t and v-head h (q/k head h % h_k), with M = state[h] (s x s, row j

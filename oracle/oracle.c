@@ -375,6 +375,76 @@ void or_gdn_step(const float *q, const float *k, const float *v, const float *ga
   free(delta);
 }
 
+/* ---- attention over a KV cache (src/forward.rs:273-375) ------------------ */
+
+/* AttnCache::append / append_f16, src/forward.rs:90-95, 120-125: the rows of
+ * n_tok tokens (n_kv_elems floats each) land at positions pos0 .. of the
+ * cache, f32 or converted by gguf::f32_to_half. */
+void or_kv_store(const float *k, const float *v, size_t n_tok, size_t n_kv_elems, void *k_cache,
+                 void *v_cache, size_t pos0, int kv_f16) {
+  size_t n = n_tok * n_kv_elems, base = pos0 * n_kv_elems;
+  for (size_t i = 0; i < n; ++i) {
+    if (kv_f16) {
+      ((uint16_t *)k_cache)[base + i] = or_f32_to_half(k[i]);
+      ((uint16_t *)v_cache)[base + i] = or_f32_to_half(v[i]);
+    } else {
+      ((float *)k_cache)[base + i] = k[i];
+      ((float *)v_cache)[base + i] = v[i];
+    }
+  }
+}
+
+static float kv_at(const void *cache, int kv_f16, size_t i) {
+  return kv_f16 ? or_half_to_f32(((const uint16_t *)cache)[i]) : ((const float *)cache)[i];
+}
+
+/* The GQA block of full_attention_layer, src/forward.rs:282-375, for n_q
+ * query tokens at positions pos0 .. pos0 + n_q - 1 (one call per token in
+ * the reference; token i sees cache positions 0 .. pos0 + i).  Per q head
+ * hq (kv head hq / (n_head / n_kv)): scores[j] = dot(q, k_j) * scale with
+ * dot / dot_f16 (:181-191: f32 products summed in index order) and scale =
+ * 1 / sqrtf(hd) (:282); probs = softmax_rows (:326); out[d] = sum_j p_j *
+ * v_j[d] in position order, skipping p_j == 0 (:361-371, f16 :349-360). */
+int or_attention(const float *q, size_t n_q, size_t pos0, const void *k_cache,
+                 const void *v_cache, int kv_f16, size_t n_head, size_t n_kv, size_t hd,
+                 float *out) {
+  if (n_kv == 0 || hd == 0 || n_head % n_kv != 0) return OR_ERR_SHAPE;
+  size_t n_rep = n_head / n_kv, n_kv_elems = n_kv * hd, n_max = pos0 + n_q;
+  float scale = 1.0f / sqrtf((float)hd);
+  float *scores = (float *)malloc((n_max ? n_max : 1) * sizeof(float));
+  float *probs = (float *)malloc((n_max ? n_max : 1) * sizeof(float));
+  if (scores == NULL || probs == NULL) {
+    free(scores);
+    free(probs);
+    return OR_ERR_SHAPE;
+  }
+  for (size_t i = 0; i < n_q; ++i) {
+    size_t n_pos = pos0 + i + 1;
+    for (size_t hq = 0; hq < n_head; ++hq) {
+      const float *qh = q + (i * n_head + hq) * hd;
+      size_t kv_off = (hq / n_rep) * hd;
+      for (size_t j = 0; j < n_pos; ++j) {
+        float sum = 0.0f;
+        size_t row = j * n_kv_elems + kv_off;
+        for (size_t d = 0; d < hd; ++d) sum += qh[d] * kv_at(k_cache, kv_f16, row + d);
+        scores[j] = sum * scale;
+      }
+      or_softmax_rows(scores, n_pos, n_pos, 1.0f, probs);
+      float *o = out + (i * n_head + hq) * hd;
+      for (size_t d = 0; d < hd; ++d) o[d] = 0.0f;
+      for (size_t j = 0; j < n_pos; ++j) {
+        float pj = probs[j];
+        if (pj == 0.0f) continue;
+        size_t row = j * n_kv_elems + kv_off;
+        for (size_t d = 0; d < hd; ++d) o[d] += pj * kv_at(v_cache, kv_f16, row + d);
+      }
+    }
+  }
+  free(scores);
+  free(probs);
+  return OR_OK;
+}
+
 /* ---- PQ2_0 products (src/kernels.rs:233-423) ------------------------------ */
 
 /* row_dot_scalar, src/kernels.rs:633-653: per 128-block an f32 sum of

@@ -95,6 +95,11 @@ void or_conv1d_silu(const float *x, float *state, const float *w, size_t n_tok, 
                     size_t k, float *out);
 
 /* src/gdn.rs:17-77 over n_tok tokens; state [h_v][s][s] in/out */
+void or_kv_store(const float *k, const float *v, size_t n_tok, size_t n_kv_elems, void *k_cache,
+                 void *v_cache, size_t pos0, int kv_f16);
+int or_attention(const float *q, size_t n_q, size_t pos0, const void *k_cache,
+                 const void *v_cache, int kv_f16, size_t n_head, size_t n_kv, size_t hd,
+                 float *out);
 void or_gdn_step(const float *q, const float *k, const float *v, const float *gate,
                  const float *beta, float *state, float *attn, size_t n_tok, size_t h_k,
                  size_t h_v, size_t s);

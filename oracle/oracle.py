@@ -46,6 +46,8 @@ _SIG = {
     "or_silu_l2_part": (ctypes.c_int, [_vp, _sz, _sz, _sz, _sz, _f, _vp]),
     "or_pq2_row_dot": (_f, [_vp, _sz, _vp]),
     "or_conv1d_silu": (None, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "or_kv_store": (None, [_vp, _vp, _sz, _sz, _vp, _vp, _sz, ctypes.c_int]),
+    "or_attention": (ctypes.c_int, [_vp, _sz, _sz, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp]),
     "or_gdn_step": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz]),
     "or_pq2_matmul_n": (None, [_vp, _sz, ctypes.c_uint64, _sz, _vp, _sz, _vp]),
 }
@@ -242,6 +244,41 @@ def gdn_step(q, k, v, gate, beta, state):
     lib().or_gdn_step(_p(q), _p(k), _p(v), _p(gate), _p(beta), _p(st), _p(attn), n_tok, h_k,
                       h_v, s)
     return attn, st
+
+
+def kv_store(k, v, k_cache, v_cache, pos0: int):
+    """AttnCache::append / append_f16 (src/forward.rs:90-95, 120-125): rows
+    k, v [n_tok, n_kv_elems] into copies of the caches [cap, n_kv_elems]
+    (float32, or uint16 f16 bits) at positions pos0 ..; returns the copies."""
+    k, v = _c(k), _c(v)
+    f16 = k_cache.dtype == np.uint16
+    kc = np.ascontiguousarray(k_cache).copy()
+    vc = np.ascontiguousarray(v_cache).copy()
+    n_tok, elems = k.shape
+    if v.shape != k.shape or kc.shape != vc.shape or kc.shape[1] != elems or \
+            pos0 + n_tok > kc.shape[0] or kc.dtype != vc.dtype:
+        raise OracleShapeError("kv_store shape")
+    lib().or_kv_store(_p(k), _p(v), n_tok, elems, _p(kc), _p(vc), pos0, int(f16))
+    return kc, vc
+
+
+def attention(q, pos0: int, k_cache, v_cache, n_kv: int):
+    """The GQA block of full_attention_layer (src/forward.rs:282-375) for
+    queries q [n_q, n_head, hd] at positions pos0 .. pos0 + n_q - 1 over
+    caches [>= pos0 + n_q, n_kv * hd] (float32, or uint16 f16 bits);
+    returns out [n_q, n_head, hd]."""
+    q = _c(q)
+    n_q, n_head, hd = q.shape
+    f16 = k_cache.dtype == np.uint16
+    kc, vc = np.ascontiguousarray(k_cache), np.ascontiguousarray(v_cache)
+    if kc.shape != vc.shape or kc.dtype != vc.dtype or kc.shape[1] != n_kv * hd or \
+            kc.shape[0] < pos0 + n_q or (f16 is False and kc.dtype != np.float32):
+        raise OracleShapeError("attention shape")
+    out = np.empty_like(q)
+    if lib().or_attention(_p(q), n_q, pos0, _p(kc), _p(vc), int(f16), n_head, n_kv, hd,
+                          _p(out)) != 0:
+        raise OracleShapeError("attention heads")
+    return out
 
 
 def pq2_row_dot(raw, ne0: int, x) -> float:

@@ -121,6 +121,9 @@ _SIGNATURES = {
     "bh_conv1d_silu": (_c_int, [_vp, _vp, _vp, _c_size, _c_size, _c_size, _vp, _vp]),
     "bh_host_gdn_step": (_c_int, [_vp, _c_size, _vp, _c_size, _vp, _c_size, _vp, _c_size, _vp,
                                   _c_size, _vp, _c_size, _vp, _c_size]),
+    "bh_kv_store": (_c_int, [_vp, _vp, _c_size, _c_size, _vp, _vp, _c_size, _c_int, _vp]),
+    "bh_attention": (_c_int, [_vp, _c_size, _c_size, _vp, _vp, _c_int, _c_size, _c_size, _c_size,
+                              _vp, _vp]),
     "bh_gdn_step": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_size, _c_size,
                              _c_size, _vp]),
     "bh_pq2_matvec_range": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp,
@@ -323,6 +326,39 @@ def conv1d_silu(x, state, w, out=None, stream=None):
     out = torch.empty_like(x) if out is None else out
     check(lib().bh_conv1d_silu(x.data_ptr(), _ptr(state), w.data_ptr(), n_tok, ch, k,
                                out.data_ptr(), _stream(stream)))
+    return out
+
+
+BH_KV_F32, BH_KV_F16 = 0, 1
+
+
+def _kv_dtype(cache):
+    import torch
+    if cache.dtype == torch.float32:
+        return BH_KV_F32
+    if cache.dtype in (torch.float16, torch.int16, torch.uint16):
+        return BH_KV_F16
+    raise TypeError(f"KV cache dtype {cache.dtype}: f32 or 16-bit f16 storage")
+
+
+def kv_store(k, v, k_cache, v_cache, pos0: int, stream=None):
+    """AttnCache::append / append_f16 (src/forward.rs:90-95, 120-125): rows
+    k, v [n_tok, n_kv_elems] f32 into the caches [cap, n_kv_elems] (f32, or
+    16-bit tensors holding f16 bits) at positions pos0 .."""
+    n_tok, elems = k.shape
+    check(lib().bh_kv_store(k.data_ptr(), v.data_ptr(), n_tok, elems, k_cache.data_ptr(),
+                            v_cache.data_ptr(), pos0, _kv_dtype(k_cache), _stream(stream)))
+
+
+def attention(q, pos0: int, k_cache, v_cache, n_kv: int, out=None, stream=None):
+    """The GQA block of full_attention_layer (src/forward.rs:282-375) for
+    queries q [n_q, n_head, hd] at positions pos0 ..; caches [cap, n_kv*hd]."""
+    import torch
+    n_q, n_head, hd = q.shape
+    out = torch.empty_like(q) if out is None else out
+    check(lib().bh_attention(q.data_ptr(), n_q, pos0, k_cache.data_ptr(), v_cache.data_ptr(),
+                             _kv_dtype(k_cache), n_head, n_kv, hd, out.data_ptr(),
+                             _stream(stream)))
     return out
 
 

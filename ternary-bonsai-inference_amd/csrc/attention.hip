@@ -1,0 +1,508 @@
+// Grouped-query attention over a KV cache, and the cache append.
+//
+// Reference: full_attention_layer, src/forward.rs:273-375 (one token per
+// call): the token's k/v rows are appended at position pos (:273-287,
+// AttnCache::append / append_f16 :90-95, 120-125); then for every q head hq
+// (kv head hq / (n_head / n_kv)): scores[j] = dot(q, k_j) * (1 / sqrtf(hd))
+// over the pos + 1 cached positions (dot / dot_f16 :181-191), probs =
+// softmax_rows(scores) (:326), out[d] = sum_j probs[j] * v_j[d], skipping
+// probs[j] == 0 (:361-371, f16 cache :349-360).
+//
+// bh_attention takes n_q query tokens at positions pos0 .. pos0 + n_q - 1
+// (query i sees positions 0 .. pos0 + i, as the reference's token loop).
+//
+// Decode path (hd = 256, n_head / n_kv in {1, 2, 3, 4, 6, 8}): the
+// positions of one (query, kv head) are split into chunks, one block each.
+// A block keeps the q slices of the kv head's REP q heads in registers and
+// runs 64-position tiles: scores with 16 lanes per position (16 dims per
+// lane, DPP row sums) into LDS, the tile's max and exponentials once per
+// tile (running max and sum per head, the accumulators rescaled once per
+// tile), then P.V with each lane owning 4 output dims of every head and the
+// four waves taking every fourth position, so K and V are each read once.
+// A second launch merges the chunks' (max, sum, acc) triples.  Results are
+// the reference's up to rounding (sums in another order); a non-finite v at
+// a position whose probability underflows to 0 is not skipped here.
+//
+// Generic path (any hd and grouping, any alignment): one block per (query,
+// head) computes the scores, the reference's softmax (f32 max, expf, f64
+// sum, inv = 1 / (f32)sum, p = e * inv) into scratch; a second launch forms
+// P.V in position order, skipping p == 0 -- the reference's sequence, with
+// only the f64 sum reduced as a tree.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <string>
+
+#include "common.hpp"
+
+namespace bh {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kHd = 256;        // head size of the decode path
+constexpr int kTile = 64;       // positions per tile
+constexpr int kQkLanes = 16;    // lanes per position in the score pass
+constexpr int kQkPer = kHd / kQkLanes;  // 16 dims per lane
+
+// gguf::f32_to_half (src/gguf.rs:914-944) in integer arithmetic: NaN keeps
+// only a quiet bit, overflow goes to inf, the subnormal range shifts the
+// mantissa before rounding to nearest even on the 13 dropped bits.
+__device__ __forceinline__ uint32_t f32_to_half_bits(float v) {
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t sign = (b >> 16) & 0x8000u;
+  const int exp = static_cast<int>((b >> 23) & 0xffu);
+  const uint32_t man = b & 0x7fffffu;
+  if (exp == 0xff) return sign | 0x7c00u | (man != 0u ? 0x200u : 0u);
+  const int e = exp - 127 + 15;
+  if (e >= 0x1f) return sign | 0x7c00u;
+  uint32_t half, rem;
+  if (e <= 0) {
+    if (e < -10) return sign;
+    const uint32_t m = (man | 0x800000u) >> (1 - e);
+    half = m >> 13;
+    rem = m & 0x1fffu;
+  } else {
+    half = (static_cast<uint32_t>(e) << 10) | (man >> 13);
+    rem = man & 0x1fffu;
+  }
+  const uint32_t up = (rem > 0x1000u || (rem == 0x1000u && (half & 1u) != 0u)) ? 1u : 0u;
+  return sign | ((half + up) & 0xffffu);
+}
+
+__device__ __forceinline__ float half_to_float(uint32_t h) {
+  return __uint_as_float(half_bits_to_f32_bits(h));
+}
+
+// Cache element access for the two storage types.
+template <class T>
+struct Kv;
+
+template <>
+struct Kv<float> {
+  static __device__ __forceinline__ float at(const float *c, size_t e) { return c[e]; }
+  // 4 values at e (a multiple of 4)
+  static __device__ __forceinline__ f32x4 load4(const float *c, size_t e) {
+    return *reinterpret_cast<const f32x4 *>(c + e);
+  }
+};
+
+template <>
+struct Kv<uint16_t> {
+  static __device__ __forceinline__ float at(const uint16_t *c, size_t e) {
+    return half_to_float(c[e]);
+  }
+  static __device__ __forceinline__ f32x4 load4(const uint16_t *c, size_t e) {
+    const uint2 u = *reinterpret_cast<const uint2 *>(c + e);
+    return f32x4{half_to_float(u.x & 0xffffu), half_to_float(u.x >> 16),
+                 half_to_float(u.y & 0xffffu), half_to_float(u.y >> 16)};
+  }
+};
+
+// ---- KV append -------------------------------------------------------------
+
+template <class T>
+__global__ __launch_bounds__(kBlock) void kv_store_kernel(const float *k, const float *v,
+                                                          size_t n, T *kc, T *vc) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= n) return;
+  if constexpr (sizeof(T) == 2) {
+    kc[i] = static_cast<T>(f32_to_half_bits(k[i]));
+    vc[i] = static_cast<T>(f32_to_half_bits(v[i]));
+  } else {
+    kc[i] = k[i];
+    vc[i] = v[i];
+  }
+}
+
+// ---- decode path -----------------------------------------------------------
+
+struct DecodeArgs {
+  const float *q;
+  const void *kc, *vc;
+  float *pm, *pl, *pacc;  // chunk partials [n_q][n_head][n_chunks] (+ [hd])
+  size_t pos0, kv_stride, chunk;
+  int n_head, n_chunks;
+  float scale;
+};
+
+template <int L>
+__device__ __forceinline__ float dpp_row(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), L, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane gets the same bits.
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_row<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_row<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_row<0x141>(x);  // row_half_mirror
+  x += dpp_row<0x140>(x);  // row_mirror
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+template <int REP, class T>
+__global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
+  constexpr int kSlots = (REP + 3) / 4;  // heads owned per wave for the softmax state
+  __shared__ float s_e[kTile][REP];       // scores, then exponentials
+  __shared__ float s_corr[REP];
+  __shared__ float s_acc[4][REP][kHd];
+  const T *kc = static_cast<const T *>(a.kc);
+  const T *vc = static_cast<const T *>(a.vc);
+  const int c = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const size_t n_pos = a.pos0 + i + 1;
+  const size_t beg = static_cast<size_t>(c) * a.chunk;
+  const size_t end = beg + a.chunk < n_pos ? beg + a.chunk : n_pos;
+  const size_t part0 = (static_cast<size_t>(i) * a.n_head + static_cast<size_t>(g) * REP) *
+                       a.n_chunks + c;  // + r * n_chunks
+  if (beg >= end) {  // this query has no positions in the chunk
+    if (tid < REP) {
+      a.pm[part0 + static_cast<size_t>(tid) * a.n_chunks] = -INFINITY;
+      a.pl[part0 + static_cast<size_t>(tid) * a.n_chunks] = 0.0f;
+    }
+    for (int o = tid; o < REP * kHd; o += kBlock)
+      a.pacc[(part0 + static_cast<size_t>(o / kHd) * a.n_chunks) * kHd + o % kHd] = 0.0f;
+    return;
+  }
+  const int grp = tid / kQkLanes, sub = tid % kQkLanes;
+  float qr[REP][kQkPer];
+#pragma unroll
+  for (int r = 0; r < REP; ++r) {
+    const f32x4 *qp = reinterpret_cast<const f32x4 *>(
+        a.q + (static_cast<size_t>(i) * a.n_head + g * REP + r) * kHd + kQkPer * sub);
+#pragma unroll
+    for (int x = 0; x < kQkPer / 4; ++x) {
+      const f32x4 f = qp[x];
+      qr[r][4 * x] = f.x;
+      qr[r][4 * x + 1] = f.y;
+      qr[r][4 * x + 2] = f.z;
+      qr[r][4 * x + 3] = f.w;
+    }
+  }
+  float run_m[kSlots], run_l[kSlots];
+#pragma unroll
+  for (int u = 0; u < kSlots; ++u) {
+    run_m[u] = -INFINITY;
+    run_l[u] = 0.0f;
+  }
+  float acc[REP][4];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) acc[r][x] = 0.0f;
+  const size_t head_off = static_cast<size_t>(g) * kHd;
+
+  for (size_t t0 = beg; t0 < end; t0 += kTile) {
+    // scores: 16 lanes per position, 4 passes of 16 positions
+    f32x4 kr[4][kQkPer / 4];
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const size_t p = t0 + pass * 16 + grp;
+      const size_t e0 = (p < end ? p : end - 1) * a.kv_stride + head_off + kQkPer * sub;
+#pragma unroll
+      for (int x = 0; x < kQkPer / 4; ++x) kr[pass][x] = Kv<T>::load4(kc, e0 + 4 * x);
+    }
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+      const size_t p = t0 + pass * 16 + grp;
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        float part[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const f32x4 kv = kr[pass][x];
+          part[x] = (qr[r][4 * x] * kv.x + qr[r][4 * x + 1] * kv.y) +
+                    (qr[r][4 * x + 2] * kv.z + qr[r][4 * x + 3] * kv.w);
+        }
+        const float d = row16_sum((part[0] + part[1]) + (part[2] + part[3]));
+        if (sub == 0) s_e[pass * 16 + grp][r] = p < end ? d * a.scale : -INFINITY;
+      }
+    }
+    __syncthreads();
+    // softmax state: wave w owns heads w, w + 4
+#pragma unroll
+    for (int u = 0; u < kSlots; ++u) {
+      const int r = w + 4 * u;
+      if (r < REP) {
+        const float s = s_e[lane][r];
+        const float m_new = fmaxf(run_m[u], wave_max(s));
+        const bool none = m_new == -INFINITY;
+        const float corr = none ? 1.0f : expf(run_m[u] - m_new);
+        const float e = none ? 0.0f : expf(s - m_new);
+        s_e[lane][r] = e;
+        run_l[u] = run_l[u] * corr + wave_sum(e);
+        run_m[u] = m_new;
+        if (lane == 0) s_corr[r] = corr;
+      }
+    }
+    __syncthreads();
+    // P.V: lane owns dims 4*lane .. +3, wave w takes positions w, w+4, ...
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const float cr = s_corr[r];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) acc[r][x] *= cr;
+    }
+    const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kTile) ? end - t0 : kTile);
+    for (int j = w; j < nt; j += 4) {
+      const f32x4 v = Kv<T>::load4(vc, (t0 + j) * a.kv_stride + head_off + 4 * lane);
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        const float e = s_e[j][r];
+        acc[r][0] += e * v.x;
+        acc[r][1] += e * v.y;
+        acc[r][2] += e * v.z;
+        acc[r][3] += e * v.w;
+      }
+    }
+    __syncthreads();  // s_e and s_corr are rewritten by the next tile
+  }
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) s_acc[w][r][4 * lane + x] = acc[r][x];
+#pragma unroll
+  for (int u = 0; u < kSlots; ++u) {
+    const int r = w + 4 * u;
+    if (r < REP && lane == 0) {
+      a.pm[part0 + static_cast<size_t>(r) * a.n_chunks] = run_m[u];
+      a.pl[part0 + static_cast<size_t>(r) * a.n_chunks] = run_l[u];
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < REP * kHd; o += kBlock) {
+    const int r = o / kHd, d = o % kHd;
+    const float sum = (s_acc[0][r][d] + s_acc[1][r][d]) + (s_acc[2][r][d] + s_acc[3][r][d]);
+    a.pacc[(part0 + static_cast<size_t>(r) * a.n_chunks) * kHd + d] = sum;
+  }
+}
+
+// out[i][h][d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M).
+__global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *pm, const float *pl,
+                                                              const float *pacc, int n_chunks,
+                                                              int hd, float *out) {
+  const size_t row = static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x;  // i * n_head + h
+  const float *m = pm + row * n_chunks;
+  const float *l = pl + row * n_chunks;
+  float big = -INFINITY;
+  for (int c = 0; c < n_chunks; ++c) big = fmaxf(big, m[c]);
+  float den = 0.0f;
+  for (int c = 0; c < n_chunks; ++c)
+    if (m[c] != -INFINITY) den += l[c] * expf(m[c] - big);
+  const float inv = 1.0f / den;
+  for (int d = threadIdx.x; d < hd; d += kBlock) {
+    float num = 0.0f;
+    for (int c = 0; c < n_chunks; ++c)
+      if (m[c] != -INFINITY) num += pacc[(row * n_chunks + c) * hd + d] * expf(m[c] - big);
+    out[row * hd + d] = num * inv;
+  }
+}
+
+// ---- generic path ----------------------------------------------------------
+
+struct GenericArgs {
+  const float *q;
+  const void *kc, *vc;
+  float *probs;  // [n_q][n_head][n_max]
+  float *out;
+  size_t pos0, n_max, kv_stride, hd;
+  int n_head, n_rep;
+  float scale;
+};
+
+// One block per (query, head): scores, max, expf, f64 sum, p = e * inv.
+// Each lane only rereads the probs entries it wrote itself.
+template <class T>
+__global__ __launch_bounds__(kBlock) void attn_probs_kernel(GenericArgs a) {
+  __shared__ float s_max[kBlock / 64];
+  __shared__ double s_sum[kBlock / 64];
+  const T *kc = static_cast<const T *>(a.kc);
+  const int h = blockIdx.x, i = blockIdx.y;
+  const int tid = threadIdx.x;
+  const size_t n_pos = a.pos0 + i + 1;
+  const float *qh = a.q + (static_cast<size_t>(i) * a.n_head + h) * a.hd;
+  const size_t kv_off = static_cast<size_t>(h / a.n_rep) * a.hd;
+  float *pr = a.probs + (static_cast<size_t>(i) * a.n_head + h) * a.n_max;
+  float mx = -INFINITY;
+  for (size_t j = tid; j < n_pos; j += kBlock) {
+    float sum = 0.0f;
+    const size_t row = j * a.kv_stride + kv_off;
+    for (size_t d = 0; d < a.hd; ++d) sum += qh[d] * Kv<T>::at(kc, row + d);  // :181-183
+    const float s = sum * a.scale;
+    pr[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = wave_max(mx);
+  if (tid % 64 == 0) s_max[tid / 64] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+  double part = 0.0;
+  for (size_t j = tid; j < n_pos; j += kBlock) {
+    const float e = expf(pr[j] - mx);
+    pr[j] = e;
+    part += static_cast<double>(e);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
+  if (tid % 64 == 0) s_sum[tid / 64] = part;
+  __syncthreads();
+  const double total = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
+  const float inv = 1.0f / static_cast<float>(total);
+  for (size_t j = tid; j < n_pos; j += kBlock) pr[j] *= inv;
+}
+
+// out[d] = sum_j p_j v_j[d] in position order, skipping p_j == 0.
+template <class T>
+__global__ __launch_bounds__(kBlock) void attn_pv_kernel(GenericArgs a) {
+  const T *vc = static_cast<const T *>(a.vc);
+  const int h = blockIdx.x, i = blockIdx.y;
+  const size_t d = static_cast<size_t>(blockIdx.z) * kBlock + threadIdx.x;
+  if (d >= a.hd) return;
+  const size_t n_pos = a.pos0 + i + 1;
+  const size_t kv_off = static_cast<size_t>(h / a.n_rep) * a.hd;
+  const float *pr = a.probs + (static_cast<size_t>(i) * a.n_head + h) * a.n_max;
+  float o = 0.0f;
+  for (size_t j = 0; j < n_pos; ++j) {
+    const float p = pr[j];
+    if (p == 0.0f) continue;
+    o += p * Kv<T>::at(vc, j * a.kv_stride + kv_off + d);
+  }
+  a.out[(static_cast<size_t>(i) * a.n_head + h) * a.hd + d] = o;
+}
+
+template <int REP, class T>
+int launch_decode(const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
+  BH_LAUNCH((attn_decode_kernel<REP, T>), dim3(a.n_chunks, n_kv, n_q), kBlock, 0, st, a);
+  return ok();
+}
+
+template <class T>
+int decode_dispatch(int rep, const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
+  switch (rep) {
+    case 1: return launch_decode<1, T>(a, n_kv, n_q, st);
+    case 2: return launch_decode<2, T>(a, n_kv, n_q, st);
+    case 3: return launch_decode<3, T>(a, n_kv, n_q, st);
+    case 4: return launch_decode<4, T>(a, n_kv, n_q, st);
+    case 6: return launch_decode<6, T>(a, n_kv, n_q, st);
+    case 8: return launch_decode<8, T>(a, n_kv, n_q, st);
+    default: return fail(BH_ERR_ARG, "attention: no decode kernel for this grouping");
+  }
+}
+
+bool decode_rep(size_t rep) {
+  return rep == 1 || rep == 2 || rep == 3 || rep == 4 || rep == 6 || rep == 8;
+}
+
+}  // namespace
+}  // namespace bh
+
+using namespace bh;
+
+extern "C" int bh_kv_store(const float *k, const float *v, size_t n_tok, size_t n_kv_elems,
+                           void *k_cache, void *v_cache, size_t pos0, int kv_dtype,
+                           bh_stream stream) {
+  if (kv_dtype != BH_KV_F32 && kv_dtype != BH_KV_F16)
+    return fail(BH_ERR_ARG, "kv_store: kv_dtype must be BH_KV_F32 or BH_KV_F16");
+  const size_t n = n_tok * n_kv_elems;
+  if (n == 0) return ok();
+  if (n_kv_elems != 0 && n / n_kv_elems != n_tok) return fail(BH_ERR_SHAPE, "kv_store: size overflow");
+  if (!k || !v || !k_cache || !v_cache) return fail(BH_ERR_ARG, "kv_store: null pointer");
+  const size_t esz = kv_dtype == BH_KV_F16 ? 2 : 4;
+  char *kc = static_cast<char *>(k_cache) + pos0 * n_kv_elems * esz;
+  char *vc = static_cast<char *>(v_cache) + pos0 * n_kv_elems * esz;
+  const size_t blocks = (n + kBlock - 1) / kBlock;
+  if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "kv_store: too many elements");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (kv_dtype == BH_KV_F16)
+    BH_LAUNCH(kv_store_kernel<uint16_t>, static_cast<unsigned>(blocks), kBlock, 0, st, k, v, n,
+              reinterpret_cast<uint16_t *>(kc), reinterpret_cast<uint16_t *>(vc));
+  else
+    BH_LAUNCH(kv_store_kernel<float>, static_cast<unsigned>(blocks), kBlock, 0, st, k, v, n,
+              reinterpret_cast<float *>(kc), reinterpret_cast<float *>(vc));
+  return ok();
+}
+
+extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void *k_cache,
+                            const void *v_cache, int kv_dtype, size_t n_head, size_t n_kv,
+                            size_t hd, float *out, bh_stream stream) {
+  if (kv_dtype != BH_KV_F32 && kv_dtype != BH_KV_F16)
+    return fail(BH_ERR_ARG, "attention: kv_dtype must be BH_KV_F32 or BH_KV_F16");
+  if (n_kv == 0 || hd == 0 || n_head == 0 || n_head % n_kv != 0)
+    return fail(BH_ERR_SHAPE, "attention: n_head " + std::to_string(n_head) +
+                                  " must be a positive multiple of n_kv " + std::to_string(n_kv) +
+                                  " and hd positive");
+  if (n_q == 0) return ok();
+  if (!q || !k_cache || !v_cache || !out) return fail(BH_ERR_ARG, "attention: null pointer");
+  const size_t n_max = pos0 + n_q;
+  if (n_head > 65535 || n_q > 65535 || n_kv > 65535 || n_max > (size_t{1} << 40) ||
+      hd > (size_t{1} << 20))
+    return fail(BH_ERR_SHAPE, "attention: sizes out of range");
+  const size_t rep = n_head / n_kv;
+  const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // src/forward.rs:282
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool f16 = kv_dtype == BH_KV_F16;
+  const size_t kv_stride = n_kv * hd;
+  const size_t esz = f16 ? 2 : 4;
+
+  const bool fast = hd == static_cast<size_t>(kHd) && decode_rep(rep) && aligned16(q) &&
+                    (reinterpret_cast<uintptr_t>(k_cache) % (4 * esz)) == 0 &&
+                    (reinterpret_cast<uintptr_t>(v_cache) % (4 * esz)) == 0;
+  if (fast) {
+    // chunks of whole tiles; about 1024 blocks over (chunk, kv head, query)
+    const size_t tiles = (n_max + kTile - 1) / kTile;
+    const size_t want = (1024 + n_kv * n_q - 1) / (n_kv * n_q);
+    const size_t per = (tiles + want - 1) / want;
+    const size_t chunk = per * kTile;
+    const size_t n_chunks = (n_max + chunk - 1) / chunk;
+    if (n_chunks > 65535) return fail(BH_ERR_SHAPE, "attention: too many positions");
+    const size_t rows = n_q * n_head * n_chunks;
+    float *scratch = static_cast<float *>(device_scratch(rows * (kHd + 2) * 4, kScratchAttention));
+    if (scratch == nullptr) return BH_ERR_HIP;
+    DecodeArgs a{q,
+                 k_cache,
+                 v_cache,
+                 scratch,
+                 scratch + rows,
+                 scratch + 2 * rows,
+                 pos0,
+                 kv_stride,
+                 chunk,
+                 static_cast<int>(n_head),
+                 static_cast<int>(n_chunks),
+                 scale};
+    const int e = f16 ? decode_dispatch<uint16_t>(static_cast<int>(rep), a, static_cast<int>(n_kv),
+                                                  static_cast<int>(n_q), st)
+                      : decode_dispatch<float>(static_cast<int>(rep), a, static_cast<int>(n_kv),
+                                               static_cast<int>(n_q), st);
+    if (e) return e;
+    BH_LAUNCH(attn_combine_kernel, dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q)),
+              kBlock, 0, st, a.pm, a.pl, a.pacc, static_cast<int>(n_chunks), kHd, out);
+    return ok();
+  }
+  float *probs = static_cast<float *>(device_scratch(n_q * n_head * n_max * 4, kScratchAttention));
+  if (probs == nullptr) return BH_ERR_HIP;
+  GenericArgs a{q, k_cache, v_cache, probs, out, pos0, n_max, kv_stride, hd,
+                static_cast<int>(n_head), static_cast<int>(rep), scale};
+  const dim3 grid(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q));
+  const dim3 grid_pv(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q),
+                     static_cast<unsigned>((hd + kBlock - 1) / kBlock));
+  if (f16) {
+    BH_LAUNCH(attn_probs_kernel<uint16_t>, grid, kBlock, 0, st, a);
+    BH_LAUNCH(attn_pv_kernel<uint16_t>, grid_pv, kBlock, 0, st, a);
+  } else {
+    BH_LAUNCH(attn_probs_kernel<float>, grid, kBlock, 0, st, a);
+    BH_LAUNCH(attn_pv_kernel<float>, grid_pv, kBlock, 0, st, a);
+  }
+  return ok();
+}

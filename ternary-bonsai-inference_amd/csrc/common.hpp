@@ -49,7 +49,8 @@ inline int pow2ceil(size_t v) {
 // nullptr on allocation failure (the status is already recorded).
 constexpr int kScratchSoftmax = 0;  // split-row softmax partials
 constexpr int kScratchMatmul = 1;   // PQ2_0 product: f16 x fragments, token scales
-constexpr int kScratchSlots = 2;
+constexpr int kScratchAttention = 2;  // attention: chunk partials or probabilities
+constexpr int kScratchSlots = 3;
 void *device_scratch(size_t bytes, int slot);
 
 

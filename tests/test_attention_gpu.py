@@ -1,0 +1,161 @@
+"""GPU parity of the KV append (bh_kv_store) and of grouped-query attention
+over the cache (bh_attention) against the oracle's restatement of
+src/forward.rs:273-375 (the reference's one-token loop, run per query).
+
+Bars: the f32 store bit for bit, the f16 store = gguf::f32_to_half bit for
+bit (specials and the subnormal range included); attention outputs
+max|gpu-ref| / max(|ref|, |gpu|) <= 1e-5 (scores and P.V summed in another
+order; the generic path keeps the reference's sequence except the f64 sum's
+order).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+MODEL = (24, 4, 256)  # n_head, n_kv, hd of the model (24 q / 4 kv heads x 256)
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _t(a, dev):
+    import torch
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+
+def _h(t):
+    import torch
+    torch.cuda.synchronize()
+    a = t.cpu().numpy()
+    return a.view(np.uint16) if a.dtype == np.int16 else a
+
+
+def _case(synth, n_q, pos0, n_head, n_kv, hd, seed, qscale=2.0):
+    r = synth.Rng(seed)
+    n = pos0 + n_q
+    q = r.normal(n_q * n_head * hd).reshape(n_q, n_head, hd) * np.float32(qscale)
+    kc = r.normal(n * n_kv * hd).reshape(n, n_kv * hd)
+    vc = r.normal(n * n_kv * hd).reshape(n, n_kv * hd)
+    return q.astype(np.float32), kc, vc
+
+
+def _run(bh, dev, q, pos0, kc, vc, n_kv):
+    return _h(bh.attention(_t(q, dev), pos0, _t(kc, dev), _t(vc, dev), n_kv))
+
+
+@pytest.mark.parametrize("n_q,pos0,f16", [
+    (1, 0, False), (1, 6, False), (1, 63, False), (1, 64, False), (1, 999, False),
+    (1, 4095, False), (1, 4095, True), (1, 130, True),
+    (3, 100, False),     # a few tokens at once (speculative verification)
+    (17, 0, False),      # a causal batch from the first position
+    (64, 2000, True),
+])
+def test_attention_model_heads(bh, oracle, synth, dev, n_q, pos0, f16):
+    n_head, n_kv, hd = MODEL
+    _say("attention", n_q, pos0, "f16" if f16 else "f32")
+    q, kc, vc = _case(synth, n_q, pos0, n_head, n_kv, hd, 300 + n_q + pos0)
+    if f16:
+        kc = kc.astype(np.float16).view(np.uint16)
+        vc = vc.astype(np.float16).view(np.uint16)
+    ref = oracle.attention(q, pos0, kc, vc, n_kv)
+    got = _run(bh, dev, q, pos0, kc, vc, n_kv)
+    err = rel_err(got, ref)
+    _say("  rel", err)
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,n_q,pos0", [
+    (8, 2, 256, 2, 50),    # grouping 4
+    (8, 8, 256, 1, 300),   # grouping 1
+    (16, 2, 256, 1, 70),   # grouping 8
+    (6, 2, 64, 3, 40),     # other head size: generic path
+    (5, 1, 80, 2, 9),      # grouping 5, hd 80: generic path
+    (12, 4, 256, 1, 33),   # grouping 3
+])
+def test_attention_other_shapes(bh, oracle, synth, dev, n_head, n_kv, hd, n_q, pos0):
+    _say("attention shape", n_head, n_kv, hd, n_q, pos0)
+    q, kc, vc = _case(synth, n_q, pos0, n_head, n_kv, hd, 400 + hd + pos0)
+    ref = oracle.attention(q, pos0, kc, vc, n_kv)
+    assert rel_err(_run(bh, dev, q, pos0, kc, vc, n_kv), ref) <= TOL
+
+
+def test_attention_unaligned_q_uses_generic(bh, oracle, synth, dev):
+    import torch
+    n_head, n_kv, hd = MODEL
+    q, kc, vc = _case(synth, 1, 20, n_head, n_kv, hd, 500)
+    buf = torch.zeros(q.size + 1, dtype=torch.float32, device=dev)
+    buf[1:] = _t(q.reshape(-1), dev)
+    got = _h(bh.attention(buf[1:].view(q.shape), 20, _t(kc, dev), _t(vc, dev), n_kv))
+    assert rel_err(got, oracle.attention(q, 20, kc, vc, n_kv)) <= TOL
+
+
+def test_attention_generic_skips_zero_probabilities(bh, oracle, synth, dev):
+    """The generic path keeps src/forward.rs:363-366: a position whose
+    probability is exactly 0 is skipped, so an inf in its v row does not
+    reach the output."""
+    q, kc, vc = _case(synth, 1, 1, 1, 1, 4, 501)
+    q[0, 0] = [100.0, 0.0, 0.0, 0.0]
+    kc[0] = [-100.0, 0.0, 0.0, 0.0]
+    kc[1] = [100.0, 0.0, 0.0, 0.0]
+    vc[0] = np.inf
+    ref = oracle.attention(q, 1, kc, vc, 1)
+    got = _run(bh, dev, q, 1, kc, vc, 1)
+    assert np.array_equal(got, ref)
+
+
+def test_kv_store_bits(bh, oracle, synth, dev):
+    """f32 rows copied exactly; f16 rows = gguf::f32_to_half, including NaN,
+    inf, overflow, ties and the subnormal range, at an offset position."""
+    import torch
+    r = synth.Rng(502)
+    n_tok, elems, cap, pos0 = 3, 1024, 8, 4
+    k = r.normal(n_tok * elems).reshape(n_tok, elems) * np.float32(3.0)
+    v = r.normal(n_tok * elems).reshape(n_tok, elems)
+    special = np.array([np.nan, np.inf, -np.inf, 65504.0, 65520.0, 1e6, -0.0, 1e-8, 6e-8,
+                        3e-8, 2.98e-8, 5.96e-8, 1e-5, -6.1e-5, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11,
+                        0.1, 1e-40], dtype=np.float32)
+    k[0, :special.size] = special
+    v[1, :special.size] = special[::-1]
+    for f16 in (False, True):
+        dt = np.uint16 if f16 else np.float32
+        kc0 = np.zeros((cap, elems), dt)
+        vc0 = np.zeros((cap, elems), dt)
+        want_k, want_v = oracle.kv_store(k, v, kc0, vc0, pos0)
+        dk, dv = _t(kc0, dev), _t(vc0, dev)
+        bh.kv_store(_t(k, dev), _t(v, dev), dk, dv, pos0)
+        gk, gv = _h(dk), _h(dv)
+        assert np.array_equal(gk.view(np.uint32 if not f16 else np.uint16),
+                              want_k.view(np.uint32 if not f16 else np.uint16))
+        assert np.array_equal(gv.view(np.uint32 if not f16 else np.uint16),
+                              want_v.view(np.uint32 if not f16 else np.uint16))
+
+
+def test_store_then_attend_token_loop(bh, oracle, synth, dev):
+    """The reference's decode loop: per token, append k/v at pos then attend
+    with n_q = 1; the same caches and outputs as one 6-token batch call."""
+    import torch
+    n_head, n_kv, hd = MODEL
+    n_tok = 6
+    r = synth.Rng(503)
+    q = r.normal(n_tok * n_head * hd).reshape(n_tok, n_head, hd)
+    k = r.normal(n_tok * n_kv * hd).reshape(n_tok, n_kv * hd)
+    v = r.normal(n_tok * n_kv * hd).reshape(n_tok, n_kv * hd)
+    dk = torch.zeros((n_tok, n_kv * hd), device=dev)
+    dv = torch.zeros_like(dk)
+    outs = []
+    for t in range(n_tok):
+        bh.kv_store(_t(k[t:t + 1], dev), _t(v[t:t + 1], dev), dk, dv, t)
+        outs.append(_h(bh.attention(_t(q[t:t + 1], dev), t, dk, dv, n_kv)))
+    ref = oracle.attention(q, 0, k, v, n_kv)
+    assert rel_err(np.concatenate(outs), ref) <= TOL
+    batch = _h(bh.attention(_t(q, dev), 0, dk, dv, n_kv))
+    assert rel_err(batch, ref) <= TOL

@@ -13,7 +13,7 @@ import pytest
 def test_library_exports_every_header_symbol(bh):
     lib = bh.lib()
     names = bh.header_symbols()
-    assert len(names) == 32
+    assert len(names) == 34
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     # and the Python binding declares a signature for each of them
@@ -240,3 +240,16 @@ def test_host_gdn_step_short_slices(bh):
             args += [None, ln]
         assert lib.bh_host_gdn_step(*args) == bh.BH_ERR_SHAPE
         assert bh.last_error() == f"gdn_step: {short} len {need[short] - 1} < {need[short]}"
+
+
+def test_attention_argument_errors(bh):
+    lib = bh.lib()
+    assert lib.bh_attention(None, 0, 0, None, None, 0, 24, 4, 256, None, None) == 0
+    assert lib.bh_attention(None, 1, 0, None, None, 0, 24, 5, 256, None, None) == bh.BH_ERR_SHAPE
+    assert "multiple of n_kv 5" in bh.last_error()
+    assert lib.bh_attention(None, 1, 0, None, None, 2, 24, 4, 256, None, None) == bh.BH_ERR_ARG
+    assert lib.bh_attention(None, 1, 0, None, None, 0, 24, 4, 256, None, None) == bh.BH_ERR_ARG
+    assert bh.last_error() == "attention: null pointer"
+    assert lib.bh_kv_store(None, None, 0, 1024, None, None, 0, 1, None) == 0
+    assert lib.bh_kv_store(None, None, 1, 1024, None, None, 0, 1, None) == bh.BH_ERR_ARG
+    assert lib.bh_kv_store(None, None, 1, 1024, None, None, 0, 7, None) == bh.BH_ERR_ARG

@@ -539,3 +539,101 @@ def test_gdn_step_matches_float64_recurrence(oracle, synth):
             want = m[h] @ qq / np.sqrt(s)
             assert np.max(np.abs(attn[t, h] - want)) <= 1e-5 * max(1.0, np.max(np.abs(want)))
     assert np.max(np.abs(st_new - m)) <= 1e-5 * np.max(np.abs(m))
+
+
+# ---- attention over a KV cache (src/forward.rs:273-375) ---------------------
+
+def _attn_case(synth, n_q, pos0, n_head, n_kv, hd, seed, cap=None):
+    r = synth.Rng(seed)
+    cap = pos0 + n_q if cap is None else cap
+    q = r.normal(n_q * n_head * hd).reshape(n_q, n_head, hd)
+    kc = r.normal(cap * n_kv * hd).reshape(cap, n_kv * hd)
+    vc = r.normal(cap * n_kv * hd).reshape(cap, n_kv * hd)
+    return q, kc, vc
+
+
+def _attn_f64(q, pos0, kc, vc, n_kv):
+    """float64 softmax(q k^T / sqrt(hd)) v per query, causal, GQA head
+    hq -> hq // (n_head / n_kv)."""
+    n_q, n_head, hd = q.shape
+    rep = n_head // n_kv
+    out = np.zeros((n_q, n_head, hd))
+    for i in range(n_q):
+        n = pos0 + i + 1
+        for h in range(n_head):
+            g = h // rep
+            k = kc[:n, g * hd:(g + 1) * hd].astype(np.float64)
+            v = vc[:n, g * hd:(g + 1) * hd].astype(np.float64)
+            s = k @ q[i, h].astype(np.float64) / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            out[i, h] = (p / p.sum()) @ v
+    return out
+
+
+def test_attention_closed_forms(oracle, synth):
+    """One cache position: the output is v_0 exactly (p = 1).  Identical
+    keys: uniform probabilities, the output is the mean of the v rows."""
+    q, kc, vc = _attn_case(synth, 1, 0, 4, 2, 16, 100)
+    out = oracle.attention(q, 0, kc, vc, 2)
+    for h in range(4):
+        assert np.array_equal(out[0, h], vc[0, (h // 2) * 16:(h // 2 + 1) * 16])
+    q, kc, vc = _attn_case(synth, 1, 9, 4, 2, 16, 101)
+    kc[:] = kc[0]
+    out = oracle.attention(q, 9, kc, vc, 2)
+    for h in range(4):
+        want = vc[:10, (h // 2) * 16:(h // 2 + 1) * 16].astype(np.float64).mean(0)
+        assert np.allclose(out[0, h], want, rtol=0, atol=1e-6)
+
+
+def test_attention_matches_float64(oracle, synth):
+    """Several causal queries over a GQA cache (6 q heads on 2 kv heads: the
+    mappings h // 3 and h % 2 differ) against a float64 evaluation."""
+    n_q, pos0, n_head, n_kv, hd = 5, 7, 6, 2, 32
+    q, kc, vc = _attn_case(synth, n_q, pos0, n_head, n_kv, hd, 102)
+    q *= 2.0
+    out = oracle.attention(q, pos0, kc, vc, n_kv)
+    want = _attn_f64(q, pos0, kc, vc, n_kv)
+    assert rel_err(out, want) <= 1e-6
+
+
+def test_attention_is_causal(oracle, synth):
+    """Query i reads positions 0 .. pos0 + i only: rewriting later rows of
+    the cache leaves it unchanged."""
+    q, kc, vc = _attn_case(synth, 3, 4, 4, 1, 8, 103, cap=12)
+    out = oracle.attention(q, 4, kc, vc, 1)
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[5:], vc2[5:] = 1e3, -1e3
+    out2 = oracle.attention(q, 4, kc2, vc2, 1)
+    assert np.array_equal(out[0], out2[0])
+    assert not np.array_equal(out[1], out2[1])
+
+
+def test_kv_store_and_f16_cache(oracle, synth):
+    """append_f16 stores gguf::f32_to_half (= IEEE round to nearest even for
+    normal-range values, as numpy's float16); attention over an f16 cache is
+    attention over the f32 cache of the widened values, bit for bit."""
+    n_q, pos0, n_head, n_kv, hd = 2, 3, 4, 2, 16
+    q, kc, vc = _attn_case(synth, n_q, pos0, n_head, n_kv, hd, 104)
+    k16 = np.zeros(kc.shape, np.uint16)
+    v16 = np.zeros(vc.shape, np.uint16)
+    k16, v16 = oracle.kv_store(kc, vc, k16, v16, 0)
+    assert np.array_equal(k16, kc.astype(np.float16).view(np.uint16))
+    kf = np.zeros_like(kc)
+    kf, vf = oracle.kv_store(kc[2:4], vc[2:4], kf, np.zeros_like(vc), 2)
+    assert np.array_equal(kf[2:4], kc[2:4]) and not kf[:2].any() and not kf[4:].any()
+    wide_k = k16.view(np.float16).astype(np.float32)
+    wide_v = v16.view(np.float16).astype(np.float32)
+    assert np.array_equal(oracle.attention(q, pos0, k16, v16, n_kv),
+                          oracle.attention(q, pos0, wide_k, wide_v, n_kv))
+
+
+def test_attention_skips_zero_probabilities(oracle, synth):
+    """src/forward.rs:363-366 skips p_j == 0: a position whose score is
+    ~1e4 below the maximum contributes nothing, not 0 * inf."""
+    q, kc, vc = _attn_case(synth, 1, 1, 1, 1, 4, 105)
+    q[0, 0] = [100.0, 0.0, 0.0, 0.0]
+    kc[0] = [-100.0, 0.0, 0.0, 0.0]
+    kc[1] = [100.0, 0.0, 0.0, 0.0]
+    vc[0] = np.inf
+    out = oracle.attention(q, 1, kc, vc, 1)
+    assert np.array_equal(out[0, 0], vc[1])
