@@ -23,6 +23,7 @@ import argparse
 import importlib.util
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -273,6 +274,36 @@ def wl_gather_rms(bh, synth, dev, stream, n_tok=8192, vocab=248320, ne0=5120):
     return launch, len(sets), bytes_per, n_tok, (table, w, sets)
 
 
+def wl_attention(bh, synth, dev, stream, n_q, pos0, f16, n_head=24, n_kv=4, hd=256):
+    """Grouped-query attention over the KV cache (src/forward.rs:282-375) for
+    n_q query tokens at positions pos0 .. on the model's heads (24 q / 4 kv x
+    256).  Algorithmic bytes: the K and V rows of positions 0 .. pos0+n_q-1
+    read once (f32 or f16 storage), q read and out written once."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    n_pos = pos0 + n_q
+    esz = 2 if f16 else 4
+    bytes_per = 2 * n_pos * n_kv * hd * esz + 2 * n_q * n_head * hd * 4
+    dt = torch.float16 if f16 else torch.float32
+    sets = []
+    for _ in range(n_sets(bytes_per)):
+        sets.append((torch.randn((n_q, n_head, hd), device=dev, generator=g),
+                     torch.randn((n_pos, n_kv * hd), device=dev, generator=g).to(dt),
+                     torch.randn((n_pos, n_kv * hd), device=dev, generator=g).to(dt),
+                     torch.empty((n_q, n_head, hd), device=dev)))
+    lib, sh = bh.lib(), stream.cuda_stream
+    kvd = bh.BH_KV_F16 if f16 else bh.BH_KV_F32
+
+    def launch(i):
+        q, kc, vc, out = sets[i]
+        st = lib.bh_attention(q.data_ptr(), n_q, pos0, kc.data_ptr(), vc.data_ptr(), kvd,
+                              n_head, n_kv, hd, out.data_ptr(), sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, n_q, sets
+
+
 def wl_pq2_matmul(bh, synth, dev, stream, n_rows, ne0, n_tok):
     """kernels::pq2_matmul_n / pq2_matvec_range (src/kernels.rs:283-423):
     Y[n_tok][n_rows] = X[n_tok][ne0] * W^T over a PQ2_0 weight tensor.  Each
@@ -408,7 +439,7 @@ def main() -> int:
     ap.add_argument("--headline-only", action="store_true",
                     help="time only the headline kernel (profiling runs)")
     ap.add_argument("--only", default="",
-                    help="after the headline, time only the entries whose name contains this")
+                    help="after the headline, time only the entries whose name matches this regex")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="length of the CPU-baseline sample (0 disables)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -465,6 +496,14 @@ def main() -> int:
                 ("pq2_gather_rms T=8192", lambda: wl_gather_rms(bh, synth, dev, stream)),
                 ("gdn_step decode T=1", lambda: wl_gdn_step(bh, synth, dev, stream, 1)),
                 ("gdn_step T=256", lambda: wl_gdn_step(bh, synth, dev, stream, 256)),
+                ("attention decode ctx=4096 f32",
+                 lambda: wl_attention(bh, synth, dev, stream, 1, 4095, False)),
+                ("attention decode ctx=32768 f32",
+                 lambda: wl_attention(bh, synth, dev, stream, 1, 32767, False)),
+                ("attention decode ctx=32768 f16",
+                 lambda: wl_attention(bh, synth, dev, stream, 1, 32767, True)),
+                ("attention batch 64 queries ctx=4096 f32",
+                 lambda: wl_attention(bh, synth, dev, stream, 64, 4032, False)),
             ]
             products = [  # (name, rows, ne0, tokens): decode matvecs and batched products
                 ("pq2_matvec LM head [248320x5120] N=1", 248320, 5120, 1),
@@ -474,10 +513,10 @@ def main() -> int:
                 ("pq2_matmul_n LM head [248320x5120] N=16", 248320, 5120, 16),
             ]
             for name, wl in entries:
-                if args.only in name:
+                if re.search(args.only, name):
                     kernels.append(measure(name, wl(), ksteps, args.warmup, stream))
             for name, rows, ne0, n_tok in products:
-                if args.only in name:
+                if re.search(args.only, name):
                     kernels.append(measure_mm(name, rows, ne0, n_tok, bh, synth, dev, stream,
                                               ksteps, args.warmup))
 

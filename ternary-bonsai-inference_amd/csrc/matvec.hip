@@ -520,6 +520,249 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Integer product for the staged shapes (16-byte aligned rows, block count a
+// multiple of 8, at most kI8Tok tokens per token group).
+//
+// x side: each (token, 128-block) is scaled by the power of two 2^e that
+// puts its largest |x| in [2^21, 2^22) and rounded to integers X (22
+// significant bits), written as three signed base-256 digits
+// X = 65536 d0 + 256 d1 + d2 (|d0| <= 65, |d1|, |d2| <= 128).  The codes
+// (0..3) are exact int8, so one v_mfma_i32_16x16x64_i8 step sums
+// code * digit exactly in i32; a block is two steps.  The three digits of a
+// token are three A rows of the same MFMA (A row m = 4 * token + digit, the
+// fourth row of each token unused), so one decode of the codes serves every
+// digit and up to 4 tokens, and lane (n, g) ends the block holding token
+// g's three digit sums for weight row n.  Then
+//     sum_j X_j (code_j - 1) = 65536 S0 + 256 S1 + S2 - sum_j X_j
+// exactly (|value| <= 2^30, i32 arithmetic, the wrap of the partial terms
+// cancels), converted to f32 once, multiplied by 2^-e (exact) and
+// accumulated as the reference adds scale * block_sum (src/kernels.rs:651).
+//
+// Codes: a dword holds codes c0..c15 (2 bits each, c0 lowest).  Bytes
+// (w >> 2k) & 0x03030303 are c_k, c_{4+k}, c_{8+k}, c_{12+k}: fragment dword
+// k, byte i carries code 4i + k.  The x digits are laid out in the same
+// slot order, so the MFMA pairs x_j with code_j.
+// ---------------------------------------------------------------------------
+constexpr int kI8Tok = 4;  // tokens per MFMA (A rows 4t .. 4t + 3)
+typedef int i4v __attribute__((ext_vector_type(4)));
+
+struct PrepI8Args {
+  const float *x;  // [n_tok][ne0]
+  uint4 *afrag;    // [group][step][lane group][16 A rows] x 16 bytes
+  float2 *bfac;    // [group][block][token in group]: (bits of sum X, 2^-e)
+  int ne0, n_tok, nblk;
+};
+
+// 8 lanes per (token, block); lane (g, h) builds the 16-byte fragment of
+// step 2b + h for lane group g: block columns 16 (2g + h) .. +15.
+__global__ __launch_bounds__(kMmThreads) void pq2_i8_prep_kernel(PrepI8Args a) {
+  const int item = blockIdx.x * kMmThreads + threadIdx.x;
+  const int tb = item >> 3, sub = item & 7;
+  const bool live = tb < a.n_tok * a.nblk;
+  const int t = live ? tb / a.nblk : 0, blk = live ? tb - t * a.nblk : 0;
+  const int g = sub >> 1, h = sub & 1;
+  const float4 *xr = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(t) * a.ne0 +
+                                                      128 * blk + 16 * (2 * g + h));
+  float f[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 v = live ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    f[4 * q] = v.x;
+    f[4 * q + 1] = v.y;
+    f[4 * q + 2] = v.z;
+    f[4 * q + 3] = v.w;
+  }
+  float mx = 0.0f;
+  int bad = 0;  // a NaN or infinity in the block
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const bool fin = __builtin_isfinite(f[c]);
+    bad |= !fin;
+    f[c] = fin ? f[c] : 0.0f;
+    mx = fmaxf(mx, fabsf(f[c]));
+  }
+#pragma unroll
+  for (int off = 4; off > 0; off >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    bad |= __shfl_xor(bad, off, 64);
+  }
+  int ex = 0;
+  if (mx > 0.0f) {
+    int k;
+    (void)frexpf(mx, &k);  // mx = f * 2^k, f in [0.5, 1): mx * 2^(22-k) in [2^21, 2^22)
+    ex = 22 - k;
+    ex = ex > 126 ? 126 : ex;  // tiny blocks round toward zero; 2^-e stays normal
+  }
+  const float s = ldexpf(1.0f, ex);
+  uint32_t dg[3][4] = {};
+  int sx = 0;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const int X = static_cast<int>(rintf(f[c] * s));  // |X| <= 2^22
+    sx += X;
+    const int d2 = ((X + 128) & 0xff) - 128;
+    const int x1 = (X - d2) >> 8;
+    const int d1 = ((x1 + 128) & 0xff) - 128;
+    const int d0 = (x1 - d1) >> 8;
+    const int k = c & 3, i = c >> 2;  // dword k, byte i holds column 4i + k
+    dg[0][k] |= (static_cast<uint32_t>(d0) & 0xffu) << (8 * i);
+    dg[1][k] |= (static_cast<uint32_t>(d1) & 0xffu) << (8 * i);
+    dg[2][k] |= (static_cast<uint32_t>(d2) & 0xffu) << (8 * i);
+  }
+#pragma unroll
+  for (int off = 4; off > 0; off >>= 1) sx += __shfl_xor(sx, off, 64);
+  if (!live) return;
+  const int grp = t / kI8Tok, tq = t % kI8Tok;
+  const int nsteps = 2 * a.nblk;
+  uint4 *dst = a.afrag + ((static_cast<size_t>(grp) * nsteps + 2 * blk + h) * 4 + g) * 16 + 4 * tq;
+#pragma unroll
+  for (int d = 0; d < 3; ++d) dst[d] = make_uint4(dg[d][0], dg[d][1], dg[d][2], dg[d][3]);
+  if (sub == 0)
+    a.bfac[(static_cast<size_t>(grp) * a.nblk + blk) * kI8Tok + tq] =
+        make_float2(__int_as_float(sx), bad ? __builtin_nanf("") : ldexpf(1.0f, -ex));
+}
+
+struct MmI8Args {
+  const uint8_t *w;  // first row of the range
+  const uint4 *afrag;
+  const float2 *bfac;
+  float *y;  // [n_tok][y_stride]
+  size_t row_bytes;
+  int n_rows, nblk, n_tok, y_stride;
+};
+
+__device__ __forceinline__ i4v decode_i8(uint32_t d) {
+  return i4v{static_cast<int>(d & 0x03030303u), static_cast<int>((d >> 2) & 0x03030303u),
+             static_cast<int>((d >> 4) & 0x03030303u), static_cast<int>((d >> 6) & 0x03030303u)};
+}
+
+// Workgroup = RT row tiles x KS waves each; wave (rt, ks) streams the chunks
+// c = ks, ks + KS, ... of row tile blockIdx.x * RT + rt through its private
+// LDS stage, and the KS partial sums of a tile are added in ks order at the
+// end.  The fragments of the (single) token group and its block factors are
+// copied to LDS once per workgroup, only the A rows of live tokens.
+template <int KS, int RT>
+__global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
+  constexpr int kWaves = KS * RT;
+  extern __shared__ uint4 smem[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int rt = wave / KS, ks = wave - rt * KS;
+  const int row0 = (blockIdx.x * RT + rt) * 16;
+  const int nsteps = 2 * a.nblk;
+
+  const int arows = 4 * a.n_tok;  // live A rows (n_tok <= kI8Tok)
+  const int total = nsteps * 4 * arows;
+  for (int i = threadIdx.x; i < total; i += 64 * kWaves) {
+    const int m = i % arows, sg = i / arows;  // sg = step * 4 + lane group
+    smem[i] = a.afrag[static_cast<size_t>(sg) * 16 + m];
+  }
+  float2 *bf = reinterpret_cast<float2 *>(smem + total);
+  for (int i = threadIdx.x; i < a.nblk * kI8Tok; i += 64 * kWaves) bf[i] = a.bfac[i];
+  const size_t a_words = static_cast<size_t>(total) + (static_cast<size_t>(a.nblk) * kI8Tok + 1) / 2;
+  // rows of absent tokens and the unused fourth digit row feed D rows that
+  // are never read: any in-bounds fragment will do
+  const uint4 *al = smem + g * arows + (n < arows ? n : (n & 3));
+  const float2 *bl = bf + g;
+  uint8_t *stage = reinterpret_cast<uint8_t *>(smem + a_words) + wave * kStageWaveBytes;
+
+  const uint8_t *src[kStageLoads];
+  int dst[kStageLoads];
+  bool live[kStageLoads];
+#pragma unroll
+  for (int k = 0; k < kStageLoads; ++k) {
+    const int idx = lane + 64 * k;
+    live[k] = idx < 16 * kStageF4;
+    const int r = live[k] ? idx / kStageF4 : 0, c16 = live[k] ? idx % kStageF4 : 0;
+    int row = row0 + r;
+    row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
+    src[k] = a.w + static_cast<size_t>(row) * a.row_bytes + 16 * c16;
+    dst[k] = r * kStageStride + 16 * c16;
+  }
+  uint4 regs[kStageLoads];
+  auto gload = [&](int chunk) {
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k)
+      if (live[k]) regs[k] = *reinterpret_cast<const uint4 *>(src[k] + static_cast<size_t>(chunk) * kStageRowBytes);
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k) {
+      if (live[k]) {
+        uint2 *d = reinterpret_cast<uint2 *>(stage + dst[k]);  // 8-byte aligned
+        d[0] = make_uint2(regs[k].x, regs[k].y);
+        d[1] = make_uint2(regs[k].z, regs[k].w);
+      }
+    }
+  };
+
+  float tot = 0.0f;
+  const int n_chunks = a.nblk / kStageBlocks;
+  int c = ks;
+  if (c < n_chunks) gload(c);
+  __syncthreads();  // x staging visible to every wave
+  if (c < n_chunks) {
+    lstore();
+    if (c + KS < n_chunks) gload(c + KS);
+  }
+  for (; c < n_chunks; c += KS) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint8_t *rowp = stage + n * kStageStride;
+#pragma unroll 2
+    for (int bb = 0; bb < kStageBlocks; ++bb) {
+      const int b = c * kStageBlocks + bb;
+      const uint8_t *blk = rowp + kPq2Blk * bb;
+      uint32_t cd0, cd1;
+      float sc;
+      if ((bb & 1) == 0) {  // block starts on a dword: codes are 2 bytes in
+        const uint32_t e0 = lds_u32(blk + 8 * g), e1 = lds_u32(blk + 8 * g + 4),
+                       e2 = lds_u32(blk + 8 * g + 8);
+        cd0 = __builtin_amdgcn_alignbyte(e1, e0, 2);
+        cd1 = __builtin_amdgcn_alignbyte(e2, e1, 2);
+        sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk))));
+      } else {  // block starts 2 bytes into a dword: codes are dword-aligned
+        cd0 = lds_u32(blk + 2 + 8 * g);
+        cd1 = lds_u32(blk + 6 + 8 * g);
+        sc = static_cast<float>(
+            __builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk - 2) >> 16)));
+      }
+      const i4v a0 = __builtin_bit_cast(i4v, al[(2 * b) * 4 * arows]);
+      const i4v a1 = __builtin_bit_cast(i4v, al[(2 * b + 1) * 4 * arows]);
+      const float2 f = bl[b * kI8Tok];
+      i4v acc = i4v{0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, decode_i8(cd0), acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, decode_i8(cd1), acc, 0, 0, 0);
+      const uint32_t v = (static_cast<uint32_t>(acc[0]) << 16) + (static_cast<uint32_t>(acc[1]) << 8) +
+                         static_cast<uint32_t>(acc[2]) - __float_as_uint(f.x);
+      const float blk_sum = static_cast<float>(static_cast<int>(v)) * f.y;  // times 2^-e: exact
+      tot = fmaf(blk_sum, sc, tot);  // src/kernels.rs:651: acc += scale * block_acc
+    }
+    if (c + KS < n_chunks) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      lstore();  // chunk c + KS replaces chunk c (this wave finished reading it)
+      if (c + 2 * KS < n_chunks) gload(c + 2 * KS);
+    }
+  }
+
+  const int row = row0 + n;
+  if constexpr (KS > 1) {
+    __syncthreads();  // every wave is done with its stage: reuse the LDS
+    float *part = reinterpret_cast<float *>(smem);
+    part[wave * 64 + lane] = tot;
+    __syncthreads();
+    if (ks == 0) {
+      float s = part[(rt * KS) * 64 + lane];
+#pragma unroll
+      for (int k = 1; k < KS; ++k) s += part[(rt * KS + k) * 64 + lane];  // fixed order
+      tot = s;
+    }
+  }
+  if (ks == 0 && g < a.n_tok && row < a.n_rows) a.y[static_cast<size_t>(g) * a.y_stride + row] = tot;
+}
+
 // Any ne0 or alignment: the scalar reference loop (src/kernels.rs:633-653),
 // one wave per (row, token), lanes over blocks, block sums in order, then a
 // fixed-order reduction of the lanes' scale * block_sum terms.
@@ -592,6 +835,52 @@ int launch_staged(const MmArgs &a, hipStream_t st) {
   return ok();
 }
 
+template <int KS>
+int launch_i8(const MmI8Args &a, size_t lds, hipStream_t st) {
+  constexpr int RT = 8 / KS;
+  const int tiles = (a.n_rows + 15) / 16;
+  const unsigned gx = static_cast<unsigned>((tiles + RT - 1) / RT);
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(lds)),
+                        "hipFuncSetAttribute"))
+    return e;
+  BH_LAUNCH((pq2_i8_kernel<KS, RT>), gx, 64 * 8, lds, st, a);
+  return ok();
+}
+
+// The integer product for n_tok <= kI8Tok on staged shapes: prepare the
+// digit fragments, then one product launch with 8 waves per workgroup; small
+// matrices split each row tile's chunks over KS waves so the grid still
+// holds a few thousand waves.
+int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok, float *y,
+           size_t a_bytes, hipStream_t st) {
+  const int nblk = static_cast<int>(ne0 / 128);
+  const size_t frag_bytes = static_cast<size_t>(2 * nblk) * 64 * sizeof(uint4);
+  const size_t bfac_off = (frag_bytes + 255) / 256 * 256;
+  const size_t bfac_bytes = static_cast<size_t>(nblk) * kI8Tok * sizeof(float2);
+  char *scratch = static_cast<char *>(device_scratch(bfac_off + bfac_bytes, kScratchMatmul));
+  if (scratch == nullptr) return BH_ERR_HIP;
+  PrepI8Args pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float2 *>(scratch + bfac_off),
+                static_cast<int>(ne0), static_cast<int>(n_tok), nblk};
+  const size_t items = n_tok * nblk * 8;
+  BH_LAUNCH(pq2_i8_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
+            kMmThreads, 0, st, pa);
+  MmI8Args a{w, pa.afrag, pa.bfac, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
+             static_cast<int>(n_tok), static_cast<int>(n_rows)};
+  const size_t lds = a_bytes + 8 * kStageWaveBytes;
+  const size_t tiles = (n_rows + 15) / 16;
+  const int n_chunks = nblk / kStageBlocks;
+  int ks = 1;
+  while (ks < 8 && ks < n_chunks && tiles * ks < 4096) ks *= 2;
+  switch (ks) {
+    case 8: return launch_i8<8>(a, lds, st);
+    case 4: return launch_i8<4>(a, lds, st);
+    case 2: return launch_i8<2>(a, lds, st);
+    default: return launch_i8<1>(a, lds, st);
+  }
+}
+
 // Y[n_tok][n_rows] = X[n_tok][ne0] * W[rows][ne0]^T on the device.
 int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok, float *y,
            hipStream_t st) {
@@ -614,6 +903,15 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
               64, 0, st, w, row_bytes, static_cast<int>(ne0), x, static_cast<int>(n_tok), y,
               static_cast<int>(n_rows));
     return ok();
+  }
+  const bool stageable = nblk % kStageBlocks == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+                         bh_pq2_row_bytes(ne0) % 16 == 0;
+  if (stageable && n_tok <= static_cast<size_t>(kI8Tok)) {
+    // LDS: the live A rows of every step, the block factors (float2 per
+    // block and token slot), rounded to whole uint4
+    const size_t a_bytes = 2 * nblk * 4 * (4 * n_tok) * sizeof(uint4) +
+                           (nblk * kI8Tok * sizeof(float2) + 15) / 16 * 16;
+    if (a_bytes <= kLdsABytes) return pq2_i8(w, ne0, n_rows, x, n_tok, y, a_bytes, st);
   }
   const int n_ksteps = static_cast<int>(ne0 / 32);
   const int n_tiles = static_cast<int>((n_tok + 15) / 16);
