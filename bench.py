@@ -47,6 +47,9 @@ def _load(name: str, path: Path):
     return mod
 
 
+SPIN_CYCLES = 5_000_000  # GPU clock cycles of the pre-timing spin (~2 ms)
+
+
 def n_sets(bytes_per_set: int, max_sets: int = 32) -> int:
     return max(1, min(max_sets, -(-ROTATE_BYTES // max(1, bytes_per_set))))
 
@@ -69,6 +72,10 @@ def time_launches(launch, n_rot: int, steps: int, warmup: int, stream) -> float:
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        # hold the stream in a ~2 ms spin (before the start event) while the
+        # host submits the graph's K launches: otherwise the first launches
+        # wait on host submission (~0.2 ms per replay), which is not kernel time
+        torch.cuda._sleep(SPIN_CYCLES)
         e0.record(stream)
         graph.replay()
         e1.record(stream)

@@ -66,6 +66,71 @@ struct MaxOp {
   __device__ float operator()(float a, float b) const { return b > a ? b : a; }
 };
 
+// Reduction over aligned groups of G consecutive lanes (G a power of two
+// <= 64) without LDS: DPP quad swaps, half-row and row mirrors inside each
+// 16-lane row, then the gfx950 row-pair and half-wave swaps
+// (v_permlane16_swap, v_permlane32_swap).  32-bit values move as they are,
+// 64-bit values as two halves.  The swap steps compute op(lower, upper) on
+// both sides of the pair; the DPP steps compute op(own, partner), which is
+// the same bits on both sides for commutative ops (sums; max over non-NaN
+// partials).  All lanes of the wave must be active.
+template <int CTRL, class T>
+__device__ __forceinline__ T dpp_move(T x) {
+  static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                             0xF, 0xF, false));
+  } else {
+    const int2 h = __builtin_bit_cast(int2, x);
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(0, h.x, CTRL, 0xF, 0xF, false);
+    r.y = __builtin_amdgcn_update_dpp(0, h.y, CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(T, r);
+  }
+}
+// Returns {value of the lower half of the pair, value of the upper half}.
+template <int SPAN, class T>
+__device__ __forceinline__ void lane_swap(T x, T &lo, T &hi) {
+  if constexpr (sizeof(T) == 4) {
+    const unsigned u = __builtin_bit_cast(unsigned, x);
+    const auto r = SPAN == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                              : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lo = __builtin_bit_cast(T, static_cast<unsigned>(r[0]));
+    hi = __builtin_bit_cast(T, static_cast<unsigned>(r[1]));
+  } else {
+    const uint2 h = __builtin_bit_cast(uint2, x);
+    const auto a = SPAN == 16 ? __builtin_amdgcn_permlane16_swap(h.x, h.x, false, false)
+                              : __builtin_amdgcn_permlane32_swap(h.x, h.x, false, false);
+    const auto b = SPAN == 16 ? __builtin_amdgcn_permlane16_swap(h.y, h.y, false, false)
+                              : __builtin_amdgcn_permlane32_swap(h.y, h.y, false, false);
+    lo = __builtin_bit_cast(T, make_uint2(a[0], b[0]));
+    hi = __builtin_bit_cast(T, make_uint2(a[1], b[1]));
+  }
+}
+template <int G, class T, class Op>
+__device__ __forceinline__ T lane_group_reduce(T x, Op op) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "group of 1..64 lanes");
+  if constexpr (G >= 2) x = op(x, dpp_move<0xB1>(x));    // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) x = op(x, dpp_move<0x4E>(x));    // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) x = op(x, dpp_move<0x141>(x));   // row_half_mirror
+  if constexpr (G >= 16) x = op(x, dpp_move<0x140>(x));  // row_mirror
+  if constexpr (G >= 32) {
+    T lo, hi;
+    lane_swap<16>(x, lo, hi);
+    x = op(lo, hi);
+  }
+  if constexpr (G >= 64) {
+    T lo, hi;
+    lane_swap<32>(x, lo, hi);
+    x = op(lo, hi);
+  }
+  return x;
+}
+template <int G>
+__device__ __forceinline__ float lane_group_sum(float x) {
+  return lane_group_reduce<G>(x, SumOp{});
+}
+
 // Reduce `v` over a group of G consecutive lanes (G a power of two <= 1024).
 // Groups of up to 64 lanes live in one wave and reduce with cross-lane
 // shuffles only; larger groups span G/64 waves of the block and combine the
@@ -75,8 +140,7 @@ struct MaxOp {
 template <int G, class T, class Op>
 __device__ __forceinline__ T group_reduce(T v, Op op, T *lds) {
   constexpr int W = G < 64 ? G : 64;
-#pragma unroll
-  for (int off = W / 2; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+  v = lane_group_reduce<W>(v, op);
   if constexpr (G > 64) {
     constexpr int WPG = G / 64;
     const int wave = threadIdx.x >> 6;

@@ -175,8 +175,7 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a, int
       ss += static_cast<double>(s.y) * static_cast<double>(s.y);
       ss += static_cast<double>(s.z) * static_cast<double>(s.z);
       ss += static_cast<double>(s.w) * static_cast<double>(s.w);
-#pragma unroll
-      for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      ss = lane_group_reduce<G>(ss, SumOp{});
       if (i < l2_4) {
         const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
         s = make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);
@@ -283,8 +282,7 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_conv_kernel(GdnParams a, int 
         ss += static_cast<double>(s.y) * static_cast<double>(s.y);
         ss += static_cast<double>(s.z) * static_cast<double>(s.z);
         ss += static_cast<double>(s.w) * static_cast<double>(s.w);
-#pragma unroll
-        for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        ss = lane_group_reduce<G>(ss, SumOp{});
         if (i < l2_4) {
           const float scale = 1.0f / fmaxf(sqrtf(static_cast<float>(ss)), a.eps);
           s = make_float4(s.x * scale, s.y * scale, s.z * scale, s.w * scale);

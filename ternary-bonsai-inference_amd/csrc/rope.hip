@@ -31,8 +31,8 @@
 namespace bh {
 namespace {
 
-constexpr int kBlock = 256;
 constexpr int kMaxHalf = 128;  // n_dims/2 for head_dim <= 256
+constexpr int kMaxBlock = 512;  // lanes of the register kernel's largest block
 
 struct RopeParams {
   const float *q;
@@ -49,21 +49,26 @@ struct RopeParams {
   float eps;
 };
 
-// theta of pair j at the given positions, band selection of src/rope.rs:37-49.
-__device__ __forceinline__ float imrope_theta(int j, const int32_t *p, const RopeParams &a) {
+// theta of pair j at the given positions, band selection of src/rope.rs:37-49,
+// then the reference's chain of j rounded f32 products (src/rope.rs:54-57).
+__device__ __forceinline__ float imrope_theta(int j, int32_t p_t, int32_t p_h, int32_t p_w,
+                                              int32_t p_e, const RopeParams &a) {
   const int sector = j % a.sect;
-  int band;
+  int32_t p;
   if (sector % 3 == 1 && sector < 3 * a.s1)
-    band = 1;
+    p = p_h;
   else if (sector % 3 == 2 && sector < 3 * a.s2)
-    band = 2;
+    p = p_w;
   else if (sector % 3 == 0 && sector < 3 * a.s0)
-    band = 0;
+    p = p_t;
   else
-    band = 3;
-  float th = static_cast<float>(p[band]);
+    p = p_e;
+  float th = static_cast<float>(p);
   for (int i = 0; i < j; ++i) th *= a.theta_scale;
   return th;
+}
+__device__ __forceinline__ float imrope_theta(int j, const int32_t *p, const RopeParams &a) {
+  return imrope_theta(j, p[0], p[1], p[2], p[3], a);
 }
 
 // rotated value of one component: role 0 holds x0 = head[j], role 1 holds
@@ -73,61 +78,51 @@ __device__ __forceinline__ float rot(float own, float other, float c, float s, b
 }
 
 
-// Fills the cos/sin table of `half` pairs for the token at `p` into LDS.
-__device__ __forceinline__ void fill_table(const RopeParams &a, const int32_t *p, int half,
-                                           float *cs_cos, float *cs_sin) {
-  if (threadIdx.x < half) {
-    const float th = imrope_theta(threadIdx.x, p, a);
-    float sn, cn;
-    sincosf(th, &sn, &cn);
-    cs_cos[threadIdx.x] = cn;
-    cs_sin[threadIdx.x] = sn;
-  }
-}
-
-// A block holds rows of ONE token: blockDim.x/G row slots, R rows per slot
-// (the loads of all R rows go out first), V float4 per lane per row (lane gl
-// holds float4 gl, gl+G, ...: G*V*4 = head_dim).  A token's rows (q heads,
-// then k heads) are spread over blocks_per_tok consecutive blocks.  The
-// token's cos/sin table is built in LDS by the first n_dims/2 lanes while the
-// loads are in flight.  Rotated dims all live in the first float4 slice
-// (n_dims <= 4G).  DPP8: the rotation partner is 8 lanes away (n_dims 64), a
-// DPP row rotation inside each 16-lane row instead of an LDS-crossbar permute.
-template <int G, int V, bool NORM, int R, bool DPP8>
-__global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int blocks_per_tok) {
-  const int slots = blockDim.x / G;
+// A block holds rows of ONE token: blockDim.x/G row slots (at most 8 waves),
+// R rows per slot, V float4 per lane per row (lane gl holds float4 gl, gl+G,
+// ...: G*V*4 = head_dim).  A token's rows (q heads, then k heads) are spread
+// evenly over blocks_per_tok consecutive blocks.  Order of work, chosen so that nothing
+// waits on the row data except the arithmetic that needs it:
+//   1. every row load is issued, branch-free (rows past the token's last
+//      head re-read a valid row and are not stored);
+//   2. the token's positions come in through the scalar cache (a separate
+//      counter from the vector loads, so the angle chain starts while the
+//      rows are in flight);
+//   3. the first n_dims/2 lanes build the token's cos/sin table in LDS;
+//   4. per row: sum of squares reduced with DPP/permlane swaps, scale,
+//      weight, rotation (the partner of dim j < n_dims/2 is 8 lanes away for
+//      n_dims 64: a DPP row rotation), non-temporal store.
+// Rotated dims all live in the first float4 slice (n_dims <= 4G).
+template <int G, int V, int R, bool NORM, bool GATE, bool DPP8>
+__global__ __launch_bounds__(kMaxBlock) void qk_norm_rope_kernel(RopeParams a, int blocks_per_tok) {
+  const int kSlots = blockDim.x / G;
   __shared__ float cs_cos[kMaxHalf];
   __shared__ float cs_sin[kMaxHalf];
 
   const size_t t = blockIdx.x / blocks_per_tok;
-  const int row0 = (blockIdx.x % blocks_per_tok) * slots * R + threadIdx.x / G;
+  const int row0 = (blockIdx.x % blocks_per_tok) * kSlots * R + threadIdx.x / G;
   const int gl = threadIdx.x % G;
   const int lane = threadIdx.x & 63;
   const int n_rows = a.n_q + a.n_k;
   const int half = a.n_dims >> 1;
 
-  float4 x[R][V], g[R][V];
+  // 1. row loads
+  float4 x[R][V];
+  float4 g[GATE ? R : 1][V];
 #pragma unroll
   for (int k = 0; k < R; ++k) {
-    const int r = row0 + k * slots;
+    const int r0 = row0 + k * kSlots;
+    const int r = r0 < n_rows ? r0 : n_rows - 1;
+    const float *row = r < a.n_q ? a.q + (t * a.n_q + r) * a.q_stride
+                                 : a.k + (t * a.n_k + (r - a.n_q)) * a.head_dim;
+    const float4 *src = reinterpret_cast<const float4 *>(row);
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      x[k][v] = make_float4(0.f, 0.f, 0.f, 0.f);
-      g[k][v] = x[k][v];
-    }
-    if (r < a.n_q) {
-      const float4 *src = reinterpret_cast<const float4 *>(a.q + (t * a.n_q + r) * a.q_stride);
+    for (int v = 0; v < V; ++v) x[k][v] = load_stream(src + gl + v * G);
+    if constexpr (GATE) {
+      // the gate half of a q head row (k rows re-read their own row, unused)
+      const float4 *gs = reinterpret_cast<const float4 *>(r < a.n_q ? row + a.head_dim : row);
 #pragma unroll
-      for (int v = 0; v < V; ++v) x[k][v] = load_stream(src + gl + v * G);
-      if (a.gate_out != nullptr) {
-        const float4 *gs = reinterpret_cast<const float4 *>(a.q + (t * a.n_q + r) * a.q_stride + a.head_dim);
-#pragma unroll
-        for (int v = 0; v < V; ++v) g[k][v] = load_stream(gs + gl + v * G);
-      }
-    } else if (r < n_rows) {
-      const float4 *src = reinterpret_cast<const float4 *>(a.k + (t * a.n_k + (r - a.n_q)) * a.head_dim);
-#pragma unroll
-      for (int v = 0; v < V; ++v) x[k][v] = load_stream(src + gl + v * G);
+      for (int v = 0; v < V; ++v) g[k][v] = load_stream(gs + gl + v * G);
     }
   }
   float4 wq[V], wk[V];
@@ -135,13 +130,23 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
   for (int v = 0; v < V; ++v) {
     wq[v] = make_float4(1.f, 1.f, 1.f, 1.f);
     wk[v] = wq[v];
-    if (NORM) {
+    if constexpr (NORM) {
       if (a.n_q > 0) wq[v] = reinterpret_cast<const float4 *>(a.wq)[gl + v * G];
       if (a.n_k > 0) wk[v] = reinterpret_cast<const float4 *>(a.wk)[gl + v * G];
     }
   }
 
-  fill_table(a, a.pos + 4 * t, half, cs_cos, cs_sin);
+  // 2. the token's positions (p_t, p_h, p_w, p_e): a uniform address, so a
+  // scalar load, whose wait does not wait for the row loads above
+  const int4 pos = *reinterpret_cast<const int4 *>(a.pos + 4 * t);
+
+  // 3. the token's cos/sin table
+  for (int j = threadIdx.x; j < half; j += blockDim.x) {  // one pass unless the block is small
+    float sn, cn;
+    sincosf(imrope_theta(j, pos.x, pos.y, pos.z, pos.w, a), &sn, &cn);
+    cs_cos[j] = cn;
+    cs_sin[j] = sn;
+  }
 
   // rotation partner (first slice): dim j <-> j + n_dims/2, lane gl <-> gl +- n_dims/8
   const int d0 = 4 * gl;
@@ -158,9 +163,10 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
     sv = make_float4(cs_sin[j0], cs_sin[j0 + 1], cs_sin[j0 + 2], cs_sin[j0 + 3]);
   }
 
+  // 4. per row
 #pragma unroll
   for (int k = 0; k < R; ++k) {
-    const int r = row0 + k * slots;
+    const int r = row0 + k * kSlots;
     const bool is_q = r < a.n_q;
     float4 vv[V];
 #pragma unroll
@@ -175,8 +181,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
         ss += vv[v].z * vv[v].z;
         ss += vv[v].w * vv[v].w;
       }
-#pragma unroll
-      for (int off = G / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      ss = lane_group_sum<G>(ss);
       const float scale = 1.0f / sqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
@@ -191,10 +196,10 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
     const float4 &u = vv[0];
     if constexpr (DPP8) {
       // lane i <- lane i^8 inside each 16-lane row: DPP row_ror:8 (0x128)
-      px = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.x), 0x128, 0xf, 0xf, false));
-      py = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.y), 0x128, 0xf, 0xf, false));
-      pz = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.z), 0x128, 0xf, 0xf, false));
-      pw = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(u.w), 0x128, 0xf, 0xf, false));
+      px = dpp_move<0x128>(u.x);
+      py = dpp_move<0x128>(u.y);
+      pz = dpp_move<0x128>(u.z);
+      pw = dpp_move<0x128>(u.w);
     } else {
       px = __shfl(u.x, src_lane, 64);
       py = __shfl(u.y, src_lane, 64);
@@ -211,12 +216,12 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(RopeParams a, int 
       float4 *dst = reinterpret_cast<float4 *>(a.q_out + (t * a.n_q + r) * a.head_dim);
 #pragma unroll
       for (int v = 0; v < V; ++v) store_stream(dst + gl + v * G, vv[v]);
-      if (a.gate_out != nullptr) {
+      if constexpr (GATE) {
         float4 *gd = reinterpret_cast<float4 *>(a.gate_out + (t * a.n_q + r) * a.head_dim);
 #pragma unroll
         for (int v = 0; v < V; ++v)
-          gd[gl + v * G] = make_float4(sigmoid(g[k][v].x), sigmoid(g[k][v].y),
-                                       sigmoid(g[k][v].z), sigmoid(g[k][v].w));
+          store_stream(gd + gl + v * G, make_float4(sigmoid(g[k][v].x), sigmoid(g[k][v].y),
+                                                    sigmoid(g[k][v].z), sigmoid(g[k][v].w)));
       }
     } else if (r < n_rows) {
       float4 *dst = reinterpret_cast<float4 *>(a.k_out + (t * a.n_k + (r - a.n_q)) * a.head_dim);
@@ -269,32 +274,48 @@ __global__ __launch_bounds__(64) void qk_norm_rope_loop_kernel(RopeParams a) {
   }
 }
 
+// Launches the register kernel for lane-group size G; the gate and the DPP
+// rotation partner are compile-time variants.
+template <int G, int V, int R, bool NORM>
+int launch_rope_g(const RopeParams &p, unsigned grid, unsigned block, int bpt, hipStream_t st) {
+  const bool dpp8 = p.n_dims == 64 && G >= 16;  // partner 8 lanes away: DPP
+  if constexpr (NORM) {
+    if (p.gate_out != nullptr) {
+      if (dpp8) BH_LAUNCH((qk_norm_rope_kernel<G, V, R, NORM, true, true>), grid, block, 0, st, p, bpt);
+      else BH_LAUNCH((qk_norm_rope_kernel<G, V, R, NORM, true, false>), grid, block, 0, st, p, bpt);
+      return ok();
+    }
+  }
+  if (dpp8) BH_LAUNCH((qk_norm_rope_kernel<G, V, R, NORM, false, true>), grid, block, 0, st, p, bpt);
+  else BH_LAUNCH((qk_norm_rope_kernel<G, V, R, NORM, false, false>), grid, block, 0, st, p, bpt);
+  return ok();
+}
+
 // Launches the register kernel with V float4 per lane and R rows per lane
-// group; returns -999 when the shape does not fit that geometry.
+// group; returns -999 when the shape does not fit.  Block size: a token's
+// rows need ceil(rows / rows-per-wave) waves; they are split evenly over the
+// fewest blocks of at most 8 waves (config 2's 28 heads of 256: 14 waves,
+// two blocks of 7 -- measured 20.7 us against 22.3 us for 16-row blocks of
+// 4 waves, which leave 4 of 32 row slots idle per token).
 template <int V, int R, bool NORM>
 int launch_rope_v(const RopeParams &p, size_t n_tok, hipStream_t st) {
   if (p.head_dim % (4 * V) != 0) return -999;
   const int G = p.head_dim / 4 / V;
   if (G < 8 || G > 64 || (G & (G - 1)) != 0 || p.n_dims > 4 * G) return -999;
   const int n_rows = p.n_q + p.n_k;
-  const int rows_per_block = (kBlock / G) * R;
-  const int bpt = (n_rows + rows_per_block - 1) / rows_per_block;  // blocks per token
+  const int rows_per_wave = (64 / G) * R;
+  const int waves = (n_rows + rows_per_wave - 1) / rows_per_wave;  // per token
+  const int max_waves = kMaxBlock / 64;
+  const int bpt = (waves + max_waves - 1) / max_waves;               // blocks per token
+  const unsigned block = 64u * static_cast<unsigned>((waves + bpt - 1) / bpt);
   const size_t blocks = n_tok * static_cast<size_t>(bpt);
   if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "rope: too many head rows");
   const unsigned grid = static_cast<unsigned>(blocks);
-  if (p.n_dims == 64 && G >= 16) {  // partner 8 lanes away: DPP
-    switch (G) {
-      case 16: BH_LAUNCH((qk_norm_rope_kernel<16, V, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
-      case 32: BH_LAUNCH((qk_norm_rope_kernel<32, V, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
-      case 64: BH_LAUNCH((qk_norm_rope_kernel<64, V, NORM, R, true>), grid, kBlock, 0, st, p, bpt); return ok();
-      default: return -999;
-    }
-  }
   switch (G) {
-    case 8: BH_LAUNCH((qk_norm_rope_kernel<8, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
-    case 16: BH_LAUNCH((qk_norm_rope_kernel<16, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
-    case 32: BH_LAUNCH((qk_norm_rope_kernel<32, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
-    case 64: BH_LAUNCH((qk_norm_rope_kernel<64, V, NORM, R, false>), grid, kBlock, 0, st, p, bpt); return ok();
+    case 8: return launch_rope_g<8, V, R, NORM>(p, grid, block, bpt, st);
+    case 16: return launch_rope_g<16, V, R, NORM>(p, grid, block, bpt, st);
+    case 32: return launch_rope_g<32, V, R, NORM>(p, grid, block, bpt, st);
+    case 64: return launch_rope_g<64, V, R, NORM>(p, grid, block, bpt, st);
     default: return -999;
   }
 }
@@ -305,13 +326,14 @@ int launch_rope(const RopeParams &p, size_t n_tok, hipStream_t st) {
                     p.head_dim <= 512 && p.head_dim >= 32 && aligned16(p.q) &&
                     aligned16(p.q_out) && (p.gate_out == nullptr || aligned16(p.gate_out)) &&
                     (p.n_k == 0 || (aligned16(p.k) && aligned16(p.k_out))) &&
-                    (!NORM || (aligned16(p.wq) && (p.n_k == 0 || aligned16(p.wk))));
+                    (!NORM || (aligned16(p.wq) && (p.n_k == 0 || aligned16(p.wk)))) && aligned16(p.pos);
   if (fast) {
-    // 2 float4 per lane, 2 rows per lane group (measured on config 2: 25.2 us
-    // vs 26.5-28.6 us at one float4 and 4 rows); shapes whose rotated dims
-    // do not fit the first half-row slice take one float4 per lane
-    if (int e = launch_rope_v<2, 2, NORM>(p, n_tok, st); e != -999) return e;
-    if (int e = launch_rope_v<1, 4, NORM>(p, n_tok, st); e != -999) return e;
+    // one float4 per lane, two rows per lane group (config 2: 20.7 us; two
+    // float4 and one row per lane group: 20.7-21.2 us; 2 x 2: 21.5 us;
+    // 1 x 1: 24.5 us); shapes whose head rows are wider than 64 float4 take
+    // two float4 per lane
+    if (int e = launch_rope_v<1, 2, NORM>(p, n_tok, st); e != -999) return e;
+    if (int e = launch_rope_v<2, 1, NORM>(p, n_tok, st); e != -999) return e;
   }
   const size_t blocks = n_tok * static_cast<size_t>(p.n_q + p.n_k);
   if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "rope: too many head rows");

@@ -127,17 +127,14 @@ struct RowLane {
   }
 };
 
-// Reduction over the lanes of a row: G-lane shuffles, or (G == 0) the whole
+// Reduction over the lanes of a row: G-lane DPP/permlane steps, or (G == 0) the whole
 // block through `lds` (blockDim.x/64 entries), combined in wave order.
 template <int G, class T, class Op>
 __device__ __forceinline__ T row_reduce(T v, Op op, T *lds) {
   if constexpr (G > 0) {
-#pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
-    return v;
+    return lane_group_reduce<G>(v, op);
   } else {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    v = lane_group_reduce<64>(v, op);
     if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
     __syncthreads();
     T r = lds[0];
@@ -507,12 +504,10 @@ __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float
     const double *ps = sc.part_s + r * nch;
     float M = -INFINITY;
     for (int i = threadIdx.x; i < nch; i += 64) M = mx(M, pm[i]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = mx(M, __shfl_xor(M, off, 64));
+    M = lane_group_reduce<64>(M, mx);
     double S = 0.0;
     for (int i = threadIdx.x; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) S += __shfl_xor(S, off, 64);
+    S = lane_group_reduce<64>(S, SumOp{});
     if (threadIdx.x == 0) stat = make_float2(M, 1.0f / static_cast<float>(S));
   }
   __syncthreads();

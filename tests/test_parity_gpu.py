@@ -332,16 +332,18 @@ def test_softmax_inplace(bh, oracle, synth, dev):
 # IMROPE and the attention pre-block
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("head_dim,n_dims,sections,pos", [
+@pytest.mark.parametrize("head_dim,n_dims,sections,pos,n_head", [(*c, 24)[:5] for c in [
     (256, 64, SECTIONS, (37, 37, 37, 37)),
     (256, 64, SECTIONS, (3, 5, 7, 0)),
     (128, 32, (2, 3, 1, 2), (100, 2000, 7, 9)),
     (256, 256, SECTIONS, (2047, 2047, 2047, 2047)),
     (128, 64, SECTIONS, (911, 12, 40, 7)),         # n_dims 64 on 32-lane rows
     (100, 20, (1, 1, 1, 1), (3, 50, 700, 9000)),   # looped kernel
-])
-def test_rope_imrope_heads(bh, oracle, synth, dev, head_dim, n_dims, sections, pos):
-    n_head = 24
+    (256, 256, SECTIONS, (1500, 3, 800, 2), 1),     # one-wave block, 128-pair table
+    (256, 64, SECTIONS, (5, 6, 7, 8), 3),           # partial wave
+    (64, 64, (4, 2, 2, 0), (900, 901, 902, 0), 61),  # several blocks per token
+]])
+def test_rope_imrope_heads(bh, oracle, synth, dev, head_dim, n_dims, sections, pos, n_head):
     h = synth.Rng(head_dim + n_dims).normal(n_head * head_dim).reshape(1, n_head, head_dim)
     ref = np.stack([oracle.rope_imrope(h[0, i], *pos, n_dims, sections, 1e7)
                     for i in range(n_head)])[None]
