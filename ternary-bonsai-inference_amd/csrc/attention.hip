@@ -139,17 +139,11 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
-  return x;
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
+struct FMaxOp {
+  __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+__device__ __forceinline__ float wave_max(float x) { return lane_group_reduce<64>(x, FMaxOp{}); }
+__device__ __forceinline__ float wave_sum(float x) { return lane_group_sum<64>(x); }
 
 template <int REP, class T>
 __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
@@ -255,15 +249,26 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
       for (int x = 0; x < 4; ++x) acc[r][x] *= cr;
     }
     const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kTile) ? end - t0 : kTile);
-    for (int j = w; j < nt; j += 4) {
-      const f32x4 v = Kv<T>::load4(vc, (t0 + j) * a.kv_stride + head_off + 4 * lane);
+    // all of the wave's V rows of the tile are loaded before the first use
+    f32x4 vr[kTile / 4];
 #pragma unroll
-      for (int r = 0; r < REP; ++r) {
-        const float e = s_e[j][r];
-        acc[r][0] += e * v.x;
-        acc[r][1] += e * v.y;
-        acc[r][2] += e * v.z;
-        acc[r][3] += e * v.w;
+    for (int jj = 0; jj < kTile / 4; ++jj) {
+      const int j = w + 4 * jj;
+      vr[jj] = Kv<T>::load4(vc, (t0 + (j < nt ? j : nt - 1)) * a.kv_stride + head_off + 4 * lane);
+    }
+#pragma unroll
+    for (int jj = 0; jj < kTile / 4; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < nt) {
+        const f32x4 v = vr[jj];
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          const float e = s_e[j][r];
+          acc[r][0] += e * v.x;
+          acc[r][1] += e * v.y;
+          acc[r][2] += e * v.z;
+          acc[r][3] += e * v.w;
+        }
       }
     }
     __syncthreads();  // s_e and s_corr are rewritten by the next tile
@@ -288,24 +293,58 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
   }
 }
 
-// out[i][h][d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M).
+// out[i][h][d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M), chunks
+// with m_c = -inf left out.  Block (h, i, z) writes dims 64z .. 64z + 63 of
+// row (i, h): the chunk weights e^(m_c - M) are computed once per block into
+// LDS (in tiles of kCombTile chunks), the four waves take every fourth chunk
+// with one lane per dim, and their sums are added in wave order.  Every
+// block of a row computes M and the denominator the same way, so they agree.
+constexpr int kCombDims = 64;
+constexpr int kCombTile = 2048;
 __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *pm, const float *pl,
                                                               const float *pacc, int n_chunks,
                                                               int hd, float *out) {
+  __shared__ float s_w[kCombTile];
+  __shared__ float s_red[kBlock / 64][kCombDims];
+  __shared__ float s_m[kBlock / 64];
+  __shared__ float s_l[kBlock / 64];
   const size_t row = static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x;  // i * n_head + h
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
   const float *m = pm + row * n_chunks;
   const float *l = pl + row * n_chunks;
   float big = -INFINITY;
-  for (int c = 0; c < n_chunks; ++c) big = fmaxf(big, m[c]);
+  for (int c = tid; c < n_chunks; c += kBlock) big = fmaxf(big, m[c]);
+  big = wave_max(big);
+  if (lane == 0) s_m[w] = big;
+  __syncthreads();
+  big = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
   float den = 0.0f;
-  for (int c = 0; c < n_chunks; ++c)
+  for (int c = tid; c < n_chunks; c += kBlock)
     if (m[c] != -INFINITY) den += l[c] * expf(m[c] - big);
-  const float inv = 1.0f / den;
-  for (int d = threadIdx.x; d < hd; d += kBlock) {
-    float num = 0.0f;
-    for (int c = 0; c < n_chunks; ++c)
-      if (m[c] != -INFINITY) num += pacc[(row * n_chunks + c) * hd + d] * expf(m[c] - big);
-    out[row * hd + d] = num * inv;
+  den = lane_group_sum<64>(den);
+  if (lane == 0) s_l[w] = den;
+  const int d = static_cast<int>(blockIdx.z) * kCombDims + lane;
+  const float *acc = pacc + row * n_chunks * static_cast<size_t>(hd) + d;
+  float num = 0.0f;
+  for (int c0 = 0; c0 < n_chunks; c0 += kCombTile) {
+    const int cn = n_chunks - c0 < kCombTile ? n_chunks - c0 : kCombTile;
+    __syncthreads();  // previous tile's weights consumed (first pass: s_l visible)
+    for (int c = tid; c < cn; c += kBlock)
+      s_w[c] = m[c0 + c] != -INFINITY ? expf(m[c0 + c] - big) : -1.0f;  // -1: left out
+    __syncthreads();
+    if (d < hd) {
+#pragma unroll 8
+      for (int c = w; c < cn; c += 4) {
+        const float wc = s_w[c];
+        if (wc != -1.0f) num += acc[static_cast<size_t>(c0 + c) * hd] * wc;
+      }
+    }
+  }
+  s_red[w][lane] = num;
+  __syncthreads();
+  if (w == 0 && d < hd) {
+    const float inv = 1.0f / ((s_l[0] + s_l[1]) + (s_l[2] + s_l[3]));
+    out[row * hd + d] = ((s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane])) * inv;
   }
 }
 
@@ -459,9 +498,9 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
                     (reinterpret_cast<uintptr_t>(k_cache) % (4 * esz)) == 0 &&
                     (reinterpret_cast<uintptr_t>(v_cache) % (4 * esz)) == 0;
   if (fast) {
-    // chunks of whole tiles; about 1024 blocks over (chunk, kv head, query)
+    // chunks of whole tiles; about 2048 blocks over (chunk, kv head, query)
     const size_t tiles = (n_max + kTile - 1) / kTile;
-    const size_t want = (1024 + n_kv * n_q - 1) / (n_kv * n_q);
+    const size_t want = (2048 + n_kv * n_q - 1) / (n_kv * n_q);
     const size_t per = (tiles + want - 1) / want;
     const size_t chunk = per * kTile;
     const size_t n_chunks = (n_max + chunk - 1) / chunk;
@@ -486,7 +525,8 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
                       : decode_dispatch<float>(static_cast<int>(rep), a, static_cast<int>(n_kv),
                                                static_cast<int>(n_q), st);
     if (e) return e;
-    BH_LAUNCH(attn_combine_kernel, dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q)),
+    BH_LAUNCH(attn_combine_kernel,
+              dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims),
               kBlock, 0, st, a.pm, a.pl, a.pacc, static_cast<int>(n_chunks), kHd, out);
     return ok();
   }
