@@ -183,6 +183,23 @@ __device__ __forceinline__ float softplus(float x) {
   return x > 20.0f ? x : logf(1.0f + expf(x));
 }
 
+// e^x through the hardware base-2 exponential (v_exp_f32, ~1 ulp) with the
+// rounding error of x * log2(e) carried by FMA (a two-part log2(e)) and put
+// back to first order: e^x = 2^t * 2^err ~ 2^t * (1 + err * ln 2).  Relative
+// error a few 1e-7 for x <= 0 (what a softmax feeds it), against expf's
+// ~1e-7; -inf gives exactly 0, NaN stays NaN.  Used where a kernel is bound
+// by the exponentials and the result only needs the reference's tolerance.
+__device__ __forceinline__ float exp_hw(float x) {
+  constexpr float kL2E = 1.44269502162933349609375f;   // log2(e) rounded to f32
+  constexpr float kL2ELo = 1.925963033500011e-08f;     // log2(e) - kL2E
+  constexpr float kLn2 = 0.693147180559945309f;
+  const float t = x * kL2E;
+  float err = __builtin_fmaf(x, kL2E, -t);
+  err = __builtin_fmaf(x, kL2ELo, err);
+  const float r = __builtin_amdgcn_exp2f(t);
+  return x == -INFINITY ? 0.0f : r * __builtin_fmaf(err, kLn2, 1.0f);
+}
+
 // gguf::half_to_f32 (src/gguf.rs:881-911) in integer arithmetic: exact for
 // every one of the 65536 patterns, NaN payloads kept (no quieting).
 __device__ __forceinline__ uint32_t half_bits_to_f32_bits(uint32_t h) {

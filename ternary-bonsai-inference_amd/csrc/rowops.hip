@@ -409,10 +409,15 @@ __device__ __forceinline__ MaxSum ms_merge(MaxSum a, MaxSum b) {
 }
 
 // Split-row pass 1: block (c, r) reduces chunk c of row r (kSplitVPT float4
-// per lane, loaded up front) to (max, sum of expf(y - max)).  The chunk max
-// comes first, so each element costs one expf.  Pass 2 folds each row's
-// chunk states (the kernel boundary orders the two launches; no block waits
-// for another).
+// per lane, loaded up front) to (max, sum of e^(y - max)).  The chunk max
+// comes first, so each element costs one exponential.  Both passes are
+// bound by the exponentials as much as by HBM, so they use exp_hw (a few
+// 1e-7 relative, inside the softmax tolerance) and each lane adds its 8
+// values in f32 before the f64 sum (pass 1 of [64, 248320]: 14.1 us against
+// 15.2 us with expf and f64 per element; 8 KB chunks make pass 1 faster
+// still but double the chunk states every pass-2 block folds: slower overall).
+// Pass 2 folds each row's chunk states (the kernel boundary orders the two
+// launches; no block waits for another).
 constexpr int kSplitVPT = 4;
 constexpr size_t kMaxSplitRows = 65535;  // grid.y limit of both passes
 constexpr size_t kSplitChunk4 = static_cast<size_t>(kBlock) * kSplitVPT;  // float4 per chunk
@@ -457,14 +462,13 @@ __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float
   m = group_reduce<kBlock>(m, mx, lm);
   double s = 0.0;
   if (m != ninf) {
+    // masked (-inf) and padding entries give exp_hw(-inf) = 0
+    float q[kSplitVPT];
 #pragma unroll
-    for (int i = 0; i < kSplitVPT; ++i) {
-      // masked (-inf) and padding entries give expf(-inf) = 0
-      s += static_cast<double>(expf(v[i].x - m));
-      s += static_cast<double>(expf(v[i].y - m));
-      s += static_cast<double>(expf(v[i].z - m));
-      s += static_cast<double>(expf(v[i].w - m));
-    }
+    for (int i = 0; i < kSplitVPT; ++i)
+      q[i] = (exp_hw(v[i].x - m) + exp_hw(v[i].y - m)) + (exp_hw(v[i].z - m) + exp_hw(v[i].w - m));
+#pragma unroll
+    for (int i = 0; i < kSplitVPT; ++i) s += static_cast<double>(q[i]);
   } else {
     // a chunk with no number above -inf adds 0, unless it holds a NaN
     // (which the reference's sum carries through)
@@ -483,8 +487,8 @@ __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float
 // (M, 1/(f32)S) while the block's x loads are in flight -- every block of a
 // row folds the same states in the same fixed order (lane i takes chunks i,
 // i+64, ..., then a fixed shuffle tree), so all of them agree bit for bit --
-// then each lane writes expf(y - M) * (1 / (f32)S), the reference's output
-// formula, for its kSplitWV float4.
+// then each lane writes e^(y - M) * (1 / (f32)S), the reference's output
+// formula (the exponential by exp_hw), for its kSplitWV float4.
 constexpr int kSplitWV = 4;  // measured: 17.6 us vs 20.2 (2) and 21.3 (8) on [64, 248320]
 __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float4 *x, float4 *out,
                                                                      size_t r4, float inv_t,
@@ -517,8 +521,10 @@ __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float
     const size_t c = c0 + static_cast<size_t>(i) * kBlock;
     if (c < r4)
       store_stream(out + r * r4 + c,
-                   make_float4(expf(v[i].x * inv_t - st.x) * st.y, expf(v[i].y * inv_t - st.x) * st.y,
-                               expf(v[i].z * inv_t - st.x) * st.y, expf(v[i].w * inv_t - st.x) * st.y));
+                   make_float4(exp_hw(v[i].x * inv_t - st.x) * st.y,
+                               exp_hw(v[i].y * inv_t - st.x) * st.y,
+                               exp_hw(v[i].z * inv_t - st.x) * st.y,
+                               exp_hw(v[i].w * inv_t - st.x) * st.y));
   }
 }
 
