@@ -91,10 +91,14 @@ struct Kv<uint16_t> {
   static __device__ __forceinline__ float at(const uint16_t *c, size_t e) {
     return half_to_float(c[e]);
   }
+  // the hardware widening (v_cvt_f32_f16): exact for every finite f16 and
+  // the infinities, as the reference's half_to_f32; only a NaN's payload may
+  // differ, and a NaN score or value propagates as NaN either way
   static __device__ __forceinline__ f32x4 load4(const uint16_t *c, size_t e) {
-    const uint2 u = *reinterpret_cast<const uint2 *>(c + e);
-    return f32x4{half_to_float(u.x & 0xffffu), half_to_float(u.x >> 16),
-                 half_to_float(u.y & 0xffffu), half_to_float(u.y >> 16)};
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = *reinterpret_cast<const h4 *>(c + e);
+    return f32x4{static_cast<float>(h.x), static_cast<float>(h.y), static_cast<float>(h.z),
+                 static_cast<float>(h.w)};
   }
 };
 
@@ -294,57 +298,68 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
 }
 
 // out[i][h][d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M), chunks
-// with m_c = -inf left out.  Block (h, i, z) writes dims 64z .. 64z + 63 of
-// row (i, h): the chunk weights e^(m_c - M) are computed once per block into
-// LDS (in tiles of kCombTile chunks), the four waves take every fourth chunk
-// with one lane per dim, and their sums are added in wave order.  Every
-// block of a row computes M and the denominator the same way, so they agree.
+// with m_c = -inf left out.  Block (h, i, z) of kCombWaves waves (16 for
+// many chunks, 4 for few) writes dims
+// 64z .. 64z + 63 of row (i, h): the chunk weights e^(m_c - M) are computed
+// once per block into LDS (in tiles of kCombTile chunks), wave w takes
+// chunks w, w + kCombWaves, ... with one lane per dim (loads unconditional,
+// so eight are in flight per lane), and the waves' sums are added in wave
+// order.  Every block of a row computes M and the denominator the same way.
 constexpr int kCombDims = 64;
 constexpr int kCombTile = 2048;
-__global__ __launch_bounds__(kBlock) void attn_combine_kernel(const float *pm, const float *pl,
-                                                              const float *pacc, int n_chunks,
-                                                              int hd, float *out) {
+template <int kCombWaves>
+__global__ __launch_bounds__(64 * kCombWaves) void attn_combine_kernel(const float *pm,
+                                                                    const float *pl,
+                                                                    const float *pacc,
+                                                                    int n_chunks, int hd,
+                                                                    float *out) {
   __shared__ float s_w[kCombTile];
-  __shared__ float s_red[kBlock / 64][kCombDims];
-  __shared__ float s_m[kBlock / 64];
-  __shared__ float s_l[kBlock / 64];
+  __shared__ float s_red[kCombWaves][kCombDims];
+  __shared__ float s_m[kCombWaves];
+  __shared__ float s_l[kCombWaves];
+  constexpr int kCombThreads = 64 * kCombWaves;
   const size_t row = static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x;  // i * n_head + h
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
   const float *m = pm + row * n_chunks;
   const float *l = pl + row * n_chunks;
   float big = -INFINITY;
-  for (int c = tid; c < n_chunks; c += kBlock) big = fmaxf(big, m[c]);
+  for (int c = tid; c < n_chunks; c += kCombThreads) big = fmaxf(big, m[c]);
   big = wave_max(big);
   if (lane == 0) s_m[w] = big;
   __syncthreads();
-  big = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  big = s_m[0];
+  for (int i = 1; i < kCombWaves; ++i) big = fmaxf(big, s_m[i]);
   float den = 0.0f;
-  for (int c = tid; c < n_chunks; c += kBlock)
+  for (int c = tid; c < n_chunks; c += kCombThreads)
     if (m[c] != -INFINITY) den += l[c] * expf(m[c] - big);
-  den = lane_group_sum<64>(den);
+  den = wave_sum(den);
   if (lane == 0) s_l[w] = den;
-  const int d = static_cast<int>(blockIdx.z) * kCombDims + lane;
+  const int d = static_cast<int>(blockIdx.z) * kCombDims + (lane < hd ? lane : 0);
   const float *acc = pacc + row * n_chunks * static_cast<size_t>(hd) + d;
   float num = 0.0f;
   for (int c0 = 0; c0 < n_chunks; c0 += kCombTile) {
     const int cn = n_chunks - c0 < kCombTile ? n_chunks - c0 : kCombTile;
     __syncthreads();  // previous tile's weights consumed (first pass: s_l visible)
-    for (int c = tid; c < cn; c += kBlock)
+    for (int c = tid; c < cn; c += kCombThreads)
       s_w[c] = m[c0 + c] != -INFINITY ? expf(m[c0 + c] - big) : -1.0f;  // -1: left out
     __syncthreads();
-    if (d < hd) {
 #pragma unroll 8
-      for (int c = w; c < cn; c += 4) {
-        const float wc = s_w[c];
-        if (wc != -1.0f) num += acc[static_cast<size_t>(c0 + c) * hd] * wc;
-      }
+    for (int c = w; c < cn; c += kCombWaves) {
+      const float a = acc[static_cast<size_t>(c0 + c) * hd];
+      const float wc = s_w[c];
+      num += wc != -1.0f ? a * wc : 0.0f;
     }
   }
   s_red[w][lane] = num;
   __syncthreads();
-  if (w == 0 && d < hd) {
-    const float inv = 1.0f / ((s_l[0] + s_l[1]) + (s_l[2] + s_l[3]));
-    out[row * hd + d] = ((s_red[0][lane] + s_red[1][lane]) + (s_red[2][lane] + s_red[3][lane])) * inv;
+  const int dd = static_cast<int>(blockIdx.z) * kCombDims + lane;
+  if (w == 0 && dd < hd) {
+    float dsum = s_l[0], nsum = s_red[0][lane];
+    for (int i = 1; i < kCombWaves; ++i) {
+      dsum += s_l[i];
+      nsum += s_red[i][lane];
+    }
+    out[row * hd + dd] = nsum * (1.0f / dsum);
   }
 }
 
@@ -525,9 +540,13 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
                       : decode_dispatch<float>(static_cast<int>(rep), a, static_cast<int>(n_kv),
                                                static_cast<int>(n_q), st);
     if (e) return e;
-    BH_LAUNCH(attn_combine_kernel,
-              dim3(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims),
-              kBlock, 0, st, a.pm, a.pl, a.pacc, static_cast<int>(n_chunks), kHd, out);
+    const dim3 cgrid(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims);
+    if (n_chunks >= 64)
+      BH_LAUNCH(attn_combine_kernel<16>, cgrid, 1024, 0, st, a.pm, a.pl, a.pacc,
+                static_cast<int>(n_chunks), kHd, out);
+    else
+      BH_LAUNCH(attn_combine_kernel<4>, cgrid, 256, 0, st, a.pm, a.pl, a.pacc,
+                static_cast<int>(n_chunks), kHd, out);
     return ok();
   }
   float *probs = static_cast<float *>(device_scratch(n_q * n_head * n_max * 4, kScratchAttention));
