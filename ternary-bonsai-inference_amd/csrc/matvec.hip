@@ -547,23 +547,18 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
 constexpr int kI8Tok = 4;  // tokens per MFMA (A rows 4t .. 4t + 3)
 typedef int i4v __attribute__((ext_vector_type(4)));
 
-struct PrepI8Args {
-  const float *x;  // [n_tok][ne0]
-  uint4 *afrag;    // [group][step][lane group][16 A rows] x 16 bytes
-  float2 *bfac;    // [group][block][token in group]: (bits of sum X, 2^-e)
-  int ne0, n_tok, nblk;
-};
 
-// 8 lanes per (token, block); lane (g, h) builds the 16-byte fragment of
-// step 2b + h for lane group g: block columns 16 (2g + h) .. +15.
-__global__ __launch_bounds__(kMmThreads) void pq2_i8_prep_kernel(PrepI8Args a) {
-  const int item = blockIdx.x * kMmThreads + threadIdx.x;
-  const int tb = item >> 3, sub = item & 7;
-  const bool live = tb < a.n_tok * a.nblk;
-  const int t = live ? tb / a.nblk : 0, blk = live ? tb - t * a.nblk : 0;
+// The digit fragments of one (token, 128-block): its 8 lanes (sub = 2g + h)
+// each build the three 16-byte fragments (digits d0, d1, d2) of step 2 blk + h
+// for lane group g, block columns 16 (2g + h) .. +15, from xb = x + t * ne0 +
+// 128 * blk; every lane of the 8 gets the block factor (bits of sum X,
+// 2^-e; NaN when the block holds a NaN or infinity).  Contains cross-lane
+// steps inside each 8-lane group: all lanes of the wave must call it
+// (dead items with live = false).
+__device__ __forceinline__ void i8_prep_item(const float *xb, int sub, bool live, uint4 frag[3],
+                                             float2 &fac) {
   const int g = sub >> 1, h = sub & 1;
-  const float4 *xr = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(t) * a.ne0 +
-                                                      128 * blk + 16 * (2 * g + h));
+  const float4 *xr = reinterpret_cast<const float4 *>(xb + 16 * (2 * g + h));
   float f[16];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -612,22 +607,42 @@ __global__ __launch_bounds__(kMmThreads) void pq2_i8_prep_kernel(PrepI8Args a) {
   }
 #pragma unroll
   for (int off = 4; off > 0; off >>= 1) sx += __shfl_xor(sx, off, 64);
-  if (!live) return;
-  const int grp = t / kI8Tok, tq = t % kI8Tok;
-  const int nsteps = 2 * a.nblk;
-  uint4 *dst = a.afrag + ((static_cast<size_t>(grp) * nsteps + 2 * blk + h) * 4 + g) * 16 + 4 * tq;
 #pragma unroll
-  for (int d = 0; d < 3; ++d) dst[d] = make_uint4(dg[d][0], dg[d][1], dg[d][2], dg[d][3]);
-  if (sub == 0)
-    a.bfac[(static_cast<size_t>(grp) * a.nblk + blk) * kI8Tok + tq] =
-        make_float2(__int_as_float(sx), bad ? __builtin_nanf("") : ldexpf(1.0f, -ex));
+  for (int d = 0; d < 3; ++d) frag[d] = make_uint4(dg[d][0], dg[d][1], dg[d][2], dg[d][3]);
+  fac = make_float2(__int_as_float(sx), bad ? __builtin_nanf("") : ldexpf(1.0f, -ex));
+}
+
+// Prepare launch for large matrices: every (token, block) item once, into
+// global fragments that each product workgroup copies to LDS.
+struct PrepI8Args {
+  const float *x;  // [n_tok][ne0]
+  uint4 *afrag;    // [step][lane group][16 A rows] x 16 bytes
+  float2 *bfac;    // [block][token slot]: (bits of sum X, 2^-e)
+  int ne0, n_tok, nblk;
+};
+
+__global__ __launch_bounds__(kMmThreads) void pq2_i8_prep_kernel(PrepI8Args a) {
+  const int item = blockIdx.x * kMmThreads + threadIdx.x;
+  const int tb = item >> 3, sub = item & 7;
+  const bool live = tb < a.n_tok * a.nblk;
+  const int t = live ? tb / a.nblk : 0, blk = live ? tb - t * a.nblk : 0;
+  uint4 frag[3];
+  float2 fac;
+  i8_prep_item(a.x + static_cast<size_t>(t) * a.ne0 + 128 * blk, sub, live, frag, fac);
+  if (!live) return;
+  const int step = 2 * blk + (sub & 1), g = sub >> 1;
+  uint4 *dst = a.afrag + (static_cast<size_t>(step) * 4 + g) * 16 + 4 * t;
+#pragma unroll
+  for (int d = 0; d < 3; ++d) dst[d] = frag[d];
+  if (sub == 0) a.bfac[static_cast<size_t>(blk) * kI8Tok + t] = fac;
 }
 
 struct MmI8Args {
-  const uint8_t *w;  // first row of the range
-  const uint4 *afrag;
-  const float2 *bfac;
-  float *y;  // [n_tok][y_stride]
+  const uint8_t *w;     // first row of the range
+  const float *x;       // [n_tok][ne0], n_tok <= kI8Tok
+  const uint4 *afrag;   // prepared fragments [step][lane group][16 A rows] (not INLINE)
+  const float2 *bfac;   // prepared block factors [block][token slot] (not INLINE)
+  float *y;             // [n_tok][y_stride]
   size_t row_bytes;
   int n_rows, nblk, n_tok, y_stride;
 };
@@ -642,7 +657,7 @@ __device__ __forceinline__ i4v decode_i8(uint32_t d) {
 // LDS stage, and the KS partial sums of a tile are added in ks order at the
 // end.  The fragments of the (single) token group and its block factors are
 // copied to LDS once per workgroup, only the A rows of live tokens.
-template <int KS, int RT>
+template <int KS, int RT, bool INLINE>
 __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   constexpr int kWaves = KS * RT;
   extern __shared__ uint4 smem[];
@@ -654,12 +669,7 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
 
   const int arows = 4 * a.n_tok;  // live A rows (n_tok <= kI8Tok)
   const int total = nsteps * 4 * arows;
-  for (int i = threadIdx.x; i < total; i += 64 * kWaves) {
-    const int m = i % arows, sg = i / arows;  // sg = step * 4 + lane group
-    smem[i] = a.afrag[static_cast<size_t>(sg) * 16 + m];
-  }
   float2 *bf = reinterpret_cast<float2 *>(smem + total);
-  for (int i = threadIdx.x; i < a.nblk * kI8Tok; i += 64 * kWaves) bf[i] = a.bfac[i];
   const size_t a_words = static_cast<size_t>(total) + (static_cast<size_t>(a.nblk) * kI8Tok + 1) / 2;
   // rows of absent tokens and the unused fourth digit row feed D rows that
   // are never read: any in-bounds fragment will do
@@ -700,7 +710,37 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   float tot = 0.0f;
   const int n_chunks = a.nblk / kStageBlocks;
   int c = ks;
-  if (c < n_chunks) gload(c);
+  if (c < n_chunks) gload(c);  // the first weight chunk is in flight while x is staged
+  if constexpr (!INLINE) {
+    for (int i = threadIdx.x; i < total; i += 64 * kWaves) {
+      const int m = i % arows, sg = i / arows;  // sg = step * 4 + lane group
+      smem[i] = a.afrag[static_cast<size_t>(sg) * 16 + m];
+    }
+    for (int i = threadIdx.x; i < a.nblk * kI8Tok; i += 64 * kWaves) bf[i] = a.bfac[i];
+  } else {
+    // x digits of every (token, block) into LDS: LDS uint4 (step * 4 + g) *
+    // arows + 4 t + digit, block factors at bf[blk * kI8Tok + t].  The trip
+    // count is the same for every wave (the prep has cross-lane steps).
+    const int n_items = a.n_tok * a.nblk * 8;
+    for (int base = 0; base < n_items; base += 64 * kWaves) {
+      const int item = base + static_cast<int>(threadIdx.x);
+      const bool live_item = item < n_items;
+      const int tb = item >> 3, sub = item & 7;
+      const int t = live_item ? tb / a.nblk : 0, blk = live_item ? tb - t * a.nblk : 0;
+      uint4 frag[3];
+      float2 fac;
+      i8_prep_item(a.x + static_cast<size_t>(t) * (128 * a.nblk) + 128 * blk, sub, live_item,
+                   frag, fac);
+      if (live_item) {
+        const int step = 2 * blk + (sub & 1), gg = sub >> 1;
+        uint4 *dst = smem + (step * 4 + gg) * arows + 4 * t;
+        dst[0] = frag[0];
+        dst[1] = frag[1];
+        dst[2] = frag[2];
+        if (sub == 0) bf[blk * kI8Tok + t] = fac;
+      }
+    }
+  }
   __syncthreads();  // x staging visible to every wave
   if (c < n_chunks) {
     lstore();
@@ -835,27 +875,48 @@ int launch_staged(const MmArgs &a, hipStream_t st) {
   return ok();
 }
 
-template <int KS>
+template <int KS, bool INLINE>
 int launch_i8(const MmI8Args &a, size_t lds, hipStream_t st) {
   constexpr int RT = 8 / KS;
   const int tiles = (a.n_rows + 15) / 16;
   const unsigned gx = static_cast<unsigned>((tiles + RT - 1) / RT);
-  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT>),
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT, INLINE>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(lds)),
                         "hipFuncSetAttribute"))
     return e;
-  BH_LAUNCH((pq2_i8_kernel<KS, RT>), gx, 64 * 8, lds, st, a);
+  BH_LAUNCH((pq2_i8_kernel<KS, RT, INLINE>), gx, 64 * 8, lds, st, a);
   return ok();
 }
 
-// The integer product for n_tok <= kI8Tok on staged shapes: prepare the
-// digit fragments, then one product launch with 8 waves per workgroup; small
-// matrices split each row tile's chunks over KS waves so the grid still
-// holds a few thousand waves.
+// The integer product for n_tok <= kI8Tok on staged shapes, 8 waves per
+// workgroup.  Up to kI8InlineTiles row tiles (the grid fits the chip about
+// once) every workgroup turns x into its digit fragments in LDS while its
+// first weight chunk loads: no prepare launch, no scratch (ffn_up N=1:
+// 20.3 -> 14.9 us).  Larger matrices run several rounds of workgroups,
+// which would each repeat that work, so a prepare launch writes the
+// fragments once and workgroups copy them (LM head N=1: 73 us vs 80).
+// Small matrices split each row tile's chunks over KS waves so the grid
+// still holds a few thousand waves.
+constexpr size_t kI8InlineTiles = 4096;
 int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok, float *y,
            size_t a_bytes, hipStream_t st) {
   const int nblk = static_cast<int>(ne0 / 128);
+  MmI8Args a{w, x, nullptr, nullptr, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
+             static_cast<int>(n_tok), static_cast<int>(n_rows)};
+  const size_t lds = a_bytes + 8 * kStageWaveBytes;
+  const size_t tiles = (n_rows + 15) / 16;
+  const int n_chunks = nblk / kStageBlocks;
+  int ks = 1;
+  while (ks < 8 && ks < n_chunks && tiles * ks < 4096) ks *= 2;
+  if (tiles <= kI8InlineTiles) {
+    switch (ks) {
+      case 8: return launch_i8<8, true>(a, lds, st);
+      case 4: return launch_i8<4, true>(a, lds, st);
+      case 2: return launch_i8<2, true>(a, lds, st);
+      default: return launch_i8<1, true>(a, lds, st);
+    }
+  }
   const size_t frag_bytes = static_cast<size_t>(2 * nblk) * 64 * sizeof(uint4);
   const size_t bfac_off = (frag_bytes + 255) / 256 * 256;
   const size_t bfac_bytes = static_cast<size_t>(nblk) * kI8Tok * sizeof(float2);
@@ -866,19 +927,9 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   const size_t items = n_tok * nblk * 8;
   BH_LAUNCH(pq2_i8_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
             kMmThreads, 0, st, pa);
-  MmI8Args a{w, pa.afrag, pa.bfac, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
-             static_cast<int>(n_tok), static_cast<int>(n_rows)};
-  const size_t lds = a_bytes + 8 * kStageWaveBytes;
-  const size_t tiles = (n_rows + 15) / 16;
-  const int n_chunks = nblk / kStageBlocks;
-  int ks = 1;
-  while (ks < 8 && ks < n_chunks && tiles * ks < 4096) ks *= 2;
-  switch (ks) {
-    case 8: return launch_i8<8>(a, lds, st);
-    case 4: return launch_i8<4>(a, lds, st);
-    case 2: return launch_i8<2>(a, lds, st);
-    default: return launch_i8<1>(a, lds, st);
-  }
+  a.afrag = pa.afrag;
+  a.bfac = pa.bfac;
+  return launch_i8<1, false>(a, lds, st);  // > 4096 tiles: ks stays 1
 }
 
 // Y[n_tok][n_rows] = X[n_tok][ne0] * W[rows][ne0]^T on the device.
