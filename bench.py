@@ -47,7 +47,8 @@ def _load(name: str, path: Path):
     return mod
 
 
-SPIN_CYCLES = 5_000_000  # GPU clock cycles of the pre-timing spin (~2 ms)
+SPIN_CYCLES = 5_000_000           # minimum pre-timing spin, GPU clock cycles (~2 ms)
+SPIN_CYCLES_PER_STEP = 100_000    # ~40 us of spin per timed launch
 
 
 def n_sets(bytes_per_set: int, max_sets: int = 32) -> int:
@@ -72,10 +73,11 @@ def time_launches(launch, n_rot: int, steps: int, warmup: int, stream) -> float:
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        # hold the stream in a ~2 ms spin (before the start event) while the
-        # host submits the graph's K launches: otherwise the first launches
-        # wait on host submission (~0.2 ms per replay), which is not kernel time
-        torch.cuda._sleep(SPIN_CYCLES)
+        # hold the stream in a spin (before the start event) long enough for
+        # the host to submit all K launches of the graph: the runtime submits
+        # graph launches at up to ~40 us each, and a kernel that starts late
+        # because the host has not submitted it yet is not kernel time
+        torch.cuda._sleep(max(SPIN_CYCLES, SPIN_CYCLES_PER_STEP * steps))
         e0.record(stream)
         graph.replay()
         e1.record(stream)
@@ -478,6 +480,16 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes_each_way": n * 4, "launches": args.steps}))
         return 0
+
+    # bring clocks up before the first measurement: ~25 ms of 256 MB copies
+    # (untimed; the first kernel measured in a cold process otherwise reads
+    # up to 10% slow)
+    warm_a = torch.empty(64 * 2**20, device=dev)
+    warm_b = torch.empty_like(warm_a)
+    for _ in range(300):
+        warm_b.copy_(warm_a)
+    torch.cuda.synchronize()
+    del warm_a, warm_b
 
     with torch.cuda.stream(stream):
         head = measure("qk_norm_rope", wl_qk_norm_rope(bh, synth, dev, stream), args.steps,
