@@ -475,6 +475,33 @@ def test_pq2_gather_every_f16_scale(bh, oracle, synth, dev):
     assert bits_equal(got, ref)
 
 
+def test_pq2_gather_rms_every_f16_scale(bh, oracle, synth, dev):
+    """The fused norm over rows holding every f16 scale pattern and every
+    code (code 3 included): the closed-form sum of squares must equal the
+    reference's sequential f32 sum, so every row with finite scales is
+    bit-exact in both outputs; rows with an infinite or NaN scale are NaN at
+    the same positions."""
+    rows, ne0 = 64, 8 * 128
+    scales = np.arange(65536, dtype=np.uint16)[::8][:rows * 8].reshape(rows, 8).copy()
+    scales[5] = 0x3c00          # scale 1.0: squares 1 and 4, sums of small integers
+    scales[6] = 0x0001          # smallest subnormal scale
+    scales[7] = 0x7bff          # largest finite scale
+    rng = synth.Rng(17)
+    codes = (rng.u64(rows * ne0) % np.uint64(4)).astype(np.uint8).reshape(rows, ne0)
+    codes[9] = 3
+    table = synth.pack_pq2_rows(codes, scales)
+    ids = np.arange(rows, dtype=np.uint32)[::-1].copy()
+    w = synth.Rng(18).normal(ne0, 1.0, 0.1)
+    e, n = bh.pq2_embed_gather(_t(table, dev), ne0, rows, _t(ids, dev), w=_t(w, dev), eps=1e-6)
+    ref_e, ref_n = oracle.embed_gather(table, ne0, rows, ids, w, 1e-6)
+    ge, gn = _h(e), _h(n)
+    assert bits_equal(ge, ref_e)
+    finite = np.all((scales[ids] & 0x7c00) != 0x7c00, axis=1)
+    assert finite.sum() >= rows - 8
+    assert bits_equal(gn[finite], ref_n[finite])
+    assert np.array_equal(np.isnan(gn), np.isnan(ref_n))
+
+
 @pytest.mark.parametrize("ne0", [128, 200, 256, 5120, 130])
 def test_pq2_gather_shapes(bh, oracle, synth, dev, ne0):
     table = synth.pq2_table(synth.Rng(ne0), 50, ne0)
