@@ -24,17 +24,29 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// out[t][c..c+3] for k = 4, channels 16-byte aligned: a lane runs kConvRun
+// out[t][c..c+3] for k = 4, channels 16-byte aligned: a lane runs RUN
 // consecutive tokens of its 4 channels with the taps and the 4-row input
-// window in registers (one new input row per token).
-constexpr int kConvRun = 8;
-
+// window in registers; the RUN input rows are loaded together before the
+// first use.  The lanes of the first run (the only ones that read the cache)
+// also write the new cache of their channels after reading the old one --
+// s_{n_tok-3 .. n_tok-1}, taken from x or, for a batch of fewer than 3
+// tokens, from the old cache they already hold -- so no second launch is
+// needed and an in-place cache is safe (each cache entry is read and
+// rewritten by the same lane).
+template <int RUN>
 __global__ __launch_bounds__(kBlock) void conv1d_silu4_kernel(ConvIn cv, float *out, size_t n4,
-                                                              size_t n_tok) {
+                                                              size_t n_tok, float *new_state) {
   const size_t i = static_cast<size_t>(blockIdx.x) * kBlock + threadIdx.x;
   if (i >= n4) return;
-  const size_t t0 = static_cast<size_t>(blockIdx.y) * kConvRun;
+  const size_t t0 = static_cast<size_t>(blockIdx.y) * RUN;
   const int c = static_cast<int>(i) * 4;
+  const int nt = n_tok - t0 < static_cast<size_t>(RUN) ? static_cast<int>(n_tok - t0) : RUN;
+  const float4 *x4 = reinterpret_cast<const float4 *>(cv.x) + i;
+  const size_t row4 = static_cast<size_t>(cv.ch) / 4;
+  float4 xr[RUN];
+#pragma unroll
+  for (int tt = 0; tt < RUN; ++tt)
+    xr[tt] = load_stream(x4 + (t0 + (tt < nt ? tt : nt - 1)) * row4);
   float wv[4][4];  // [channel q][tap j]
   const float4 *w4 = reinterpret_cast<const float4 *>(cv.w + static_cast<size_t>(c) * 4);
 #pragma unroll
@@ -46,33 +58,51 @@ __global__ __launch_bounds__(kBlock) void conv1d_silu4_kernel(ConvIn cv, float *
     wv[q][3] = f.w;
   }
   float4 win[4];
+  if (t0 != 0) {  // runs start at 0 or at RUN >= 3: the window is three input rows
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const long p = static_cast<long>(t0) - 3 + j;
-    if (p >= 0) {
-      win[j] = reinterpret_cast<const float4 *>(cv.x + static_cast<size_t>(p) * cv.ch)[i];
-    } else {
-      const float *st = cv.state + static_cast<size_t>(c) * 3 + (p + 3);
-      win[j] = make_float4(st[0], st[3], st[6], st[9]);
+    for (int j = 0; j < 3; ++j) win[j] = x4[(t0 - 3 + j) * row4];
+  } else {  // the first run: the window is the cache (oldest first)
+    const float *st = cv.state + static_cast<size_t>(c) * 3;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) win[j] = make_float4(st[j], st[3 + j], st[6 + j], st[9 + j]);
+    if (new_state != nullptr) {
+      // new cache entry e of channel c+q = s_{n_tok-3+e}: input row n_tok-3+e,
+      // or for a batch of fewer than 3 tokens an old entry this lane holds.
+      // Selects are per component on values: a select between a load and an
+      // array element would become a load through a selected pointer and
+      // move the window to scratch memory.
+      auto entry = [&](int e) {
+        const long p = static_cast<long>(n_tok) - 3 + e;
+        const float4 xv = x4[static_cast<size_t>(p >= 0 ? p : 0) * row4];
+        const float4 ov = sel4(p == -2, win[1], win[2]);
+        return sel4(p >= 0, xv, ov);
+      };
+      const float4 n0 = entry(0), n1 = entry(1), n2 = entry(2);
+      float *nst = new_state + static_cast<size_t>(c) * 3;
+      nst[0] = n0.x; nst[1] = n1.x; nst[2] = n2.x;
+      nst[3] = n0.y; nst[4] = n1.y; nst[5] = n2.y;
+      nst[6] = n0.z; nst[7] = n1.z; nst[8] = n2.z;
+      nst[9] = n0.w; nst[10] = n1.w; nst[11] = n2.w;
     }
   }
-  const int nt = n_tok - t0 < static_cast<size_t>(kConvRun) ? static_cast<int>(n_tok - t0) : kConvRun;
-  for (int tt = 0; tt < nt; ++tt) {
-    const size_t t = t0 + tt;
-    win[3] = load_stream(reinterpret_cast<const float4 *>(cv.x + t * cv.ch) + i);
-    // src/forward.rs:518-522: acc = sum_j w[c][j] * win[j], j ascending
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      acc.x += wv[0][j] * win[j].x;
-      acc.y += wv[1][j] * win[j].y;
-      acc.z += wv[2][j] * win[j].z;
-      acc.w += wv[3][j] * win[j].w;
+  for (int tt = 0; tt < RUN; ++tt) {
+    if (tt < nt) {
+      win[3] = xr[tt];
+      // src/forward.rs:518-522: acc = sum_j w[c][j] * win[j], j ascending
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc.x += wv[0][j] * win[j].x;
+        acc.y += wv[1][j] * win[j].y;
+        acc.z += wv[2][j] * win[j].z;
+        acc.w += wv[3][j] * win[j].w;
+      }
+      store_stream(reinterpret_cast<float4 *>(out + (t0 + tt) * cv.ch) + i,
+                   make_float4(silu(acc.x), silu(acc.y), silu(acc.z), silu(acc.w)));
+#pragma unroll
+      for (int j = 0; j < 3; ++j) win[j] = win[j + 1];
     }
-    store_stream(reinterpret_cast<float4 *>(out + t * cv.ch) + i,
-                 make_float4(silu(acc.x), silu(acc.y), silu(acc.z), silu(acc.w)));
-#pragma unroll
-    for (int j = 0; j < 3; ++j) win[j] = win[j + 1];
   }
 }
 
@@ -138,12 +168,14 @@ extern "C" int bh_conv1d_silu(const float *x, float *state, const float *w, size
   if (int e = conv_check(cv, out, "conv1d_silu")) return e;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t total = n_tok * ch;
-  const size_t runs = (n_tok + kConvRun - 1) / kConvRun;
+  constexpr int kRun = 8;  // tokens per lane ([4096, 10240]: 63.4 us; 4: 70.1, 16: 66.8)
+  const size_t runs = (n_tok + kRun - 1) / kRun;
   if (k == 4 && ch % 4 == 0 && aligned16(x) && aligned16(out) && aligned16(w) && runs <= 65535) {
     const size_t n4 = ch / 4;
-    BH_LAUNCH(conv1d_silu4_kernel, dim3(static_cast<unsigned>((n4 + kBlock - 1) / kBlock),
-                                        static_cast<unsigned>(runs)),
-              kBlock, 0, st, cv, out, n4, n_tok);
+    BH_LAUNCH(conv1d_silu4_kernel<kRun>, dim3(static_cast<unsigned>((n4 + kBlock - 1) / kBlock),
+                                              static_cast<unsigned>(runs)),
+              kBlock, 0, st, cv, out, n4, n_tok, state);
+    return ok();  // the kernel advanced the cache
   } else {
     if ((total + kBlock - 1) / kBlock > 0x7fffffffu)
       return fail(BH_ERR_SHAPE, "conv1d_silu: too many elements");

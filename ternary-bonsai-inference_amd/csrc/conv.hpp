@@ -63,6 +63,13 @@ __device__ __forceinline__ float4 conv_window4(const ConvIn &cv, size_t t, int c
   return acc;
 }
 
+// Component-wise select of two float4 values.  Selecting between a load and
+// an array element with ?: can compile to a load through a selected pointer,
+// which moves the array to scratch memory; selecting values does not.
+__device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
+  return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+
 // Argument checks shared by the conv entry points (BH_OK or a status).
 int conv_check(const ConvIn &cv, const float *out, const char *who);
 // The state shift after a pass over n_tok tokens (second launch on `st`).

@@ -122,6 +122,7 @@ struct GdnParams {
   int sigmoid_gate;  // 1: y * sigmoid(z), 0: y * silu(z)
   float eps;
   ConvIn cv;         // cv.k > 0: `conv` holds the raw qkv, convolved here first
+  int conv_state_out;  // the conv-mode kernel advances cv.state itself
 };
 
 // src/forward.rs:501-507: beta = sigmoid(beta_raw); gate = softplus(alpha_raw
@@ -246,25 +247,59 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_conv_kernel(GdnParams a, int 
         wv[u][q][2] = f.z;
         wv[u][q][3] = f.w;
       }
+      if (t0 != 0) {  // groups start at 0 or at kConvTok >= 3: three input rows
 #pragma unroll
-      for (int j = 0; j < 3; ++j) {  // the three inputs before t0
-        const long p = static_cast<long>(t0) - 3 + j;
-        if (p >= 0) {
-          win[u][j] = reinterpret_cast<const float4 *>(a.cv.x + static_cast<size_t>(p) * a.conv_dim)[c / 4];
-        } else {
-          const float *st = a.cv.state + static_cast<size_t>(c) * 3 + (p + 3);
-          win[u][j] = make_float4(st[0], st[3], st[6], st[9]);
-        }
+        for (int j = 0; j < 3; ++j)
+          win[u][j] = reinterpret_cast<const float4 *>(a.cv.x + (t0 - 3 + j) * a.conv_dim)[c / 4];
+      } else {  // the first group: the cache (oldest first)
+        const float *st = a.cv.state + static_cast<size_t>(c) * 3;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) win[u][j] = make_float4(st[j], st[3 + j], st[6 + j], st[9 + j]);
       }
     }
-    for (int tt = 0; tt < nt; ++tt) {
-      const size_t t = t0 + tt;
+    // every input row of the group, loaded before the first use
+    float4 xin[kConvTok][kU];
+#pragma unroll
+    for (int tt = 0; tt < kConvTok; ++tt) {
+      const size_t t = t0 + (tt < nt ? tt : nt - 1);
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const int i = (part * kU + u) * kBlock + tid;
         const int c = 4 * (i < n4 ? i : 0);
-        win[u][3] = load_stream(reinterpret_cast<const float4 *>(a.cv.x + t * a.conv_dim) + c / 4);
+        xin[tt][u] = load_stream(reinterpret_cast<const float4 *>(a.cv.x + t * a.conv_dim) + c / 4);
       }
+    }
+    if (t0 == 0 && a.conv_state_out) {
+      // The first group's lanes, the only readers of the cache, write its new
+      // contents for their channels after reading them: entry e = s_{n_tok-3+e},
+      // an input row, or for fewer than 3 tokens an old entry held in win.
+      // Selects per component on values (see conv.hip).
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = (part * kU + u) * kBlock + tid;
+        if (i >= n4) continue;
+        const float4 *x4 = reinterpret_cast<const float4 *>(a.cv.x) + i;
+        const size_t row4 = static_cast<size_t>(a.conv_dim) / 4;
+        auto entry = [&](int e) {
+          const long p = static_cast<long>(n_tok) - 3 + e;
+          const float4 xv = x4[static_cast<size_t>(p >= 0 ? p : 0) * row4];
+          const float4 ov = sel4(p == -2, win[u][1], win[u][2]);
+          return sel4(p >= 0, xv, ov);
+        };
+        const float4 n0 = entry(0), n1 = entry(1), n2 = entry(2);
+        float *nst = const_cast<float *>(a.cv.state) + static_cast<size_t>(4 * i) * 3;
+        nst[0] = n0.x; nst[1] = n1.x; nst[2] = n2.x;
+        nst[3] = n0.y; nst[4] = n1.y; nst[5] = n2.y;
+        nst[6] = n0.z; nst[7] = n1.z; nst[8] = n2.z;
+        nst[9] = n0.w; nst[10] = n1.w; nst[11] = n2.w;
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < kConvTok; ++tt) {
+      if (tt >= nt) break;
+      const size_t t = t0 + tt;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) win[u][3] = xin[tt][u];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const int i = (part * kU + u) * kBlock + tid;
@@ -503,6 +538,9 @@ extern "C" int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream)
       p.conv_dim = 0;
       p.l2_dim = 0;
     }
+    // with conv outputs the conv-mode kernel's first token group advances
+    // the cache itself (no second launch)
+    p.conv_state_out = conv_in && g.conv_out != nullptr ? 1 : 0;
     int e = -999;
     switch (g.conv_out == nullptr ? 64 : hq) {
       case 1: e = launch_fused<1>(p, conv_in, g.n_tok, bc, bg, st); break;
@@ -516,8 +554,8 @@ extern "C" int bh_gdn_prep_fused(const bh_gdn_prep_args *args, bh_stream stream)
     }
     if (e != -999) {
       if (e != BH_OK) return e;
-      // the conv cache shifts only after every token has read it
-      return conv_in ? conv_state_update(p.cv, g.n_tok, st) : ok();
+      // otherwise the conv cache shifts after every token has read it
+      return conv_in && !p.conv_state_out ? conv_state_update(p.cv, g.n_tok, st) : ok();
     }
   }
   BH_LAUNCH(gdn_prep_loop_kernel, grid, kBlock, 0, st, p);

@@ -103,6 +103,8 @@ def test_conv1d_graph_replay_advances_cache(bh, oracle, synth, dev):
 @pytest.mark.parametrize("shape", [
     (4096, 10240, 4096, 6144, 48),   # model layout: conv over qkv, q,k L2, 48 gates
     (3, 10240, 4096, 6144, 48),      # fewer tokens than taps
+    (1, 10240, 4096, 6144, 48),      # one token: the new cache keeps two old entries
+    (2, 10240, 4096, 6144, 48),      # two tokens: one old entry
     (3, 100, 60, 10, 5),             # odd widths: looped kernel
 ])
 def test_gdn_prep_fused_with_conv(bh, oracle, synth, dev, shape):
