@@ -155,6 +155,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
   __shared__ float s_e[kTile][REP];       // scores, then exponentials
   __shared__ float s_corr[REP];
   __shared__ float s_acc[4][REP][kHd];
+  __shared__ f32x4 s_q[REP * kHd / 4];
   const T *kc = static_cast<const T *>(a.kc);
   const T *vc = static_cast<const T *>(a.vc);
   const int c = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
@@ -174,19 +175,12 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
     return;
   }
   const int grp = tid / kQkLanes, sub = tid % kQkLanes;
-  float qr[REP][kQkPer];
-#pragma unroll
-  for (int r = 0; r < REP; ++r) {
-    const f32x4 *qp = reinterpret_cast<const f32x4 *>(
-        a.q + (static_cast<size_t>(i) * a.n_head + g * REP + r) * kHd + kQkPer * sub);
-#pragma unroll
-    for (int x = 0; x < kQkPer / 4; ++x) {
-      const f32x4 f = qp[x];
-      qr[r][4 * x] = f.x;
-      qr[r][4 * x + 1] = f.y;
-      qr[r][4 * x + 2] = f.z;
-      qr[r][4 * x + 3] = f.w;
-    }
+  // the group's q rows in LDS (REP x 256 floats, the kv head's q heads are
+  // consecutive): registers go to the K and V tiles instead
+  {
+    const f32x4 *qg = reinterpret_cast<const f32x4 *>(
+        a.q + (static_cast<size_t>(i) * a.n_head + g * REP) * kHd);
+    for (int o = tid; o < REP * kHd / 4; o += kBlock) s_q[o] = qg[o];
   }
   float run_m[kSlots], run_l[kSlots];
 #pragma unroll
@@ -211,21 +205,33 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int x = 0; x < kQkPer / 4; ++x) kr[pass][x] = Kv<T>::load4(kc, e0 + 4 * x);
     }
+    __syncthreads();  // s_q written (first tile), while the K rows are in flight
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-      const size_t p = t0 + pass * 16 + grp;
+    for (int r = 0; r < REP; ++r) {
+      f32x4 qv[kQkPer / 4];  // head r's 16 dims of this lane, read once per tile
 #pragma unroll
-      for (int r = 0; r < REP; ++r) {
+      for (int x = 0; x < kQkPer / 4; ++x) qv[x] = s_q[(r * kHd + kQkPer * sub) / 4 + x];
+#pragma unroll
+      for (int pass = 0; pass < 4; ++pass) {
+        const size_t p = t0 + pass * 16 + grp;
         float part[4];
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
           const f32x4 kv = kr[pass][x];
-          part[x] = (qr[r][4 * x] * kv.x + qr[r][4 * x + 1] * kv.y) +
-                    (qr[r][4 * x + 2] * kv.z + qr[r][4 * x + 3] * kv.w);
+          part[x] = (qv[x].x * kv.x + qv[x].y * kv.y) + (qv[x].z * kv.z + qv[x].w * kv.w);
         }
         const float d = row16_sum((part[0] + part[1]) + (part[2] + part[3]));
         if (sub == 0) s_e[pass * 16 + grp][r] = p < end ? d * a.scale : -INFINITY;
       }
+    }
+    // the wave's V rows of the tile: issued now (the K registers are free) so
+    // their latency overlaps the softmax step and its barriers
+    const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kTile) ? end - t0 : kTile);
+    f32x4 vr[kTile / 4];
+#pragma unroll
+    for (int jj = 0; jj < kTile / 4; ++jj) {
+      const int j = w + 4 * jj;
+      vr[jj] = Kv<T>::load4(vc, (t0 + (j < nt ? j : nt - 1)) * a.kv_stride + head_off + 4 * lane);
     }
     __syncthreads();
     // softmax state: wave w owns heads w, w + 4
@@ -251,14 +257,6 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
       const float cr = s_corr[r];
 #pragma unroll
       for (int x = 0; x < 4; ++x) acc[r][x] *= cr;
-    }
-    const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kTile) ? end - t0 : kTile);
-    // all of the wave's V rows of the tile are loaded before the first use
-    f32x4 vr[kTile / 4];
-#pragma unroll
-    for (int jj = 0; jj < kTile / 4; ++jj) {
-      const int j = w + 4 * jj;
-      vr[jj] = Kv<T>::load4(vc, (t0 + (j < nt ? j : nt - 1)) * a.kv_stride + head_off + 4 * lane);
     }
 #pragma unroll
     for (int jj = 0; jj < kTile / 4; ++jj) {
