@@ -875,17 +875,17 @@ int launch_staged(const MmArgs &a, hipStream_t st) {
   return ok();
 }
 
-template <int KS, bool INLINE>
-int launch_i8(const MmI8Args &a, size_t lds, hipStream_t st) {
-  constexpr int RT = 8 / KS;
+template <int KS, bool INLINE, int RT = 8 / KS>
+int launch_i8(const MmI8Args &a, size_t lds_a, hipStream_t st) {
   const int tiles = (a.n_rows + 15) / 16;
   const unsigned gx = static_cast<unsigned>((tiles + RT - 1) / RT);
+  const size_t lds = lds_a + static_cast<size_t>(KS * RT) * kStageWaveBytes;
   if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT, INLINE>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(lds)),
                         "hipFuncSetAttribute"))
     return e;
-  BH_LAUNCH((pq2_i8_kernel<KS, RT, INLINE>), gx, 64 * 8, lds, st, a);
+  BH_LAUNCH((pq2_i8_kernel<KS, RT, INLINE>), gx, 64 * KS * RT, lds, st, a);
   return ok();
 }
 
@@ -904,12 +904,18 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   const int nblk = static_cast<int>(ne0 / 128);
   MmI8Args a{w, x, nullptr, nullptr, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
              static_cast<int>(n_tok), static_cast<int>(n_rows)};
-  const size_t lds = a_bytes + 8 * kStageWaveBytes;
+  const size_t lds = a_bytes;
   const size_t tiles = (n_rows + 15) / 16;
   const int n_chunks = nblk / kStageBlocks;
   int ks = 1;
   while (ks < 8 && ks < n_chunks && tiles * ks < 4096) ks *= 2;
   if (tiles <= kI8InlineTiles) {
+    // wide x (an 8-wave workgroup's LDS leaves room for one per CU) and few
+    // row tiles: two tiles per 16-wave workgroup, so the grid is one round
+    // over the CUs instead of two (ffn_down N=1: 320 row tiles)
+    if (ks == 8 && 2 * (a_bytes + 8 * kStageWaveBytes) > 160 * 1024 && tiles <= 512 &&
+        a_bytes + 16 * kStageWaveBytes <= 160 * 1024)
+      return launch_i8<8, true, 2>(a, lds, st);
     switch (ks) {
       case 8: return launch_i8<8, true>(a, lds, st);
       case 4: return launch_i8<4, true>(a, lds, st);

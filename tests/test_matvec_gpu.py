@@ -73,6 +73,7 @@ def test_matmul_reference_case(bh, oracle, synth, dev):
 @pytest.mark.parametrize("ne0,n_rows,base_row", [
     (5120, 17408, 0),     # ffn_up / ffn_gate shape
     (17408, 512, 0),      # ffn_down's row width (136 blocks)
+    (17408, 333, 1),      # the same, odd tile count and a ragged tail (two tiles per workgroup)
     (5120, 1000, 3),      # ragged rows, offset range
     (128, 33, 0), (256, 1, 5),
     (300, 70, 2),         # partial last block: generic path
