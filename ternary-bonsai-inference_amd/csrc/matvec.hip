@@ -30,6 +30,7 @@
 // reference adds scale * block_sum.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 
 #include "common.hpp"
@@ -889,6 +890,20 @@ int launch_i8(const MmI8Args &a, size_t lds_a, hipStream_t st) {
   return ok();
 }
 
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // The integer product for n_tok <= kI8Tok on staged shapes, 8 waves per
 // workgroup.  Up to kI8InlineTiles row tiles (the grid fits the chip about
 // once) every workgroup turns x into its digit fragments in LDS while its
@@ -911,11 +926,26 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   while (ks < 8 && ks < n_chunks && tiles * ks < 4096) ks *= 2;
   if (tiles <= kI8InlineTiles) {
     // wide x (an 8-wave workgroup's LDS leaves room for one per CU) and few
-    // row tiles: two tiles per 16-wave workgroup, so the grid is one round
-    // over the CUs instead of two (ffn_down N=1: 320 row tiles)
-    if (ks == 8 && 2 * (a_bytes + 8 * kStageWaveBytes) > 160 * 1024 && tiles <= 512 &&
-        a_bytes + 16 * kStageWaveBytes <= 160 * 1024)
+    // row tiles: two tiles per 16-wave workgroup, 8 waves each, so the grid
+    // is one round over the CUs instead of two (ffn_down N=1, 320 row tiles:
+    // 13.7 us, against 20.2 with 8 waves and 14.8 with 4 waves per tile)
+    if (n_chunks >= 8 && 2 * (a_bytes + 8 * kStageWaveBytes) > 160 * 1024 &&
+        tiles <= 2 * static_cast<size_t>(cu_count()) && a_bytes + 16 * kStageWaveBytes <= 160 * 1024)
       return launch_i8<8, true, 2>(a, lds, st);
+    // the most waves per row tile whose grid still runs in one round: a
+    // workgroup is 8 waves (8 / ks row tiles), as many per CU as LDS and the
+    // wave limit allow (ffn_up N=1: 4 waves per tile made 544 workgroups for
+    // 512 slots, a 32-workgroup second round)
+    const size_t wg_lds = a_bytes + 8 * kStageWaveBytes;
+    const size_t per_cu = std::min<size_t>(4, (160 * 1024) / wg_lds);
+    const size_t slots = per_cu * static_cast<size_t>(cu_count());
+    for (int k = 8; k >= 1; k >>= 1) {
+      const size_t wgs = (tiles + (8 / k) - 1) / (8 / k);
+      if (k <= n_chunks && per_cu > 0 && wgs <= slots) {
+        ks = k;
+        break;
+      }
+    }
     switch (ks) {
       case 8: return launch_i8<8, true>(a, lds, st);
       case 4: return launch_i8<4, true>(a, lds, st);
