@@ -25,9 +25,10 @@
  * expf/logf/sinf/cosf, no FMA contraction.  The PQ2_0 decode is bit-exact.
  *
  * Threading: every device entry point is re-entrant per stream, except
- * bh_softmax_rows on rows too wide for one workgroup and the PQ2_0 products
- * (bh_pq2_matvec_range, bh_pq2_matmul_n), which use per-device scratch
- * buffers: each must not run concurrently with itself on one device.
+ * bh_softmax_rows on rows too wide for one workgroup, bh_attention, and the
+ * PQ2_0 products (bh_pq2_matvec_range, bh_pq2_matmul_n) with more than 4
+ * tokens or on shapes outside the integer path, which use per-device
+ * scratch buffers: each must not run concurrently with itself on one device.
  */
 #ifndef BONSAI_HIP_H
 #define BONSAI_HIP_H
@@ -283,8 +284,10 @@ int bh_pq2_embed_gather_rms(const uint8_t *table, size_t ne0, size_t n_rows,
  * the product reads rows base_row .. base_row + n_rows - 1.  Results agree
  * with the reference's scalar row dot to <= 1e-5 of the output's largest
  * magnitude (the summation order differs, as the reference's AVX2 path's
- * does).  Uses the library's per-device scratch (x fragments): calls must
- * not overlap on one device.
+ * does).  Up to 4 tokens on rows of whole 1024-weight chunks (16-byte
+ * aligned) the products keep x in LDS and use no scratch; otherwise they
+ * use the library's per-device scratch (x fragments): such calls must not
+ * overlap on one device.
  * ------------------------------------------------------------------------- */
 
 /* kernels::pq2_matvec_range (src/kernels.rs:283-333):

@@ -613,36 +613,9 @@ __device__ __forceinline__ void i8_prep_item(const float *xb, int sub, bool live
   fac = make_float2(__int_as_float(sx), bad ? __builtin_nanf("") : ldexpf(1.0f, -ex));
 }
 
-// Prepare launch for large matrices: every (token, block) item once, into
-// global fragments that each product workgroup copies to LDS.
-struct PrepI8Args {
-  const float *x;  // [n_tok][ne0]
-  uint4 *afrag;    // [step][lane group][16 A rows] x 16 bytes
-  float2 *bfac;    // [block][token slot]: (bits of sum X, 2^-e)
-  int ne0, n_tok, nblk;
-};
-
-__global__ __launch_bounds__(kMmThreads) void pq2_i8_prep_kernel(PrepI8Args a) {
-  const int item = blockIdx.x * kMmThreads + threadIdx.x;
-  const int tb = item >> 3, sub = item & 7;
-  const bool live = tb < a.n_tok * a.nblk;
-  const int t = live ? tb / a.nblk : 0, blk = live ? tb - t * a.nblk : 0;
-  uint4 frag[3];
-  float2 fac;
-  i8_prep_item(a.x + static_cast<size_t>(t) * a.ne0 + 128 * blk, sub, live, frag, fac);
-  if (!live) return;
-  const int step = 2 * blk + (sub & 1), g = sub >> 1;
-  uint4 *dst = a.afrag + (static_cast<size_t>(step) * 4 + g) * 16 + 4 * t;
-#pragma unroll
-  for (int d = 0; d < 3; ++d) dst[d] = frag[d];
-  if (sub == 0) a.bfac[static_cast<size_t>(blk) * kI8Tok + t] = fac;
-}
-
 struct MmI8Args {
   const uint8_t *w;     // first row of the range
   const float *x;       // [n_tok][ne0], n_tok <= kI8Tok
-  const uint4 *afrag;   // prepared fragments [step][lane group][16 A rows] (not INLINE)
-  const float2 *bfac;   // prepared block factors [block][token slot] (not INLINE)
   float *y;             // [n_tok][y_stride]
   size_t row_bytes;
   int n_rows, nblk, n_tok, y_stride;
@@ -653,12 +626,76 @@ __device__ __forceinline__ i4v decode_i8(uint32_t d) {
              static_cast<int>((d >> 4) & 0x03030303u), static_cast<int>((d >> 6) & 0x03030303u)};
 }
 
+// x digits of every (token, block) into LDS, by all `lanes` lanes of the
+// workgroup: uint4 (step * 4 + g) * arows + 4 t + digit, block factors at
+// bf[blk * kI8Tok + t].  The trip count is the same for every wave (the
+// prep has cross-lane steps).
+__device__ __forceinline__ void i8_stage_x(const MmI8Args &a, uint4 *smem, float2 *bf, int arows,
+                                           int lanes) {
+  const int n_items = a.n_tok * a.nblk * 8;
+  for (int base = 0; base < n_items; base += lanes) {
+    const int item = base + static_cast<int>(threadIdx.x);
+    const bool live_item = item < n_items;
+    const int tb = item >> 3, sub = item & 7;
+    const int t = live_item ? tb / a.nblk : 0, blk = live_item ? tb - t * a.nblk : 0;
+    uint4 frag[3];
+    float2 fac;
+    i8_prep_item(a.x + static_cast<size_t>(t) * (128 * a.nblk) + 128 * blk, sub, live_item, frag,
+                 fac);
+    if (live_item) {
+      const int step = 2 * blk + (sub & 1), gg = sub >> 1;
+      uint4 *dst = smem + (step * 4 + gg) * arows + 4 * t;
+      dst[0] = frag[0];
+      dst[1] = frag[1];
+      dst[2] = frag[2];
+      if (sub == 0) bf[blk * kI8Tok + t] = fac;
+    }
+  }
+}
+
+// One 8-block chunk of a wave's 16-row tile from its LDS stage into the
+// row total `tot` (blocks b0 .. b0 + 7 of the row).
+__device__ __forceinline__ float i8_chunk(const uint8_t *stage, const uint4 *al, const float2 *bl,
+                                          int arows, int n, int g, int b0, float tot) {
+  const uint8_t *rowp = stage + n * kStageStride;
+#pragma unroll 2
+  for (int bb = 0; bb < kStageBlocks; ++bb) {
+    const int b = b0 + bb;
+    const uint8_t *blk = rowp + kPq2Blk * bb;
+    uint32_t cd0, cd1;
+    float sc;
+    if ((bb & 1) == 0) {  // block starts on a dword: codes are 2 bytes in
+      const uint32_t e0 = lds_u32(blk + 8 * g), e1 = lds_u32(blk + 8 * g + 4),
+                     e2 = lds_u32(blk + 8 * g + 8);
+      cd0 = __builtin_amdgcn_alignbyte(e1, e0, 2);
+      cd1 = __builtin_amdgcn_alignbyte(e2, e1, 2);
+      sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk))));
+    } else {  // block starts 2 bytes into a dword: codes are dword-aligned
+      cd0 = lds_u32(blk + 2 + 8 * g);
+      cd1 = lds_u32(blk + 6 + 8 * g);
+      sc = static_cast<float>(
+          __builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk - 2) >> 16)));
+    }
+    const i4v a0 = __builtin_bit_cast(i4v, al[(2 * b) * 4 * arows]);
+    const i4v a1 = __builtin_bit_cast(i4v, al[(2 * b + 1) * 4 * arows]);
+    const float2 f = bl[b * kI8Tok];
+    i4v acc = i4v{0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, decode_i8(cd0), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, decode_i8(cd1), acc, 0, 0, 0);
+    const uint32_t v = (static_cast<uint32_t>(acc[0]) << 16) + (static_cast<uint32_t>(acc[1]) << 8) +
+                       static_cast<uint32_t>(acc[2]) - __float_as_uint(f.x);
+    const float blk_sum = static_cast<float>(static_cast<int>(v)) * f.y;  // times 2^-e: exact
+    tot = fmaf(blk_sum, sc, tot);  // src/kernels.rs:651: acc += scale * block_acc
+  }
+  return tot;
+}
+
 // Workgroup = RT row tiles x KS waves each; wave (rt, ks) streams the chunks
 // c = ks, ks + KS, ... of row tile blockIdx.x * RT + rt through its private
 // LDS stage, and the KS partial sums of a tile are added in ks order at the
 // end.  The fragments of the (single) token group and its block factors are
 // copied to LDS once per workgroup, only the A rows of live tokens.
-template <int KS, int RT, bool INLINE>
+template <int KS, int RT>
 __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   constexpr int kWaves = KS * RT;
   extern __shared__ uint4 smem[];
@@ -712,36 +749,7 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   const int n_chunks = a.nblk / kStageBlocks;
   int c = ks;
   if (c < n_chunks) gload(c);  // the first weight chunk is in flight while x is staged
-  if constexpr (!INLINE) {
-    for (int i = threadIdx.x; i < total; i += 64 * kWaves) {
-      const int m = i % arows, sg = i / arows;  // sg = step * 4 + lane group
-      smem[i] = a.afrag[static_cast<size_t>(sg) * 16 + m];
-    }
-    for (int i = threadIdx.x; i < a.nblk * kI8Tok; i += 64 * kWaves) bf[i] = a.bfac[i];
-  } else {
-    // x digits of every (token, block) into LDS: LDS uint4 (step * 4 + g) *
-    // arows + 4 t + digit, block factors at bf[blk * kI8Tok + t].  The trip
-    // count is the same for every wave (the prep has cross-lane steps).
-    const int n_items = a.n_tok * a.nblk * 8;
-    for (int base = 0; base < n_items; base += 64 * kWaves) {
-      const int item = base + static_cast<int>(threadIdx.x);
-      const bool live_item = item < n_items;
-      const int tb = item >> 3, sub = item & 7;
-      const int t = live_item ? tb / a.nblk : 0, blk = live_item ? tb - t * a.nblk : 0;
-      uint4 frag[3];
-      float2 fac;
-      i8_prep_item(a.x + static_cast<size_t>(t) * (128 * a.nblk) + 128 * blk, sub, live_item,
-                   frag, fac);
-      if (live_item) {
-        const int step = 2 * blk + (sub & 1), gg = sub >> 1;
-        uint4 *dst = smem + (step * 4 + gg) * arows + 4 * t;
-        dst[0] = frag[0];
-        dst[1] = frag[1];
-        dst[2] = frag[2];
-        if (sub == 0) bf[blk * kI8Tok + t] = fac;
-      }
-    }
-  }
+  i8_stage_x(a, smem, bf, arows, 64 * kWaves);
   __syncthreads();  // x staging visible to every wave
   if (c < n_chunks) {
     lstore();
@@ -750,36 +758,7 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   for (; c < n_chunks; c += KS) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint8_t *rowp = stage + n * kStageStride;
-#pragma unroll 2
-    for (int bb = 0; bb < kStageBlocks; ++bb) {
-      const int b = c * kStageBlocks + bb;
-      const uint8_t *blk = rowp + kPq2Blk * bb;
-      uint32_t cd0, cd1;
-      float sc;
-      if ((bb & 1) == 0) {  // block starts on a dword: codes are 2 bytes in
-        const uint32_t e0 = lds_u32(blk + 8 * g), e1 = lds_u32(blk + 8 * g + 4),
-                       e2 = lds_u32(blk + 8 * g + 8);
-        cd0 = __builtin_amdgcn_alignbyte(e1, e0, 2);
-        cd1 = __builtin_amdgcn_alignbyte(e2, e1, 2);
-        sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk))));
-      } else {  // block starts 2 bytes into a dword: codes are dword-aligned
-        cd0 = lds_u32(blk + 2 + 8 * g);
-        cd1 = lds_u32(blk + 6 + 8 * g);
-        sc = static_cast<float>(
-            __builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk - 2) >> 16)));
-      }
-      const i4v a0 = __builtin_bit_cast(i4v, al[(2 * b) * 4 * arows]);
-      const i4v a1 = __builtin_bit_cast(i4v, al[(2 * b + 1) * 4 * arows]);
-      const float2 f = bl[b * kI8Tok];
-      i4v acc = i4v{0, 0, 0, 0};
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, decode_i8(cd0), acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, decode_i8(cd1), acc, 0, 0, 0);
-      const uint32_t v = (static_cast<uint32_t>(acc[0]) << 16) + (static_cast<uint32_t>(acc[1]) << 8) +
-                         static_cast<uint32_t>(acc[2]) - __float_as_uint(f.x);
-      const float blk_sum = static_cast<float>(static_cast<int>(v)) * f.y;  // times 2^-e: exact
-      tot = fmaf(blk_sum, sc, tot);  // src/kernels.rs:651: acc += scale * block_acc
-    }
+    tot = i8_chunk(stage, al, bl, arows, n, g, c * kStageBlocks, tot);
     if (c + KS < n_chunks) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -802,6 +781,98 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
     }
   }
   if (ks == 0 && g < a.n_tok && row < a.n_rows) a.y[static_cast<size_t>(g) * a.y_stride + row] = tot;
+}
+
+// Persistent form for matrices with more row tiles than one round of
+// workgroups holds (the LM head): G workgroups of RT waves, G sized to one
+// round; workgroup w builds the x fragments once, then wave rt walks the row
+// tiles (w + i G) RT + rt, i = 0, 1, ..., as one flat stream of (tile, chunk)
+// items through its LDS stage -- the next item's loads in flight across tile
+// boundaries -- and writes each tile's outputs when its last chunk is done.
+// No prepare launch, no scratch, no later rounds of workgroups each repeating
+// the x preparation.
+template <int RT>
+__global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
+  extern __shared__ uint4 smem[];
+  const int lane = threadIdx.x & 63, rt = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int nsteps = 2 * a.nblk;
+  const int arows = 4 * a.n_tok;
+  const int total = nsteps * 4 * arows;
+  float2 *bf = reinterpret_cast<float2 *>(smem + total);
+  const size_t a_words = static_cast<size_t>(total) + (static_cast<size_t>(a.nblk) * kI8Tok + 1) / 2;
+  const uint4 *al = smem + g * arows + (n < arows ? n : (n & 3));
+  const float2 *bl = bf + g;
+  uint8_t *stage = reinterpret_cast<uint8_t *>(smem + a_words) + rt * kStageWaveBytes;
+
+  const int n_chunks = a.nblk / kStageBlocks;
+  const int tiles = (a.n_rows + 15) / 16;
+  const int groups = (tiles + RT - 1) / RT;
+  const int gw = static_cast<int>(blockIdx.x), G = static_cast<int>(gridDim.x);
+  const int my_groups = groups > gw ? (groups - gw + G - 1) / G : 0;
+  const int n_items = my_groups * n_chunks;
+  auto item_tile = [&](int q) { return (gw + (q / n_chunks) * G) * RT + rt; };
+
+  int r_of[kStageLoads], c16_of[kStageLoads], dst[kStageLoads];
+  bool live[kStageLoads];
+#pragma unroll
+  for (int k = 0; k < kStageLoads; ++k) {
+    const int idx = lane + 64 * k;
+    live[k] = idx < 16 * kStageF4;
+    r_of[k] = live[k] ? idx / kStageF4 : 0;
+    c16_of[k] = live[k] ? idx % kStageF4 : 0;
+    dst[k] = r_of[k] * kStageStride + 16 * c16_of[k];
+  }
+  uint4 regs[kStageLoads];
+  auto gload = [&](int q) {
+    const int tile = item_tile(q), c = q % n_chunks;
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k) {
+      if (live[k]) {
+        int row = tile * 16 + r_of[k];
+        row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
+        regs[k] = *reinterpret_cast<const uint4 *>(a.w + static_cast<size_t>(row) * a.row_bytes +
+                                                   16 * c16_of[k] +
+                                                   static_cast<size_t>(c) * kStageRowBytes);
+      }
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k) {
+      if (live[k]) {
+        uint2 *d = reinterpret_cast<uint2 *>(stage + dst[k]);
+        d[0] = make_uint2(regs[k].x, regs[k].y);
+        d[1] = make_uint2(regs[k].z, regs[k].w);
+      }
+    }
+  };
+
+  if (n_items > 0) gload(0);  // the first weight chunk is in flight while x is prepared
+  i8_stage_x(a, smem, bf, arows, 64 * RT);
+  __syncthreads();  // x staging visible to every wave
+  if (n_items > 0) {
+    lstore();
+    if (n_items > 1) gload(1);
+  }
+  float tot = 0.0f;
+  for (int q = 0; q < n_items; ++q) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int c = q % n_chunks;
+    tot = i8_chunk(stage, al, bl, arows, n, g, c * kStageBlocks, tot);
+    if (c == n_chunks - 1) {  // the tile's last chunk: its outputs are final
+      const int row = item_tile(q) * 16 + n;
+      if (g < a.n_tok && row < a.n_rows) a.y[static_cast<size_t>(g) * a.y_stride + row] = tot;
+      tot = 0.0f;
+    }
+    if (q + 1 < n_items) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      lstore();  // item q + 1 replaces item q (this wave finished reading it)
+      if (q + 2 < n_items) gload(q + 2);
+    }
+  }
 }
 
 // Any ne0 or alignment: the scalar reference loop (src/kernels.rs:633-653),
@@ -876,17 +947,17 @@ int launch_staged(const MmArgs &a, hipStream_t st) {
   return ok();
 }
 
-template <int KS, bool INLINE, int RT = 8 / KS>
+template <int KS, int RT = 8 / KS>
 int launch_i8(const MmI8Args &a, size_t lds_a, hipStream_t st) {
   const int tiles = (a.n_rows + 15) / 16;
   const unsigned gx = static_cast<unsigned>((tiles + RT - 1) / RT);
   const size_t lds = lds_a + static_cast<size_t>(KS * RT) * kStageWaveBytes;
-  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT, INLINE>),
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(lds)),
                         "hipFuncSetAttribute"))
     return e;
-  BH_LAUNCH((pq2_i8_kernel<KS, RT, INLINE>), gx, 64 * KS * RT, lds, st, a);
+  BH_LAUNCH((pq2_i8_kernel<KS, RT>), gx, 64 * KS * RT, lds, st, a);
   return ok();
 }
 
@@ -904,34 +975,33 @@ int cu_count() {
   return cached[dev];
 }
 
-// The integer product for n_tok <= kI8Tok on staged shapes, 8 waves per
-// workgroup.  Up to kI8InlineTiles row tiles (the grid fits the chip about
-// once) every workgroup turns x into its digit fragments in LDS while its
-// first weight chunk loads: no prepare launch, no scratch (ffn_up N=1:
-// 20.3 -> 14.9 us).  Larger matrices run several rounds of workgroups,
-// which would each repeat that work, so a prepare launch writes the
-// fragments once and workgroups copy them (LM head N=1: 73 us vs 80).
-// Small matrices split each row tile's chunks over KS waves so the grid
-// still holds a few thousand waves.
-constexpr size_t kI8InlineTiles = 4096;
+// The integer product for n_tok <= kI8Tok on staged shapes.  Every
+// workgroup turns x into its digit fragments in LDS while its first weight
+// chunks load: no prepare launch, no scratch (ffn_up N=1: 20.3 -> 14.9 us
+// against a prepare launch).  Up to kI8RoundTiles row tiles the grid is one
+// workgroup per tile group, and small matrices split each row tile's chunks
+// over KS waves so the grid still holds a few thousand waves; beyond that
+// (the LM head) a persistent grid of one round walks the tiles, so the x
+// preparation is not repeated by later rounds of workgroups.
+constexpr size_t kI8RoundTiles = 4096;
 int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok, float *y,
            size_t a_bytes, hipStream_t st) {
   const int nblk = static_cast<int>(ne0 / 128);
-  MmI8Args a{w, x, nullptr, nullptr, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
+  MmI8Args a{w, x, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
              static_cast<int>(n_tok), static_cast<int>(n_rows)};
   const size_t lds = a_bytes;
   const size_t tiles = (n_rows + 15) / 16;
   const int n_chunks = nblk / kStageBlocks;
   int ks = 1;
   while (ks < 8 && ks < n_chunks && tiles * ks < 4096) ks *= 2;
-  if (tiles <= kI8InlineTiles) {
+  if (tiles <= kI8RoundTiles) {
     // wide x (an 8-wave workgroup's LDS leaves room for one per CU) and few
     // row tiles: two tiles per 16-wave workgroup, 8 waves each, so the grid
     // is one round over the CUs instead of two (ffn_down N=1, 320 row tiles:
     // 13.7 us, against 20.2 with 8 waves and 14.8 with 4 waves per tile)
     if (n_chunks >= 8 && 2 * (a_bytes + 8 * kStageWaveBytes) > 160 * 1024 &&
         tiles <= 2 * static_cast<size_t>(cu_count()) && a_bytes + 16 * kStageWaveBytes <= 160 * 1024)
-      return launch_i8<8, true, 2>(a, lds, st);
+      return launch_i8<8, 2>(a, lds, st);
     // the most waves per row tile whose grid still runs in one round: a
     // workgroup is 8 waves (8 / ks row tiles), as many per CU as LDS and the
     // wave limit allow (ffn_up N=1: 4 waves per tile made 544 workgroups for
@@ -947,25 +1017,25 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
       }
     }
     switch (ks) {
-      case 8: return launch_i8<8, true>(a, lds, st);
-      case 4: return launch_i8<4, true>(a, lds, st);
-      case 2: return launch_i8<2, true>(a, lds, st);
-      default: return launch_i8<1, true>(a, lds, st);
+      case 8: return launch_i8<8>(a, lds, st);
+      case 4: return launch_i8<4>(a, lds, st);
+      case 2: return launch_i8<2>(a, lds, st);
+      default: return launch_i8<1>(a, lds, st);
     }
   }
-  const size_t frag_bytes = static_cast<size_t>(2 * nblk) * 64 * sizeof(uint4);
-  const size_t bfac_off = (frag_bytes + 255) / 256 * 256;
-  const size_t bfac_bytes = static_cast<size_t>(nblk) * kI8Tok * sizeof(float2);
-  char *scratch = static_cast<char *>(device_scratch(bfac_off + bfac_bytes, kScratchMatmul));
-  if (scratch == nullptr) return BH_ERR_HIP;
-  PrepI8Args pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float2 *>(scratch + bfac_off),
-                static_cast<int>(ne0), static_cast<int>(n_tok), nblk};
-  const size_t items = n_tok * nblk * 8;
-  BH_LAUNCH(pq2_i8_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
-            kMmThreads, 0, st, pa);
-  a.afrag = pa.afrag;
-  a.bfac = pa.bfac;
-  return launch_i8<1, false>(a, lds, st);  // > 4096 tiles: ks stays 1
+  // many row tiles: the persistent kernel, one round of 8-wave workgroups
+  constexpr int kPRT = 8;
+  const size_t plds = a_bytes + kPRT * kStageWaveBytes;
+  const size_t per_cu = std::max<size_t>(1, std::min<size_t>(4, (160 * 1024) / plds));
+  const size_t groups = (tiles + kPRT - 1) / kPRT;
+  const size_t G = std::min(groups, per_cu * static_cast<size_t>(cu_count()));
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_persist_kernel<kPRT>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(plds)),
+                        "hipFuncSetAttribute"))
+    return e;
+  BH_LAUNCH(pq2_i8_persist_kernel<kPRT>, static_cast<unsigned>(G), 64 * kPRT, plds, st, a);
+  return ok();
 }
 
 // Y[n_tok][n_rows] = X[n_tok][ne0] * W[rows][ne0]^T on the device.

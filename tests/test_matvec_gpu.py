@@ -113,6 +113,19 @@ def test_matmul_wide_row_tiles(bh, oracle, synth, dev, n_tok):
     assert _per_token_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("n_tok", [1, 3])
+def test_matvec_many_row_tiles_persistent(bh, oracle, synth, dev, n_tok):
+    """More than 4096 row tiles on the integer path (up to 4 tokens): the
+    persistent grid, each wave walking several tiles, with a ragged tail."""
+    ne0, n_rows = 1024, 4096 * 16 + 1000 + 13
+    _say("persistent", n_tok, n_rows)
+    table = synth.pq2_table(synth.Rng(21), n_rows, ne0)
+    x = synth.Rng(22).normal(n_tok * ne0).reshape(n_tok, ne0)
+    ref = oracle.pq2_matmul_n(table, ne0, n_rows, x)
+    got = _h(bh.pq2_matmul_n(_dev_table(table, dev), ne0, n_rows, _t(x, dev)))
+    assert _per_token_err(got, ref) <= TOL
+
+
 def test_matmul_dynamic_range(bh, oracle, synth, dev):
     """Tokens of magnitude 1e-30 .. 1e30, outliers, and zero tokens: the
     per-token power-of-two scaling keeps every token at the bar."""
