@@ -22,7 +22,10 @@
  *
  * Numerics follow the reference CPU path: f32 storage, f64 accumulation where
  * the Rust accumulates in f64 (l2_norm_rows, softmax_rows), libm-accurate
- * expf/logf/sinf/cosf, no FMA contraction.  The PQ2_0 decode is bit-exact.
+ * expf/logf/sinf/cosf, no FMA contraction -- except the two passes of the
+ * softmax over rows too wide for one workgroup, which use the hardware base-2
+ * exponential with an FMA-compensated argument (a few 1e-7 relative, inside
+ * the softmax tolerance of 2e-5).  The PQ2_0 decode is bit-exact.
  *
  * Threading: every device entry point is re-entrant per stream, except
  * bh_softmax_rows on rows too wide for one workgroup, bh_attention, and the
