@@ -44,6 +44,13 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its global loads, so weight and fragment prefetches
+// stay in flight across it (__syncthreads() would also drain them).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Block column (0..127) of element e (0..7) of lane group g's A/B fragment
 // in MFMA step i (0..3) of a block.  Lane group g owns code bytes [8g, 8g+8)
 // of the block (columns [32g, 32g + 32)); step i uses the dword of code bytes
@@ -875,6 +882,195 @@ __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Integer product for more than kI8Tok tokens (prefill batches).  Tokens go
+// in groups of 4 (A rows 4 t + digit of an MFMA, as above).  A prepare launch
+// writes every group's digit fragments once, laid out so one block of all
+// groups is contiguous: uint4 [block][step in block][group][lane group][16
+// rows], block factors float2 [block][group][token slot].  A workgroup is 8
+// waves (8 row tiles of 16) x kGemmGroups token groups: per block, the
+// block's fragments of its groups (16 KB) are copied to a double-buffered
+// LDS stage shared by the 8 waves -- the next block's copy is loaded into
+// registers while the current block is multiplied -- and each wave decodes
+// its tile's codes once and runs two integer MFMAs per group.  The barrier
+// between blocks waits for LDS traffic only, so the weight chunks each wave
+// prefetches stay in flight across it.
+// ---------------------------------------------------------------------------
+constexpr int kGemmGroups = 8;   // token groups per workgroup (32 tokens)
+constexpr int kGemmWaves = 8;    // row tiles per workgroup
+constexpr int kGemmFragPerBlk = 2 * kGemmGroups * 4 * 16;  // uint4 per staged block
+constexpr int kGemmFacPerBlk = kGemmGroups * kI8Tok;         // float2 per staged block
+
+struct GemmI8Args {
+  const uint8_t *w;     // first row of the range
+  const uint4 *afrag;   // [nblk][2][n_groups][4][16]
+  const float2 *bfac;   // [nblk][n_groups][4]
+  float *y;             // [n_tok][y_stride]
+  size_t row_bytes;
+  int n_rows, nblk, n_tok, n_groups, y_stride;
+};
+
+struct GprepArgs {
+  const float *x;  // [n_tok][ne0]
+  uint4 *afrag;
+  float2 *bfac;
+  int ne0, n_tok, nblk, n_groups;
+};
+
+__global__ __launch_bounds__(kMmThreads) void pq2_gemm_i8_prep_kernel(GprepArgs a) {
+  const int item = blockIdx.x * kMmThreads + threadIdx.x;
+  const int tb = item >> 3, sub = item & 7;
+  const bool live = tb < a.n_tok * a.nblk;
+  const int t = live ? tb / a.nblk : 0, blk = live ? tb - t * a.nblk : 0;
+  uint4 frag[3];
+  float2 fac;
+  i8_prep_item(a.x + static_cast<size_t>(t) * a.ne0 + 128 * blk, sub, live, frag, fac);
+  if (!live) return;
+  const int grp = t / kI8Tok, tq = t % kI8Tok;
+  const int h = sub & 1, g = sub >> 1;
+  uint4 *dst = a.afrag + ((static_cast<size_t>(blk) * 2 + h) * a.n_groups + grp) * 64 + g * 16 + 4 * tq;
+#pragma unroll
+  for (int d = 0; d < 3; ++d) dst[d] = frag[d];
+  if (sub == 0) a.bfac[(static_cast<size_t>(blk) * a.n_groups + grp) * kI8Tok + tq] = fac;
+}
+
+__global__ __launch_bounds__(64 * kGemmWaves) void pq2_gemm_i8_kernel(GemmI8Args a) {
+  extern __shared__ uint4 smem[];
+  constexpr int kThreads = 64 * kGemmWaves;
+  uint4 *sa = smem;                                                  // [2][kGemmFragPerBlk]
+  float2 *sf = reinterpret_cast<float2 *>(smem + 2 * kGemmFragPerBlk);  // [2][kGemmFacPerBlk]
+  uint8_t *stage = reinterpret_cast<uint8_t *>(sf + 2 * kGemmFacPerBlk) +
+                   (threadIdx.x >> 6) * kStageWaveBytes;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int row0 = (blockIdx.x * kGemmWaves + wave) * 16;
+  const int grp0 = blockIdx.y * kGemmGroups;
+  const int ng = a.n_groups - grp0 < kGemmGroups ? a.n_groups - grp0 : kGemmGroups;
+
+  // weight staging per wave, as pq2_i8_kernel (8-block chunks, 17 x 16 B per row)
+  const uint8_t *src[kStageLoads];
+  int dst[kStageLoads];
+  bool live[kStageLoads];
+#pragma unroll
+  for (int k = 0; k < kStageLoads; ++k) {
+    const int idx = lane + 64 * k;
+    live[k] = idx < 16 * kStageF4;
+    const int r = live[k] ? idx / kStageF4 : 0, c16 = live[k] ? idx % kStageF4 : 0;
+    int row = row0 + r;
+    row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
+    src[k] = a.w + static_cast<size_t>(row) * a.row_bytes + 16 * c16;
+    dst[k] = r * kStageStride + 16 * c16;
+  }
+  uint4 regs[kStageLoads];
+  auto gload = [&](int chunk) {
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k)
+      if (live[k]) regs[k] = *reinterpret_cast<const uint4 *>(src[k] + static_cast<size_t>(chunk) * kStageRowBytes);
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int k = 0; k < kStageLoads; ++k) {
+      if (live[k]) {
+        uint2 *d = reinterpret_cast<uint2 *>(stage + dst[k]);
+        d[0] = make_uint2(regs[k].x, regs[k].y);
+        d[1] = make_uint2(regs[k].z, regs[k].w);
+      }
+    }
+  };
+  // the workgroup's fragments of block b: step h of group gi at [h][gi][64];
+  // each lane moves one uint4 of each step (two named registers: an array
+  // here is indexed through a pointer select and lands in scratch memory)
+  static_assert(kGemmFragPerBlk == 2 * kThreads, "one uint4 per lane and step");
+  const int fgi = static_cast<int>(threadIdx.x) >> 6;
+  const bool flive = fgi < ng;
+  const uint4 *fsrc = a.afrag + static_cast<size_t>(grp0 + (flive ? fgi : 0)) * 64 + lane;
+  const size_t fstep = static_cast<size_t>(a.n_groups) * 64;
+  uint4 fr0 = make_uint4(0, 0, 0, 0), fr1 = make_uint4(0, 0, 0, 0);
+  float2 fc = make_float2(0.f, 0.f);
+  const bool fclive = threadIdx.x < kGemmFacPerBlk && static_cast<int>(threadIdx.x) / kI8Tok < ng;
+  auto fload = [&](int b) {
+    if (flive) {
+      fr0 = fsrc[(2 * static_cast<size_t>(b)) * fstep];
+      fr1 = fsrc[(2 * static_cast<size_t>(b) + 1) * fstep];
+    }
+    if (fclive) fc = a.bfac[(static_cast<size_t>(b) * a.n_groups + grp0) * kI8Tok + threadIdx.x];
+  };
+  auto fstore = [&](int b) {
+    sa[(b & 1) * kGemmFragPerBlk + threadIdx.x] = fr0;
+    sa[(b & 1) * kGemmFragPerBlk + kThreads + threadIdx.x] = fr1;
+    if (threadIdx.x < kGemmFacPerBlk) sf[(b & 1) * kGemmFacPerBlk + threadIdx.x] = fc;
+  };
+
+  float tot[kGemmGroups];
+#pragma unroll
+  for (int gi = 0; gi < kGemmGroups; ++gi) tot[gi] = 0.0f;
+  const int n_chunks = a.nblk / kStageBlocks;
+  gload(0);
+  fload(0);
+  fstore(0);
+  lstore();
+  if (n_chunks > 1) gload(1);
+  if (a.nblk > 1) fload(1);
+  lds_barrier();  // block 0's fragments and this wave's first chunk staged
+  for (int c = 0; c < n_chunks; ++c) {
+    const uint8_t *rowp = stage + n * kStageStride;
+    for (int bb = 0; bb < kStageBlocks; ++bb) {
+      const int b = c * kStageBlocks + bb;
+      const uint8_t *blk = rowp + kPq2Blk * bb;
+      uint32_t cd0, cd1;
+      float sc;
+      if ((bb & 1) == 0) {  // block starts on a dword: codes are 2 bytes in
+        const uint32_t e0 = lds_u32(blk + 8 * g), e1 = lds_u32(blk + 8 * g + 4),
+                       e2 = lds_u32(blk + 8 * g + 8);
+        cd0 = __builtin_amdgcn_alignbyte(e1, e0, 2);
+        cd1 = __builtin_amdgcn_alignbyte(e2, e1, 2);
+        sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk))));
+      } else {  // block starts 2 bytes into a dword: codes are dword-aligned
+        cd0 = lds_u32(blk + 2 + 8 * g);
+        cd1 = lds_u32(blk + 6 + 8 * g);
+        sc = static_cast<float>(
+            __builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk - 2) >> 16)));
+      }
+      const i4v b0 = decode_i8(cd0), b1 = decode_i8(cd1);
+      const uint4 *fa = sa + (b & 1) * kGemmFragPerBlk + g * 16 + n;
+      const float2 *ff = sf + (b & 1) * kGemmFacPerBlk + g;
+#pragma unroll
+      for (int gi = 0; gi < kGemmGroups; ++gi) {
+        if (gi < ng) {
+          const i4v a0 = __builtin_bit_cast(i4v, fa[gi * 64]);
+          const i4v a1 = __builtin_bit_cast(i4v, fa[(kGemmGroups + gi) * 64]);
+          i4v acc = i4v{0, 0, 0, 0};
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
+          const float2 f = ff[gi * kI8Tok];
+          const uint32_t v = (static_cast<uint32_t>(acc[0]) << 16) +
+                             (static_cast<uint32_t>(acc[1]) << 8) + static_cast<uint32_t>(acc[2]) -
+                             __float_as_uint(f.x);
+          const float blk_sum = static_cast<float>(static_cast<int>(v)) * f.y;  // times 2^-e: exact
+          tot[gi] = fmaf(blk_sum, sc, tot[gi]);  // src/kernels.rs:651
+        }
+      }
+      // block b + 1's fragments to the other buffer (its readers passed the
+      // last barrier), block b + 2's requested
+      if (b + 1 < a.nblk) fstore(b + 1);
+      if (b + 2 < a.nblk) fload(b + 2);
+      if (bb == kStageBlocks - 1 && c + 1 < n_chunks) {
+        lstore();  // chunk c + 1 replaces chunk c (this wave finished reading it)
+        if (c + 2 < n_chunks) gload(c + 2);
+      }
+      lds_barrier();
+    }
+  }
+  const int row = row0 + n;
+  if (row < a.n_rows) {
+#pragma unroll
+    for (int gi = 0; gi < kGemmGroups; ++gi) {
+      const int t = (grp0 + gi) * kI8Tok + g;
+      if (gi < ng && t < a.n_tok) a.y[static_cast<size_t>(t) * a.y_stride + row] = tot[gi];
+    }
+  }
+}
+
 // Any ne0 or alignment: the scalar reference loop (src/kernels.rs:633-653),
 // one wave per (row, token), lanes over blocks, block sums in order, then a
 // fixed-order reduction of the lanes' scale * block_sum terms.
@@ -1038,6 +1234,38 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   return ok();
 }
 
+// Integer product for more than kI8Tok tokens: prepare launch, then one
+// product launch over (row-tile groups of 8, token-group sets of 8).
+int pq2_gemm_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok,
+                float *y, hipStream_t st) {
+  const int nblk = static_cast<int>(ne0 / 128);
+  const int n_groups = static_cast<int>((n_tok + kI8Tok - 1) / kI8Tok);
+  const size_t frag_bytes = static_cast<size_t>(nblk) * 2 * n_groups * 64 * sizeof(uint4);
+  const size_t fac_off = (frag_bytes + 255) / 256 * 256;
+  const size_t fac_bytes = static_cast<size_t>(nblk) * n_groups * kI8Tok * sizeof(float2);
+  char *scratch = static_cast<char *>(device_scratch(fac_off + fac_bytes, kScratchMatmul));
+  if (scratch == nullptr) return BH_ERR_HIP;
+  GprepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float2 *>(scratch + fac_off),
+               static_cast<int>(ne0), static_cast<int>(n_tok), nblk, n_groups};
+  const size_t items = n_tok * nblk * 8;
+  BH_LAUNCH(pq2_gemm_i8_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
+            kMmThreads, 0, st, pa);
+  GemmI8Args a{w, pa.afrag, pa.bfac, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
+               static_cast<int>(n_tok), n_groups, static_cast<int>(n_rows)};
+  const size_t lds = 2 * kGemmFragPerBlk * sizeof(uint4) + 2 * kGemmFacPerBlk * sizeof(float2) +
+                     kGemmWaves * kStageWaveBytes;
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_gemm_i8_kernel),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(lds)),
+                        "hipFuncSetAttribute"))
+    return e;
+  const unsigned gx = static_cast<unsigned>((n_rows + 16 * kGemmWaves - 1) / (16 * kGemmWaves));
+  const unsigned gy = static_cast<unsigned>((n_groups + kGemmGroups - 1) / kGemmGroups);
+  if (gy > 65535) return fail(BH_ERR_SHAPE, "pq2_matmul_n: too many tokens for one launch");
+  BH_LAUNCH(pq2_gemm_i8_kernel, dim3(gx, gy), 64 * kGemmWaves, lds, st, a);
+  return ok();
+}
+
 // Y[n_tok][n_rows] = X[n_tok][ne0] * W[rows][ne0]^T on the device.
 int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok, float *y,
            hipStream_t st) {
@@ -1070,6 +1298,7 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
                            (nblk * kI8Tok * sizeof(float2) + 15) / 16 * 16;
     if (a_bytes <= kLdsABytes) return pq2_i8(w, ne0, n_rows, x, n_tok, y, a_bytes, st);
   }
+  if (stageable && n_tok > static_cast<size_t>(kI8Tok)) return pq2_gemm_i8(w, ne0, n_rows, x, n_tok, y, st);
   const int n_ksteps = static_cast<int>(ne0 / 32);
   const int n_tiles = static_cast<int>((n_tok + 15) / 16);
   const int mt = n_tiles >= 4 ? 4 : (n_tiles >= 2 ? 2 : 1);

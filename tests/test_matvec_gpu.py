@@ -101,6 +101,22 @@ def test_matmul_token_counts(bh, oracle, synth, dev, n_tok):
     assert _per_token_err(got, ref) <= TOL
 
 
+@pytest.mark.parametrize("ne0,n_rows,n_tok", [
+    (5120, 700, 37),      # several chunks, a partial token-group set and row tile
+    (2048, 129, 260),     # 65 token groups: a second launch row of sets, one live group
+    (17408, 48, 9),       # ffn_down's width, 136 blocks, three groups
+])
+def test_matmul_prefill_shapes(bh, oracle, synth, dev, ne0, n_rows, n_tok):
+    """The integer product for more than 4 tokens: x fragments prepared once
+    into scratch, 8 row tiles x 8 token groups per workgroup."""
+    _say("prefill", ne0, n_rows, n_tok)
+    table = synth.pq2_table(synth.Rng(ne0 + n_tok), n_rows, ne0)
+    x = synth.Rng(500 + n_tok).normal(n_tok * ne0).reshape(n_tok, ne0)
+    ref = oracle.pq2_matmul_n(table, ne0, n_rows, x)
+    got = _h(bh.pq2_matmul_n(_dev_table(table, dev), ne0, n_rows, _t(x, dev)))
+    assert _per_token_err(got, ref) <= TOL
+
+
 @pytest.mark.parametrize("n_tok", [1, 16, 40])
 def test_matmul_wide_row_tiles(bh, oracle, synth, dev, n_tok):
     """Enough rows for the 4-tiles-per-wave kernel, with a ragged tail."""
