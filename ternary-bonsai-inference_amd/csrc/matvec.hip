@@ -457,7 +457,6 @@ __global__ __launch_bounds__(kMmThreads) void pq2_mm_staged_kernel(MmArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const uint8_t *rowp = stage + n * kStageStride;
-#pragma unroll 2
     for (int bb = 0; bb < kStageBlocks; ++bb) {
       const int b = c * kStageBlocks + bb;
       const uint8_t *blk = rowp + kPq2Blk * bb;
@@ -887,19 +886,15 @@ __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
 // in groups of 4 (A rows 4 t + digit of an MFMA, as above).  A prepare launch
 // writes every group's digit fragments once, laid out so one block of all
 // groups is contiguous: uint4 [block][step in block][group][lane group][16
-// rows], block factors float2 [block][group][token slot].  A workgroup is 8
-// waves (8 row tiles of 16) x kGemmGroups token groups: per block, the
-// block's fragments of its groups (16 KB) are copied to a double-buffered
-// LDS stage shared by the 8 waves -- the next block's copy is loaded into
+// rows], block factors float2 [block][group][token slot].  A workgroup is W
+// waves (W row tiles of 16) x G token groups: per block, the block's
+// fragments of its groups (2 G KB) are copied to a double-buffered LDS
+// stage shared by the W waves -- the next block's copy is loaded into
 // registers while the current block is multiplied -- and each wave decodes
 // its tile's codes once and runs two integer MFMAs per group.  The barrier
 // between blocks waits for LDS traffic only, so the weight chunks each wave
 // prefetches stay in flight across it.
 // ---------------------------------------------------------------------------
-constexpr int kGemmGroups = 8;   // token groups per workgroup (32 tokens)
-constexpr int kGemmWaves = 8;    // row tiles per workgroup
-constexpr int kGemmFragPerBlk = 2 * kGemmGroups * 4 * 16;  // uint4 per staged block
-constexpr int kGemmFacPerBlk = kGemmGroups * kI8Tok;         // float2 per staged block
 
 struct GemmI8Args {
   const uint8_t *w;     // first row of the range
@@ -934,18 +929,21 @@ __global__ __launch_bounds__(kMmThreads) void pq2_gemm_i8_prep_kernel(GprepArgs 
   if (sub == 0) a.bfac[(static_cast<size_t>(blk) * a.n_groups + grp) * kI8Tok + tq] = fac;
 }
 
-__global__ __launch_bounds__(64 * kGemmWaves) void pq2_gemm_i8_kernel(GemmI8Args a) {
+template <int W, int G>
+__global__ __launch_bounds__(64 * W) void pq2_gemm_i8_kernel(GemmI8Args a) {
   extern __shared__ uint4 smem[];
-  constexpr int kThreads = 64 * kGemmWaves;
-  uint4 *sa = smem;                                                  // [2][kGemmFragPerBlk]
-  float2 *sf = reinterpret_cast<float2 *>(smem + 2 * kGemmFragPerBlk);  // [2][kGemmFacPerBlk]
-  uint8_t *stage = reinterpret_cast<uint8_t *>(sf + 2 * kGemmFacPerBlk) +
-                   (threadIdx.x >> 6) * kStageWaveBytes;
+  constexpr int kThreads = 64 * W;
+  constexpr int kFrag = 2 * G * 64;  // uint4 per staged block
+  constexpr int kFac = G * kI8Tok;   // float2 per staged block
+  static_assert(kFrag <= 2 * kThreads && kFac <= kThreads, "at most two uint4 per lane");
+  uint4 *sa = smem;                                       // [2][kFrag]
+  float2 *sf = reinterpret_cast<float2 *>(smem + 2 * kFrag);  // [2][kFac]
+  uint8_t *stage = reinterpret_cast<uint8_t *>(sf + 2 * kFac) + (threadIdx.x >> 6) * kStageWaveBytes;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int row0 = (blockIdx.x * kGemmWaves + wave) * 16;
-  const int grp0 = blockIdx.y * kGemmGroups;
-  const int ng = a.n_groups - grp0 < kGemmGroups ? a.n_groups - grp0 : kGemmGroups;
+  const int row0 = (blockIdx.x * W + wave) * 16;
+  const int grp0 = blockIdx.y * G;
+  const int ng = a.n_groups - grp0 < G ? a.n_groups - grp0 : G;
 
   // weight staging per wave, as pq2_i8_kernel (8-block chunks, 17 x 16 B per row)
   const uint8_t *src[kStageLoads];
@@ -978,32 +976,37 @@ __global__ __launch_bounds__(64 * kGemmWaves) void pq2_gemm_i8_kernel(GemmI8Args
     }
   };
   // the workgroup's fragments of block b: step h of group gi at [h][gi][64];
-  // each lane moves one uint4 of each step (two named registers: an array
+  // lane i moves uint4 i and i + kThreads (two named registers: an array
   // here is indexed through a pointer select and lands in scratch memory)
-  static_assert(kGemmFragPerBlk == 2 * kThreads, "one uint4 per lane and step");
-  const int fgi = static_cast<int>(threadIdx.x) >> 6;
-  const bool flive = fgi < ng;
-  const uint4 *fsrc = a.afrag + static_cast<size_t>(grp0 + (flive ? fgi : 0)) * 64 + lane;
-  const size_t fstep = static_cast<size_t>(a.n_groups) * 64;
+  const size_t fblk = 2 * static_cast<size_t>(a.n_groups) * 64;  // uint4 per block, all groups
+  auto fsrc_of = [&](int i, bool &live_i) {
+    const int h = i / (G * 64), gi = (i / 64) % G;
+    live_i = i < kFrag && gi < ng;
+    return a.afrag + (static_cast<size_t>(h) * a.n_groups + grp0 + (live_i ? gi : 0)) * 64 + (i & 63);
+  };
+  bool fl0, fl1;
+  const uint4 *fs0 = fsrc_of(static_cast<int>(threadIdx.x), fl0);
+  const uint4 *fs1 = fsrc_of(static_cast<int>(threadIdx.x) + kThreads, fl1);
   uint4 fr0 = make_uint4(0, 0, 0, 0), fr1 = make_uint4(0, 0, 0, 0);
   float2 fc = make_float2(0.f, 0.f);
-  const bool fclive = threadIdx.x < kGemmFacPerBlk && static_cast<int>(threadIdx.x) / kI8Tok < ng;
+  const bool fclive = threadIdx.x < kFac && static_cast<int>(threadIdx.x) / kI8Tok < ng;
+  // predicated loads and a branch per group keep the register count low
+  // (unconditional loads and straight-line groups measured slower: more
+  // registers, fewer waves per SIMD)
   auto fload = [&](int b) {
-    if (flive) {
-      fr0 = fsrc[(2 * static_cast<size_t>(b)) * fstep];
-      fr1 = fsrc[(2 * static_cast<size_t>(b) + 1) * fstep];
-    }
+    if (fl0) fr0 = fs0[b * fblk];
+    if (fl1) fr1 = fs1[b * fblk];
     if (fclive) fc = a.bfac[(static_cast<size_t>(b) * a.n_groups + grp0) * kI8Tok + threadIdx.x];
   };
   auto fstore = [&](int b) {
-    sa[(b & 1) * kGemmFragPerBlk + threadIdx.x] = fr0;
-    sa[(b & 1) * kGemmFragPerBlk + kThreads + threadIdx.x] = fr1;
-    if (threadIdx.x < kGemmFacPerBlk) sf[(b & 1) * kGemmFacPerBlk + threadIdx.x] = fc;
+    if (threadIdx.x < kFrag) sa[(b & 1) * kFrag + threadIdx.x] = fr0;
+    if (threadIdx.x + kThreads < kFrag) sa[(b & 1) * kFrag + kThreads + threadIdx.x] = fr1;
+    if (threadIdx.x < kFac) sf[(b & 1) * kFac + threadIdx.x] = fc;
   };
 
-  float tot[kGemmGroups];
+  float tot[G];
 #pragma unroll
-  for (int gi = 0; gi < kGemmGroups; ++gi) tot[gi] = 0.0f;
+  for (int gi = 0; gi < G; ++gi) tot[gi] = 0.0f;
   const int n_chunks = a.nblk / kStageBlocks;
   gload(0);
   fload(0);
@@ -1032,13 +1035,13 @@ __global__ __launch_bounds__(64 * kGemmWaves) void pq2_gemm_i8_kernel(GemmI8Args
             __builtin_bit_cast(_Float16, static_cast<uint16_t>(lds_u32(blk - 2) >> 16)));
       }
       const i4v b0 = decode_i8(cd0), b1 = decode_i8(cd1);
-      const uint4 *fa = sa + (b & 1) * kGemmFragPerBlk + g * 16 + n;
-      const float2 *ff = sf + (b & 1) * kGemmFacPerBlk + g;
+      const uint4 *fa = sa + (b & 1) * kFrag + g * 16 + n;
+      const float2 *ff = sf + (b & 1) * kFac + g;
 #pragma unroll
-      for (int gi = 0; gi < kGemmGroups; ++gi) {
+      for (int gi = 0; gi < G; ++gi) {
         if (gi < ng) {
           const i4v a0 = __builtin_bit_cast(i4v, fa[gi * 64]);
-          const i4v a1 = __builtin_bit_cast(i4v, fa[(kGemmGroups + gi) * 64]);
+          const i4v a1 = __builtin_bit_cast(i4v, fa[(G + gi) * 64]);
           i4v acc = i4v{0, 0, 0, 0};
           acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, acc, 0, 0, 0);
           acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, acc, 0, 0, 0);
@@ -1064,7 +1067,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void pq2_gemm_i8_kernel(GemmI8Args
   const int row = row0 + n;
   if (row < a.n_rows) {
 #pragma unroll
-    for (int gi = 0; gi < kGemmGroups; ++gi) {
+    for (int gi = 0; gi < G; ++gi) {
       const int t = (grp0 + gi) * kI8Tok + g;
       if (gi < ng && t < a.n_tok) a.y[static_cast<size_t>(t) * a.y_stride + row] = tot[gi];
     }
@@ -1234,6 +1237,22 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   return ok();
 }
 
+template <int W, int G>
+int launch_gemm(const GemmI8Args &a, int n_groups, hipStream_t st) {
+  const size_t lds = 2 * (2 * G * 64) * sizeof(uint4) + 2 * (G * kI8Tok) * sizeof(float2) +
+                     W * kStageWaveBytes;
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_gemm_i8_kernel<W, G>),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(lds)),
+                        "hipFuncSetAttribute"))
+    return e;
+  const unsigned gx = static_cast<unsigned>((a.n_rows + 16 * W - 1) / (16 * W));
+  const unsigned gy = static_cast<unsigned>((n_groups + G - 1) / G);
+  if (gy > 65535) return fail(BH_ERR_SHAPE, "pq2_matmul_n: too many tokens for one launch");
+  BH_LAUNCH((pq2_gemm_i8_kernel<W, G>), dim3(gx, gy), 64 * W, lds, st, a);
+  return ok();
+}
+
 // Integer product for more than kI8Tok tokens: prepare launch, then one
 // product launch over (row-tile groups of 8, token-group sets of 8).
 int pq2_gemm_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok,
@@ -1252,18 +1271,10 @@ int pq2_gemm_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, siz
             kMmThreads, 0, st, pa);
   GemmI8Args a{w, pa.afrag, pa.bfac, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
                static_cast<int>(n_tok), n_groups, static_cast<int>(n_rows)};
-  const size_t lds = 2 * kGemmFragPerBlk * sizeof(uint4) + 2 * kGemmFacPerBlk * sizeof(float2) +
-                     kGemmWaves * kStageWaveBytes;
-  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_gemm_i8_kernel),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            static_cast<int>(lds)),
-                        "hipFuncSetAttribute"))
-    return e;
-  const unsigned gx = static_cast<unsigned>((n_rows + 16 * kGemmWaves - 1) / (16 * kGemmWaves));
-  const unsigned gy = static_cast<unsigned>((n_groups + kGemmGroups - 1) / kGemmGroups);
-  if (gy > 65535) return fail(BH_ERR_SHAPE, "pq2_matmul_n: too many tokens for one launch");
-  BH_LAUNCH(pq2_gemm_i8_kernel, dim3(gx, gy), 64 * kGemmWaves, lds, st, a);
-  return ok();
+  // 8 row tiles x 4 token groups (16 tokens) per workgroup: of 8x8, 8x4,
+  // 8x2, 8x1, 4x4 and 4x2 the fastest for ffn_up N=64 and the LM head N=16
+  // (more workgroups per CU outweigh the extra weight passes of smaller sets)
+  return launch_gemm<8, 4>(a, n_groups, st);
 }
 
 // Y[n_tok][n_rows] = X[n_tok][ne0] * W[rows][ne0]^T on the device.
