@@ -214,13 +214,23 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int pass = 0; pass < 4; ++pass) {
         const size_t p = t0 + pass * 16 + grp;
-        float part[4];
+        // fused multiply-adds, two chains of 8 dims (the library builds
+        // with contraction off, so a * b + c would cost two instructions)
+        float part[2];
 #pragma unroll
-        for (int x = 0; x < 4; ++x) {
-          const f32x4 kv = kr[pass][x];
-          part[x] = (qv[x].x * kv.x + qv[x].y * kv.y) + (qv[x].z * kv.z + qv[x].w * kv.w);
+        for (int h = 0; h < 2; ++h) {
+          const f32x4 k0 = kr[pass][2 * h], k1 = kr[pass][2 * h + 1];
+          const f32x4 q0 = qv[2 * h], q1 = qv[2 * h + 1];
+          float s = q0.x * k0.x;
+          s = fmaf(q0.y, k0.y, s);
+          s = fmaf(q0.z, k0.z, s);
+          s = fmaf(q0.w, k0.w, s);
+          s = fmaf(q1.x, k1.x, s);
+          s = fmaf(q1.y, k1.y, s);
+          s = fmaf(q1.z, k1.z, s);
+          part[h] = fmaf(q1.w, k1.w, s);
         }
-        const float d = row16_sum((part[0] + part[1]) + (part[2] + part[3]));
+        const float d = row16_sum(part[0] + part[1]);
         if (sub == 0) s_e[pass * 16 + grp][r] = p < end ? d * a.scale : -INFINITY;
       }
     }
@@ -266,10 +276,10 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
           const float e = s_e[j][r];
-          acc[r][0] += e * v.x;
-          acc[r][1] += e * v.y;
-          acc[r][2] += e * v.z;
-          acc[r][3] += e * v.w;
+          acc[r][0] = fmaf(e, v.x, acc[r][0]);
+          acc[r][1] = fmaf(e, v.y, acc[r][1]);
+          acc[r][2] = fmaf(e, v.z, acc[r][2]);
+          acc[r][3] = fmaf(e, v.w, acc[r][3]);
         }
       }
     }
