@@ -58,11 +58,12 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
-// In-lane part of a dot over the lane's 8 elements, as a depth-3 tree.
+// In-lane part of a dot over the lane's 8 elements: two fused multiply-add
+// chains (the library builds with contraction off) and their sum.
 __device__ __forceinline__ float part8(const float (&m)[kPerLane], const float4 a, const float4 b) {
-  const float s0 = m[0] * a.x + m[1] * a.y, s1 = m[2] * a.z + m[3] * a.w;
-  const float s2 = m[4] * b.x + m[5] * b.y, s3 = m[6] * b.z + m[7] * b.w;
-  return (s0 + s1) + (s2 + s3);
+  const float s0 = fmaf(m[3], a.w, fmaf(m[2], a.z, fmaf(m[1], a.y, m[0] * a.x)));
+  const float s1 = fmaf(m[7], b.w, fmaf(m[6], b.z, fmaf(m[5], b.y, m[4] * b.x)));
+  return s0 + s1;
 }
 
 // One token on the lane's 8 state floats; returns the row's attn value
@@ -80,12 +81,12 @@ __device__ __forceinline__ float token_step(float (&m)[kPerLane], const float4 k
   const float kq = row16_sum(part8({k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w}, q0, q1));
   const float dk = row16_sum(part8(m, k0, k1));
   const float dq = row16_sum(part8(m, q0, q1));
-  const float delta = (v - eg * dk) * beta;
-  m[0] = eg * m[0] + k0.x * delta; m[1] = eg * m[1] + k0.y * delta;
-  m[2] = eg * m[2] + k0.z * delta; m[3] = eg * m[3] + k0.w * delta;
-  m[4] = eg * m[4] + k1.x * delta; m[5] = eg * m[5] + k1.y * delta;
-  m[6] = eg * m[6] + k1.z * delta; m[7] = eg * m[7] + k1.w * delta;
-  return (eg * dq + delta * kq) * scale;
+  const float delta = fmaf(-eg, dk, v) * beta;
+  m[0] = fmaf(k0.x, delta, eg * m[0]); m[1] = fmaf(k0.y, delta, eg * m[1]);
+  m[2] = fmaf(k0.z, delta, eg * m[2]); m[3] = fmaf(k0.w, delta, eg * m[3]);
+  m[4] = fmaf(k1.x, delta, eg * m[4]); m[5] = fmaf(k1.y, delta, eg * m[5]);
+  m[6] = fmaf(k1.z, delta, eg * m[6]); m[7] = fmaf(k1.w, delta, eg * m[7]);
+  return fmaf(eg, dq, delta * kq) * scale;
 }
 
 __device__ __forceinline__ void load_state(const float *mp, float (&m)[kPerLane]) {
@@ -244,7 +245,8 @@ __device__ __forceinline__ float part_dot(const float (&m)[4 * N], const f32x4 (
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const f32x4 v = x[i];
-    p[i] = (m[4 * i] * v.x + m[4 * i + 1] * v.y) + (m[4 * i + 2] * v.z + m[4 * i + 3] * v.w);
+    // fused multiply-adds (the library builds with contraction off)
+    p[i] = fmaf(m[4 * i + 3], v.w, fmaf(m[4 * i + 2], v.z, fmaf(m[4 * i + 1], v.y, m[4 * i] * v.x)));
   }
 #pragma unroll
   for (int w = 1; w < N; w *= 2)
@@ -298,15 +300,15 @@ __global__ __launch_bounds__(kBlock) void gdn_step128_kernel(GdnStepArgs a) {
       const float eg = lds.eg[t], kq = lds.kq[t], beta = lds.gb[1][t], v = lds.v[t][rl];
       const float dk = row_sum<L>(part_dot<S::kVec>(m, kc));
       const float dq = row_sum<L>(part_dot<S::kVec>(m, qc));
-      const float delta = (v - eg * dk) * beta;
+      const float delta = fmaf(-eg, dk, v) * beta;
 #pragma unroll
       for (int i = 0; i < S::kVec; ++i) {
-        m[4 * i] = eg * m[4 * i] + kc[i].x * delta;
-        m[4 * i + 1] = eg * m[4 * i + 1] + kc[i].y * delta;
-        m[4 * i + 2] = eg * m[4 * i + 2] + kc[i].z * delta;
-        m[4 * i + 3] = eg * m[4 * i + 3] + kc[i].w * delta;
+        m[4 * i] = fmaf(kc[i].x, delta, eg * m[4 * i]);
+        m[4 * i + 1] = fmaf(kc[i].y, delta, eg * m[4 * i + 1]);
+        m[4 * i + 2] = fmaf(kc[i].z, delta, eg * m[4 * i + 2]);
+        m[4 * i + 3] = fmaf(kc[i].w, delta, eg * m[4 * i + 3]);
       }
-      const float out = (eg * dq + delta * kq) * a.scale;
+      const float out = fmaf(eg, dq, delta * kq) * a.scale;
       if (sub == 0) attn[static_cast<size_t>(t) * a.h_v * kFast] = out;
     };
     // two tokens per pass: the state stays in the same registers
