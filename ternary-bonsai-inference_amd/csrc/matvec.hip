@@ -1267,6 +1267,8 @@ int pq2_gemm_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, siz
   GprepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float2 *>(scratch + fac_off),
                static_cast<int>(ne0), static_cast<int>(n_tok), nblk, n_groups};
   const size_t items = n_tok * nblk * 8;
+  if (items > static_cast<size_t>(INT32_MAX) - kMmThreads)  // the prepare kernel indexes items in int
+    return fail(BH_ERR_SHAPE, "pq2_matmul_n: n_tok * ne0 too large for one call");
   BH_LAUNCH(pq2_gemm_i8_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
             kMmThreads, 0, st, pa);
   GemmI8Args a{w, pa.afrag, pa.bfac, y, bh_pq2_row_bytes(ne0), static_cast<int>(n_rows), nblk,
@@ -1323,6 +1325,8 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   PrepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float *>(scratch + binv_off),
               static_cast<int>(ne0), static_cast<int>(n_tok), static_cast<int>(nblk), n_ksteps};
   const size_t items = n_tok * nblk * 16;
+  if (items > static_cast<size_t>(INT32_MAX) - kMmThreads)  // the prepare kernel indexes items in int
+    return fail(BH_ERR_SHAPE, "pq2_matmul_n: n_tok * ne0 too large for one call");
   BH_LAUNCH(pq2_mm_prep_kernel, static_cast<unsigned>((items + kMmThreads - 1) / kMmThreads),
             kMmThreads, 0, st, pa);
 
