@@ -55,6 +55,7 @@ def _run(bh, dev, q, pos0, kc, vc, n_kv):
 @pytest.mark.parametrize("n_q,pos0,f16", [
     (1, 0, False), (1, 6, False), (1, 63, False), (1, 64, False), (1, 999, False),
     (1, 4095, False), (1, 4095, True), (1, 130, True),
+    (1, 9000, False), (1, 20000, True),   # one query, chunks of several tiles (ragged last chunk)
     (3, 100, False),     # a few tokens at once (speculative verification)
     (17, 0, False),      # a causal batch from the first position
     (64, 2000, True),
@@ -80,6 +81,7 @@ def test_attention_model_heads(bh, oracle, synth, dev, n_q, pos0, f16):
     (6, 2, 64, 3, 40),     # other head size: generic path
     (5, 1, 80, 2, 9),      # grouping 5, hd 80: generic path
     (12, 4, 256, 1, 33),   # grouping 3
+    (8, 2, 256, 1, 40000), # one query, long context: 3-tile chunks
 ])
 def test_attention_other_shapes(bh, oracle, synth, dev, n_head, n_kv, hd, n_q, pos0):
     _say("attention shape", n_head, n_kv, hd, n_q, pos0)
