@@ -1208,9 +1208,12 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
     const size_t wg_lds = a_bytes + 8 * kStageWaveBytes;
     const size_t per_cu = std::min<size_t>(4, (160 * 1024) / wg_lds);
     const size_t slots = per_cu * static_cast<size_t>(cu_count());
+    // (a wave count past the chunk count still pays when it shortens the
+    // longest chain: 5 chunks over 8 waves are one round trip, over 4 two)
     for (int k = 8; k >= 1; k >>= 1) {
       const size_t wgs = (tiles + (8 / k) - 1) / (8 / k);
-      if (k <= n_chunks && per_cu > 0 && wgs <= slots) {
+      const bool shorter = k == 1 || (n_chunks + k - 1) / k < (n_chunks + k / 2 - 1) / (k / 2);
+      if (shorter && per_cu > 0 && wgs <= slots) {
         ks = k;
         break;
       }
