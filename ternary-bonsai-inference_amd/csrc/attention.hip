@@ -127,6 +127,7 @@ struct DecodeArgs {
   size_t pos0, kv_stride, chunk;
   int n_head, n_chunks;
   float scale;
+  int tile;  // positions per tile: 64, or 32 when 64-position tiles leave the chip short of blocks
 };
 
 template <int L>
@@ -149,10 +150,12 @@ struct FMaxOp {
 __device__ __forceinline__ float wave_max(float x) { return lane_group_reduce<64>(x, FMaxOp{}); }
 __device__ __forceinline__ float wave_sum(float x) { return lane_group_sum<64>(x); }
 
-template <int REP, class T>
+template <int REP, class T, int TILE>
 __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
+  static_assert(TILE == 32 || TILE == 64, "tiles of 32 or 64 positions");
+  constexpr int kPasses = TILE / 16;
   constexpr int kSlots = (REP + 3) / 4;  // heads owned per wave for the softmax state
-  __shared__ float s_e[kTile][REP];       // scores, then exponentials
+  __shared__ float s_e[TILE][REP];       // scores, then exponentials
   __shared__ float s_corr[REP];
   __shared__ float s_acc[4][REP][kHd];
   __shared__ f32x4 s_q[REP * kHd / 4];
@@ -195,11 +198,11 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
     for (int x = 0; x < 4; ++x) acc[r][x] = 0.0f;
   const size_t head_off = static_cast<size_t>(g) * kHd;
 
-  for (size_t t0 = beg; t0 < end; t0 += kTile) {
+  for (size_t t0 = beg; t0 < end; t0 += TILE) {
     // scores: 16 lanes per position, 4 passes of 16 positions
-    f32x4 kr[4][kQkPer / 4];
+    f32x4 kr[kPasses][kQkPer / 4];
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
+    for (int pass = 0; pass < kPasses; ++pass) {
       const size_t p = t0 + pass * 16 + grp;
       const size_t e0 = (p < end ? p : end - 1) * a.kv_stride + head_off + kQkPer * sub;
 #pragma unroll
@@ -212,7 +215,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int x = 0; x < kQkPer / 4; ++x) qv[x] = s_q[(r * kHd + kQkPer * sub) / 4 + x];
 #pragma unroll
-      for (int pass = 0; pass < 4; ++pass) {
+      for (int pass = 0; pass < kPasses; ++pass) {
         const size_t p = t0 + pass * 16 + grp;
         // fused multiply-adds, two chains of 8 dims (the library builds
         // with contraction off, so a * b + c would cost two instructions)
@@ -236,10 +239,10 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
     }
     // the wave's V rows of the tile: issued now (the K registers are free) so
     // their latency overlaps the softmax step and its barriers
-    const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kTile) ? end - t0 : kTile);
-    f32x4 vr[kTile / 4];
+    const int nt = static_cast<int>(end - t0 < static_cast<size_t>(TILE) ? end - t0 : TILE);
+    f32x4 vr[TILE / 4];
 #pragma unroll
-    for (int jj = 0; jj < kTile / 4; ++jj) {
+    for (int jj = 0; jj < TILE / 4; ++jj) {
       const int j = w + 4 * jj;
       vr[jj] = Kv<T>::load4(vc, (t0 + (j < nt ? j : nt - 1)) * a.kv_stride + head_off + 4 * lane);
     }
@@ -249,12 +252,12 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
     for (int u = 0; u < kSlots; ++u) {
       const int r = w + 4 * u;
       if (r < REP) {
-        const float s = s_e[lane][r];
+        const float s = lane < TILE ? s_e[lane][r] : -INFINITY;
         const float m_new = fmaxf(run_m[u], wave_max(s));
         const bool none = m_new == -INFINITY;
         const float corr = none ? 1.0f : expf(run_m[u] - m_new);
         const float e = none ? 0.0f : expf(s - m_new);
-        s_e[lane][r] = e;
+        if (lane < TILE) s_e[lane][r] = e;
         run_l[u] = run_l[u] * corr + wave_sum(e);
         run_m[u] = m_new;
         if (lane == 0) s_corr[r] = corr;
@@ -269,7 +272,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
       for (int x = 0; x < 4; ++x) acc[r][x] *= cr;
     }
 #pragma unroll
-    for (int jj = 0; jj < kTile / 4; ++jj) {
+    for (int jj = 0; jj < TILE / 4; ++jj) {
       const int j = w + 4 * jj;
       if (j < nt) {
         const f32x4 v = vr[jj];
@@ -445,7 +448,10 @@ __global__ __launch_bounds__(kBlock) void attn_pv_kernel(GenericArgs a) {
 
 template <int REP, class T>
 int launch_decode(const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
-  BH_LAUNCH((attn_decode_kernel<REP, T>), dim3(a.n_chunks, n_kv, n_q), kBlock, 0, st, a);
+  if (a.tile == 32)
+    BH_LAUNCH((attn_decode_kernel<REP, T, 32>), dim3(a.n_chunks, n_kv, n_q), kBlock, 0, st, a);
+  else
+    BH_LAUNCH((attn_decode_kernel<REP, T, 64>), dim3(a.n_chunks, n_kv, n_q), kBlock, 0, st, a);
   return ok();
 }
 
@@ -527,11 +533,13 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
     // 39, 512 58 / 40, 256 68 / 57 -- longer chunks amortize the block's q
     // stage and partial writes and shrink the combine; 64 queries at ctx
     // 4096: 2048 blocks 176 us, 1024 197, 4096 180.
-    const size_t tiles = (n_max + kTile - 1) / kTile;
     const size_t blocks = n_q == 1 ? 512 : 2048;
+    // one query over a short context: 32-position tiles, twice the blocks
+    const int tile = n_q == 1 && (n_max + kTile - 1) / kTile * n_kv < blocks ? 32 : kTile;
+    const size_t tiles = (n_max + tile - 1) / tile;
     const size_t want = (blocks + n_kv * n_q - 1) / (n_kv * n_q);
     const size_t per = (tiles + want - 1) / want;
-    const size_t chunk = per * kTile;
+    const size_t chunk = per * tile;
     const size_t n_chunks = (n_max + chunk - 1) / chunk;
     if (n_chunks > 65535) return fail(BH_ERR_SHAPE, "attention: too many positions");
     const size_t rows = n_q * n_head * n_chunks;
@@ -548,7 +556,8 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
                  chunk,
                  static_cast<int>(n_head),
                  static_cast<int>(n_chunks),
-                 scale};
+                 scale,
+                 tile};
     const int e = f16 ? decode_dispatch<uint16_t>(static_cast<int>(rep), a, static_cast<int>(n_kv),
                                                   static_cast<int>(n_q), st)
                       : decode_dispatch<float>(static_cast<int>(rep), a, static_cast<int>(n_kv),
