@@ -216,10 +216,16 @@ constexpr int kConvTok = 4;
 
 template <int G>
 __global__ __launch_bounds__(kBlock) void gdn_prep_conv_kernel(GdnParams a, int bc, int bg,
-                                                               size_t n_tok) {
+                                                               size_t n_tok, int gpx) {
   const int per_grp = bc + kConvTok * bg;
-  const size_t grp = blockIdx.x / per_grp;
-  const int part = blockIdx.x % per_grp;
+  // XCD-aware order: workgroups are dealt to the 8 XCDs in turn, so XCD
+  // b % 8 takes groups [x gpx, (x + 1) gpx) in token order, and a conv
+  // block's three window rows (the previous group's last inputs, read by
+  // the same part of that group just before) are still in that XCD's L2
+  const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+  const size_t grp = static_cast<size_t>(xcd) * gpx + slot / per_grp;
+  const int part = slot % per_grp;
+  if (grp * kConvTok >= n_tok) return;
   const int tid = threadIdx.x;
   const size_t t0 = grp * kConvTok;
   const int nt = n_tok - t0 < static_cast<size_t>(kConvTok) ? static_cast<int>(n_tok - t0) : kConvTok;
@@ -357,10 +363,11 @@ template <int G>
 int launch_fused(const GdnParams &p, bool conv, size_t n_tok, int bc, int bg, hipStream_t st) {
   if (conv) {
     const size_t groups = (n_tok + kConvTok - 1) / kConvTok;
-    const size_t blocks = groups * static_cast<size_t>(bc + kConvTok * bg);
+    const size_t gpx = (groups + 7) / 8;  // token groups per XCD
+    const size_t blocks = 8 * gpx * static_cast<size_t>(bc + kConvTok * bg);
     if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: too many blocks");
     BH_LAUNCH(gdn_prep_conv_kernel<G>, static_cast<unsigned>(blocks), kBlock, 0, st, p, bc, bg,
-              n_tok);
+              n_tok, static_cast<int>(gpx));
   } else {
     const size_t blocks = n_tok * static_cast<size_t>(bc + bg);
     if (blocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "gdn_prep_fused: too many blocks");
