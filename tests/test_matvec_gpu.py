@@ -105,6 +105,7 @@ def test_matmul_token_counts(bh, oracle, synth, dev, n_tok):
     (5120, 700, 37),      # several chunks, a partial token-group set and row tile
     (2048, 129, 260),     # 65 token groups: a second launch row of sets, one live group
     (17408, 48, 9),       # ffn_down's width, 136 blocks, three groups
+    (1024, 5, 5),         # fewer rows than one tile, a group and one token
 ])
 def test_matmul_prefill_shapes(bh, oracle, synth, dev, ne0, n_rows, n_tok):
     """The integer product for more than 4 tokens: x fragments prepared once
