@@ -503,6 +503,8 @@ def main() -> int:
                 ("rms_norm_rows T=512", rows_wl[512]),
                 ("rms_norm_rows T=2048", rows_wl[2048]),
                 ("rms_norm_rows T=8192", rows_wl[8192]),
+                ("qk_norm_rope T=4096", lambda: wl_qk_norm_rope(bh, synth, dev, stream, 4096)),
+                ("qk_norm_rope T=8192", lambda: wl_qk_norm_rope(bh, synth, dev, stream, 8192)),
                 ("gdn_prep_fused T=4096", lambda: wl_gdn_prep(bh, synth, dev, stream)),
                 ("gdn_prep_fused + conv1d T=4096",
                  lambda: wl_gdn_prep(bh, synth, dev, stream, with_conv=True)),
