@@ -637,3 +637,140 @@ def test_attention_skips_zero_probabilities(oracle, synth):
     vc[0] = np.inf
     out = oracle.attention(q, 1, kc, vc, 1)
     assert np.array_equal(out[0, 0], vc[1])
+
+
+# --- composite functions: built from the pinned pieces above ------------------
+# or_qk_norm_rope restates the attention pre-block of full_attention_layer
+# (src/forward.rs:237-270, gate at :379): per token, split each q head's
+# [q(hd) | gate(hd)], rms_norm_rows on the q heads and on the k heads with the
+# shared hd-long weights, rope_imrope per head at that token's (t, h, w, e),
+# sigmoid of the gate.  The composition below calls only the separately
+# pinned oracle.rms_norm_rows / rope_imrope / sigmoid, in the reference's
+# order, and must agree bit for bit; a float64 brute force bounds it too.
+def _qk_case(n_tok, n_q, n_k, hd, stride, seed, mixed):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((n_tok, n_q, stride)).astype(np.float32)
+    k = rng.standard_normal((n_tok, n_k, hd)).astype(np.float32)
+    wq = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    wk = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    if mixed:
+        pos = rng.integers(0, 5000, (n_tok, 4)).astype(np.int32)
+    else:
+        pos = np.repeat(np.arange(n_tok, dtype=np.int32)[:, None], 4, 1)
+    return q, k, wq, wk, pos
+
+
+def _qk_composed(oracle, q, k, wq, wk, pos, hd, n_dims, sections, base, eps, want_gate):
+    n_tok, n_q, _ = q.shape
+    n_k = 0 if k is None else k.shape[1]
+    q_out = np.empty((n_tok, n_q, hd), np.float32)
+    k_out = np.empty((n_tok, n_k, hd), np.float32) if n_k else None
+    gate = np.empty((n_tok, n_q, hd), np.float32) if want_gate else None
+    for t in range(n_tok):
+        qs = np.ascontiguousarray(q[t, :, :hd]).reshape(-1)          # forward.rs:237-241
+        qn = oracle.rms_norm_rows(qs, wq, hd, eps).reshape(n_q, hd)  # forward.rs:242-243
+        for h in range(n_q):                                          # forward.rs:247-258
+            q_out[t, h] = oracle.rope_imrope(qn[h], *map(int, pos[t]), n_dims, sections, base)
+        if n_k:
+            kn = oracle.rms_norm_rows(k[t].reshape(-1), wk, hd, eps).reshape(n_k, hd)
+            for h in range(n_k):                                      # forward.rs:259-270
+                k_out[t, h] = oracle.rope_imrope(kn[h], *map(int, pos[t]), n_dims, sections,
+                                                 base)
+        if want_gate:                                                 # forward.rs:379
+            for h in range(n_q):
+                gate[t, h] = [oracle.sigmoid(float(v)) for v in q[t, h, hd:2 * hd]]
+    return q_out, k_out, gate
+
+
+QK_CASES = [
+    # n_tok, n_q, n_k, hd, stride, gate, mixed positions, n_dims, sections
+    (5, 3, 2, 256, 256, False, False, 64, SECTIONS),
+    (4, 3, 1, 256, 512, True, True, 64, SECTIONS),
+    (3, 2, 0, 256, 512, True, True, 64, SECTIONS),
+    (6, 2, 2, 32, 64, True, True, 16, (1, 2, 3, 2)),
+]
+
+
+@pytest.mark.parametrize("case", QK_CASES)
+def test_qk_norm_rope_is_composition_of_pinned_pieces(oracle, case):
+    n_tok, n_q, n_k, hd, stride, gate, mixed, n_dims, sec = case
+    q, k, wq, wk, pos = _qk_case(n_tok, n_q, max(n_k, 1), hd, stride, 11 + n_tok, mixed)
+    k = k[:, :n_k] if n_k else None
+    got = oracle.qk_norm_rope(q, k, wq, wk if n_k else None, pos, n_q, n_k, hd, n_dims, sec,
+                              1e7, 1e-6, q_head_stride=stride, want_gate=gate)
+    ref = _qk_composed(oracle, q, k, wq, wk, pos, hd, n_dims, sec, 1e7, np.float32(1e-6), gate)
+    assert np.array_equal(got[0].view(np.uint32), ref[0].view(np.uint32))
+    if n_k:
+        assert np.array_equal(got[1].view(np.uint32), ref[1].view(np.uint32))
+    else:
+        assert got[1] is None
+    if gate:
+        assert np.array_equal(got[2].view(np.uint32), ref[2].view(np.uint32))
+
+
+def _sector_bands(n_dims, sections):
+    """Band of pair j from src/rope.rs:37-49, derived by hand: sector =
+    j % sum(sections); t for sector % 3 == 0 below 3*s0, h for % 3 == 1 below
+    3*s1, w for % 3 == 2 below 3*s2, e otherwise."""
+    tot = sum(sections)
+    out = []
+    for j in range(n_dims // 2):
+        sec = j % tot
+        if sec % 3 == 0 and sec < 3 * sections[0]:
+            out.append(0)
+        elif sec % 3 == 1 and sec < 3 * sections[1]:
+            out.append(1)
+        elif sec % 3 == 2 and sec < 3 * sections[2]:
+            out.append(2)
+        else:
+            out.append(3)
+    return out
+
+
+def test_qk_norm_rope_matches_float64_brute_force(oracle):
+    """Independent of every oracle piece: RMSNorm and the rotation in float64
+    with the reference's f32 theta chain, the gate as a float64 logistic; a
+    swapped q/gate half, a dropped weight or an unrotated k head fails."""
+    n_tok, n_q, n_k, hd, stride = 4, 3, 2, 256, 512
+    q, k, wq, wk, pos = _qk_case(n_tok, n_q, n_k, hd, stride, 99, True)
+    qo, ko, g = oracle.qk_norm_rope(q, k, wq, wk, pos, n_q, n_k, hd, 64, SECTIONS, 1e7, 1e-6,
+                                    q_head_stride=stride, want_gate=True)
+    bands = _sector_bands(64, SECTIONS)
+    assert bands == [(j % 3 if not (j % 3 == 2 and j >= 30) else 3) for j in range(32)]
+
+    def ref_head(x, w, p):
+        x = x.astype(np.float64)
+        y = x / np.sqrt(np.mean(x * x) + 1e-6) * w.astype(np.float64)
+        r = _rope_double(y.astype(np.float32), p, 64, bands, 1e7, chain=True)
+        return np.concatenate([r[:64], y[64:]])
+
+    for t in range(n_tok):
+        p = tuple(int(v) for v in pos[t])
+        for h in range(n_q):
+            assert rel_err(qo[t, h], ref_head(q[t, h, :hd], wq, p)) < 2e-6, (t, h)
+            gref = 1.0 / (1.0 + np.exp(-q[t, h, hd:].astype(np.float64)))
+            assert np.max(np.abs(g[t, h] - gref)) < 2e-7, (t, h)
+        for h in range(n_k):
+            assert rel_err(ko[t, h], ref_head(k[t, h], wk, p)) < 2e-6, (t, h)
+
+
+def test_add_rms_norm_rows_is_add_then_pinned_norm(oracle):
+    """or_add_rms_norm_rows restates src/forward.rs:708-713 (cur += attn_out,
+    then rms_norm(cur, post_w)) per row: the sum must be numpy's f32 add bit
+    for bit and the norm the pinned oracle.rms_norm_rows of that sum."""
+    rng = np.random.default_rng(21)
+    for rows, n in [(1, 5120), (7, 256), (3, 130)]:
+        x = rng.standard_normal((rows, n)).astype(np.float32)
+        r = (3 * rng.standard_normal((rows, n))).astype(np.float32)
+        w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+        s, out = oracle.add_rms_norm_rows(x, r, w, n, 1e-6)
+        s_ref = x + r
+        assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+        ref = oracle.rms_norm_rows(s_ref, w, n, 1e-6)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+        s64 = s_ref.astype(np.float64)
+        ref64 = s64 / np.sqrt(np.mean(s64 * s64, axis=1, keepdims=True) + 1e-6) * w
+        assert rel_err(out, ref64) < 2e-6
+    with pytest.raises(oracle.OracleShapeError):
+        oracle.add_rms_norm_rows(np.zeros(10, np.float32), np.zeros(10, np.float32),
+                                 np.ones(4, np.float32), 4, 1e-6)
