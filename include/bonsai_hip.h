@@ -32,6 +32,13 @@
  * PQ2_0 products (bh_pq2_matvec_range, bh_pq2_matmul_n) with more than 4
  * tokens or on shapes outside the integer path, which use per-device
  * scratch buffers: each must not run concurrently with itself on one device.
+ *
+ * Scratch and HIP graphs: a scratch buffer grows (allocates) the first time
+ * a call needs more than it holds.  The buffer it replaces is kept until the
+ * process ends, so a graph captured earlier still replays on valid memory.
+ * Growth is refused while the stream is capturing (BH_ERR_HIP, with a
+ * message): run a scratch-using call once outside capture at its largest
+ * shape before capturing it.  The other entry points allocate nothing.
  */
 #ifndef BONSAI_HIP_H
 #define BONSAI_HIP_H

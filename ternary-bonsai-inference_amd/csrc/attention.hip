@@ -547,7 +547,10 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
     const size_t n_chunks = (n_max + chunk - 1) / chunk;
     if (n_chunks > 65535) return fail(BH_ERR_SHAPE, "attention: too many positions");
     const size_t rows = n_q * n_head * n_chunks;
-    float *scratch = static_cast<float *>(device_scratch(rows * (kHd + 2) * 4, kScratchAttention));
+    size_t sbytes;
+    if (!mul_size(rows, kHd + 2, 4, &sbytes))
+      return fail(BH_ERR_SHAPE, "attention: scratch size overflows");
+    float *scratch = static_cast<float *>(device_scratch(sbytes, kScratchAttention, st));
     if (scratch == nullptr) return BH_ERR_HIP;
     DecodeArgs a{q,
                  k_cache,
@@ -576,7 +579,10 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
                 static_cast<int>(n_chunks), kHd, out);
     return ok();
   }
-  float *probs = static_cast<float *>(device_scratch(n_q * n_head * n_max * 4, kScratchAttention));
+  size_t pbytes;
+  if (!mul_size(n_q, n_head, n_max, &pbytes) || !mul_size(pbytes, 4, &pbytes))
+    return fail(BH_ERR_SHAPE, "attention: probability scratch size overflows");
+  float *probs = static_cast<float *>(device_scratch(pbytes, kScratchAttention, st));
   if (probs == nullptr) return BH_ERR_HIP;
   GenericArgs a{q, k_cache, v_cache, probs, out, pos0, n_max, kv_stride, hd,
                 static_cast<int>(n_head), static_cast<int>(rep), scale};

@@ -43,15 +43,27 @@ inline int pow2ceil(size_t v) {
   return p;
 }
 
-// Per-device scratch owned by the library (grown on demand, never shrunk),
-// one buffer per client so different entry points never share one.  Calls
-// of the same client on one device must not overlap in time.  Returns
-// nullptr on allocation failure (the status is already recorded).
+// Per-device scratch owned by the library, one buffer per client so
+// different entry points never share one.  Calls of the same client on one
+// device must not overlap in time.  A buffer grows on demand (at least
+// twofold) and the buffer it replaces is kept until the process ends, so a
+// graph captured earlier keeps valid addresses.  Growth while `stream` is
+// capturing is refused (it would allocate inside the capture).  Returns
+// nullptr with the status recorded on failure.
 constexpr int kScratchSoftmax = 0;  // split-row softmax partials
 constexpr int kScratchMatmul = 1;   // PQ2_0 product: f16 x fragments, token scales
 constexpr int kScratchAttention = 2;  // attention: chunk partials or probabilities
 constexpr int kScratchSlots = 3;
-void *device_scratch(size_t bytes, int slot);
+void *device_scratch(size_t bytes, int slot, hipStream_t stream);
+// Current size of this device's buffer for `slot` (0 before the first use).
+size_t scratch_bytes(int slot);
+
+// a * b (* c), or false when the product does not fit in size_t.
+inline bool mul_size(size_t a, size_t b, size_t *out) { return !__builtin_mul_overflow(a, b, out); }
+inline bool mul_size(size_t a, size_t b, size_t c, size_t *out) {
+  size_t t;
+  return mul_size(a, b, &t) && mul_size(t, c, out);
+}
 
 
 // ---------------------------------------------------------------------------

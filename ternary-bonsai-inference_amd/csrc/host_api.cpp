@@ -208,13 +208,29 @@ extern "C" int bh_host_decode_pq2_0_row(const uint8_t *raw, size_t raw_len, size
   return ok();
 }
 
+namespace {
+// (base_row + n_rows) * rb, or false when it does not fit in size_t.
+bool rows_end_bytes(uint64_t base_row, size_t n_rows, size_t rb, size_t *out) {
+  const unsigned __int128 v = (static_cast<unsigned __int128>(base_row) + n_rows) * rb;
+  if (v > static_cast<unsigned __int128>(SIZE_MAX)) return false;
+  *out = static_cast<size_t>(v);
+  return true;
+}
+}  // namespace
+
 extern "C" int bh_host_batch_embed(const uint8_t *payload, size_t payload_len, size_t ne0,
                                    size_t n_rows, const uint32_t *tokens, size_t n_tok,
                                    float *out) {
   const size_t rb = bh_pq2_row_bytes(ne0);
-  if (payload_len < rb * n_rows)
+  size_t tab_bytes = 0;
+  if (!rows_end_bytes(0, n_rows, rb, &tab_bytes))
+    return fail(BH_ERR_SHAPE, "batch_embed: n_rows * row bytes overflows");
+  if (payload_len < tab_bytes)
     return fail(BH_ERR_SHAPE, "batch_embed: payload len " + std::to_string(payload_len) +
-                                  " < n_rows * row bytes " + std::to_string(rb * n_rows));
+                                  " < n_rows * row bytes " + std::to_string(tab_bytes));
+  size_t out_bytes = 0;
+  if (!mul_size(n_tok, ne0, 4, &out_bytes))
+    return fail(BH_ERR_SHAPE, "batch_embed: output size overflows");
   // Weights::row_f32 range check (src/weights.rs:337-341), first bad token wins
   for (size_t k = 0; k < n_tok; ++k) {
     if (tokens[k] >= n_rows)
@@ -226,13 +242,13 @@ extern "C" int bh_host_batch_embed(const uint8_t *payload, size_t payload_len, s
   Stream s;
   if (s.status()) return s.status();
   DevBuf dtab, dids, dout;
-  if (int e = upload(dtab, payload, rb * n_rows, s.get())) return e;
+  if (int e = upload(dtab, payload, tab_bytes, s.get())) return e;
   if (int e = upload(dids, tokens, n_tok * 4, s.get())) return e;
-  if (int e = dout.alloc(n_tok * ne0 * 4)) return e;
+  if (int e = dout.alloc(out_bytes)) return e;
   if (int e = bh_pq2_embed_gather(dtab.as<uint8_t>(), ne0, n_rows, dids.as<uint32_t>(), n_tok,
                                   dout.as<float>(), nullptr, s.handle()))
     return e;
-  if (int e = download(out, dout, n_tok * ne0 * 4, s.get())) return e;
+  if (int e = download(out, dout, out_bytes, s.get())) return e;
   return ok();
 }
 
@@ -255,12 +271,6 @@ int host_matmul_rows(const uint8_t *payload, size_t ne0, uint64_t base_row, size
   return download(y, dy, n_tok * n_rows * 4, s.get());
 }
 
-bool rows_end_bytes(uint64_t base_row, size_t n_rows, size_t rb, size_t *out) {
-  const unsigned __int128 v = (static_cast<unsigned __int128>(base_row) + n_rows) * rb;
-  if (v > static_cast<unsigned __int128>(SIZE_MAX)) return false;
-  *out = static_cast<size_t>(v);
-  return true;
-}
 }  // namespace
 
 extern "C" int bh_host_dot_pq2_0_row(const uint8_t *payload, size_t payload_len, size_t ne0,
@@ -270,7 +280,12 @@ extern "C" int bh_host_dot_pq2_0_row(const uint8_t *payload, size_t payload_len,
     return fail(BH_ERR_SHAPE, "dot_pq2_0_row: x length " + std::to_string(x_len) + " != ne0 " +
                                   std::to_string(ne0));
   const size_t rb = bh_pq2_row_bytes(ne0);
-  const size_t start = static_cast<size_t>(row) * rb, end = start + rb;
+  size_t end = 0;
+  if (!rows_end_bytes(row, 1, rb, &end))
+    return fail(BH_ERR_SHAPE, "dot_pq2_0_row: row " + std::to_string(row) +
+                                  " byte range overflows, payload is " +
+                                  std::to_string(payload_len));
+  const size_t start = end - rb;
   if (end > payload_len)
     return fail(BH_ERR_SHAPE, "dot_pq2_0_row: row " + std::to_string(row) + " needs bytes " +
                                   std::to_string(start) + ".." + std::to_string(end) +

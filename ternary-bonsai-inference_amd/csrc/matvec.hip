@@ -1265,7 +1265,7 @@ int pq2_gemm_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, siz
   const size_t frag_bytes = static_cast<size_t>(nblk) * 2 * n_groups * 64 * sizeof(uint4);
   const size_t fac_off = (frag_bytes + 255) / 256 * 256;
   const size_t fac_bytes = static_cast<size_t>(nblk) * n_groups * kI8Tok * sizeof(float2);
-  char *scratch = static_cast<char *>(device_scratch(fac_off + fac_bytes, kScratchMatmul));
+  char *scratch = static_cast<char *>(device_scratch(fac_off + fac_bytes, kScratchMatmul, st));
   if (scratch == nullptr) return BH_ERR_HIP;
   GprepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float2 *>(scratch + fac_off),
                static_cast<int>(ne0), static_cast<int>(n_tok), nblk, n_groups};
@@ -1323,7 +1323,7 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   const size_t frag_bytes = static_cast<size_t>(tiles_padded) * n_ksteps * 2 * 64 * sizeof(uint4);
   const size_t binv_off = (frag_bytes + 255) / 256 * 256;
   const size_t binv_bytes = static_cast<size_t>(tiles_padded) * nblk * 8 * sizeof(float4);
-  char *scratch = static_cast<char *>(device_scratch(binv_off + binv_bytes, kScratchMatmul));
+  char *scratch = static_cast<char *>(device_scratch(binv_off + binv_bytes, kScratchMatmul, st));
   if (scratch == nullptr) return BH_ERR_HIP;
   PrepArgs pa{x, reinterpret_cast<uint4 *>(scratch), reinterpret_cast<float *>(scratch + binv_off),
               static_cast<int>(ne0), static_cast<int>(n_tok), static_cast<int>(nblk), n_ksteps};

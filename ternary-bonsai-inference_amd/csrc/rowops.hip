@@ -639,7 +639,7 @@ int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float
   const size_t nparts = rows * nch;
   // scratch: f64 partial sums, then f32 partial maxima
   const size_t off_m = nparts * sizeof(double);
-  char *scratch = static_cast<char *>(device_scratch(off_m + nparts * sizeof(float), kScratchSoftmax));
+  char *scratch = static_cast<char *>(device_scratch(off_m + nparts * sizeof(float), kScratchSoftmax, st));
   if (scratch == nullptr) return BH_ERR_HIP;
   SplitScratch sc;
   sc.part_s = reinterpret_cast<double *>(scratch);

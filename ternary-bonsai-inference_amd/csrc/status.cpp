@@ -5,6 +5,7 @@
 // thread-local string readable through bh_last_error().
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -22,6 +23,11 @@ struct Scratch {
 };
 std::mutex g_scratch_mu;
 std::vector<Scratch> g_scratch;  // indexed by device ordinal * kScratchSlots + slot
+// Buffers replaced by a larger one.  They are never freed: a HIP graph
+// captured while one was current still holds its address, and replaying that
+// graph must find the memory alive.  Growth is at least twofold, so the
+// retired buffers of a slot add up to less than its current one.
+std::vector<void *> g_retired;
 }  // namespace
 
 int fail(int code, const std::string &msg) {
@@ -43,7 +49,7 @@ int check_launch(const char *what) {
   return check_hip(hipGetLastError(), what);
 }
 
-void *device_scratch(size_t bytes, int slot) {
+void *device_scratch(size_t bytes, int slot, hipStream_t stream) {
   int dev = 0;
   if (check_hip(hipGetDevice(&dev), "hipGetDevice") != BH_OK) return nullptr;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -51,21 +57,36 @@ void *device_scratch(size_t bytes, int slot) {
   if (g_scratch.size() <= idx) g_scratch.resize(idx + 1);
   Scratch &s = g_scratch[idx];
   if (s.bytes >= bytes) return s.ptr;
-  // grow: the old buffer may still be read by queued work, so wait for the
-  // device before releasing it
-  if (s.ptr != nullptr) {
-    if (check_hip(hipDeviceSynchronize(), "scratch grow: hipDeviceSynchronize") != BH_OK)
-      return nullptr;
-    (void)hipFree(s.ptr);
-    s.ptr = nullptr;
-    s.bytes = 0;
+  // Growth allocates.  Under stream capture that would put an allocation
+  // (and the new address) into the graph being recorded, so it is refused:
+  // the caller runs the call once eagerly at its largest shape first.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (check_hip(hipStreamIsCapturing(stream, &cap), "hipStreamIsCapturing") != BH_OK)
+    return nullptr;
+  if (cap != hipStreamCaptureStatusNone) {
+    fail(BH_ERR_HIP, "scratch of " + std::to_string(bytes) + " bytes needed but " +
+                         std::to_string(s.bytes) +
+                         " reserved, and the stream is capturing: run this call once outside "
+                         "capture at its largest shape before capturing it");
+    return nullptr;
   }
   size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  if (s.bytes <= SIZE_MAX / 2 && want < 2 * s.bytes) want = 2 * s.bytes;
   void *p = nullptr;
   if (check_hip(hipMalloc(&p, want), "scratch hipMalloc") != BH_OK) return nullptr;
+  // queued work and captured graphs may still use the old buffer: keep it
+  if (s.ptr != nullptr) g_retired.push_back(s.ptr);
   s.ptr = p;
   s.bytes = want;
   return p;
+}
+
+size_t scratch_bytes(int slot) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  const size_t idx = static_cast<size_t>(dev) * kScratchSlots + slot;
+  return idx < g_scratch.size() ? g_scratch[idx].bytes : 0;
 }
 
 }  // namespace bh

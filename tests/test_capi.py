@@ -253,3 +253,36 @@ def test_attention_argument_errors(bh):
     assert lib.bh_kv_store(None, None, 0, 1024, None, None, 0, 1, None) == 0
     assert lib.bh_kv_store(None, None, 1, 1024, None, None, 0, 1, None) == bh.BH_ERR_ARG
     assert lib.bh_kv_store(None, None, 1, 1024, None, None, 0, 7, None) == bh.BH_ERR_ARG
+
+
+def test_host_byte_ranges_do_not_wrap(bh):
+    """Sizes whose byte products overflow 64 bits are shape errors, not a
+    wrapped length that passes the payload check (the reference's slice
+    indexing would panic instead of reading past the buffer)."""
+    lib = bh.lib()
+    table = np.zeros(34 * 4, np.uint8)
+    toks = np.zeros(1, np.uint32)
+    out = np.empty(128, np.float32)
+    huge = (1 << 64) // 34 + 1  # huge * 34 wraps to a small number
+    st = lib.bh_host_batch_embed(table.ctypes.data, table.size, 128, huge, toks.ctypes.data, 1,
+                                 out.ctypes.data)
+    assert st == bh.BH_ERR_SHAPE and "overflows" in bh.last_error()
+    x = np.zeros(128, np.float32)
+    y = np.zeros(1, np.float32)
+    st = lib.bh_host_dot_pq2_0_row(table.ctypes.data, table.size, 128, huge, x.ctypes.data, 128,
+                                   y.ctypes.data)
+    assert st == bh.BH_ERR_SHAPE and "overflows" in bh.last_error()
+    # an ordinary out-of-payload row keeps the reference's text
+    st = lib.bh_host_dot_pq2_0_row(table.ctypes.data, table.size, 128, 4, x.ctypes.data, 128,
+                                   y.ctypes.data)
+    assert st == bh.BH_ERR_SHAPE
+    assert bh.last_error() == "dot_pq2_0_row: row 4 needs bytes 136..170, payload is 136"
+
+
+def test_attention_scratch_size_does_not_wrap(bh):
+    """n_q * n_head * n_max * 4 above 2^64 is rejected before any allocation
+    (generic path: hd 64 is not the decode path's head size)."""
+    lib = bh.lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: the call fails on the size first
+    st = lib.bh_attention(p, 65535, (1 << 40) - 65535, p, p, 0, 65535, 1, 64, p, None)
+    assert st == bh.BH_ERR_SHAPE and "overflows" in bh.last_error()

@@ -90,3 +90,46 @@ def test_graph_qk_norm_rope(bh, synth, dev):
         return outs
 
     _replay_check(make_out, run, dev)
+
+
+def test_graph_softmax_survives_scratch_growth(bh, oracle, synth, dev):
+    """A graph captured with the wide-row softmax keeps the library scratch
+    address it recorded.  A later eager call needing more scratch (here about
+    1.2 MB of row partials, above the 1 MB first allocation) makes the library
+    switch to a larger buffer; the old one must stay alive, so every replay of
+    the graph still matches the oracle."""
+    import torch
+    from conftest import rel_err
+    xs = synth.Rng(40).normal(4 * 248320, 0.0, 3.0).reshape(4, 248320)
+    ref = oracle.softmax_rows(xs, 248320, 1.25)
+    x = _t(xs, dev)
+    out = torch.empty_like(x)
+    s = torch.cuda.Stream()
+    bh.softmax_rows(x, 248320, 1.25, out=out, stream=s)  # eager: scratch exists before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        bh.softmax_rows(x, 248320, 1.25, out=out, stream=s)
+    first = None
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert rel_err(got, ref) < 2e-5, f"replay {i}"
+        if first is None:
+            first = got
+        assert np.array_equal(got.view(np.uint32), first.view(np.uint32)), f"replay {i} differs"
+        if i == 0:
+            # 100 rows of 2^22: 1024 chunks per row -> 102400 partials x 12 B
+            row = 1 << 22
+            big = torch.randn((100, row), device=dev, generator=torch.Generator(dev).manual_seed(3))
+            bout = bh.softmax_rows(big, row, 1.0, stream=s)
+            torch.cuda.synchronize()
+            for r in (0, 99):
+                assert rel_err(bout[r].cpu().numpy(),
+                               oracle.softmax_rows(big[r].cpu().numpy(), row)) < 2e-5, r
+            del big, bout
+            torch.cuda.synchronize()
