@@ -222,6 +222,18 @@ int bh_gdn_step(const float *q, const float *k, const float *v, const float *gat
 int bh_softmax_rows(const float *x, size_t x_len, size_t row_len,
                     float inv_temp, float *out, bh_stream stream);
 
+/* No counterpart in the reference: bh_softmax_rows for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * bh_softmax_rows, but rows too wide for one workgroup keep their partials
+ * in a fixed 1 MiB per-device array of the library (12 bytes per 4096-element
+ * chunk of a row: up to 87381 chunks, e.g. 1432 rows of 248320) instead of
+ * the growable scratch; larger inputs return BH_ERR_SHAPE.  Nothing is
+ * allocated or freed.  Every call on one device shares that array: calls
+ * that overlap in time on one device race. */
+int bh_softmax_rows_noalloc(const float *x, size_t x_len, size_t row_len,
+                            float inv_temp, float *out, bh_stream stream);
+
 /* ---------------------------------------------------------------------------
  * Rotary embedding (src/rope.rs:9-70)
  * ------------------------------------------------------------------------- */

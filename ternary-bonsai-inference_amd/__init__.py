@@ -102,6 +102,7 @@ _SIGNATURES = {
     "bh_gdn_gate_prep": (_c_int, [_vp, _vp, _vp, _vp, _c_size, _c_size, _vp, _vp, _vp]),
     "bh_gdn_prep_fused": (_c_int, [ctypes.POINTER(GdnPrepArgs), _vp]),
     "bh_softmax_rows": (_c_int, [_vp, _c_size, _c_size, _c_float, _vp, _vp]),
+    "bh_softmax_rows_noalloc": (_c_int, [_vp, _c_size, _c_size, _c_float, _vp, _vp]),
     "bh_rope_imrope": (_c_int, [_vp, _c_size, _c_size, _c_size, _vp, _c_size,
                                 ctypes.POINTER(ctypes.c_int32), _c_float, _vp]),
     "bh_qk_norm_rope": (_c_int, [ctypes.POINTER(QkNormRopeArgs), _vp]),
@@ -239,12 +240,15 @@ def unary(mode: int, a, b=None, out=None, stream=None):
     return out
 
 
-def softmax_rows(x, row_len: int, inv_temp: float = 1.0, out=None, stream=None):
+def softmax_rows(x, row_len: int, inv_temp: float = 1.0, out=None, stream=None,
+                 noalloc: bool = False):
+    """bh_softmax_rows, or with noalloc=True bh_softmax_rows_noalloc (fixed
+    library scratch, no device allocation by the library)."""
     import torch
     _f32(x, "x")
     out = torch.empty_like(x) if out is None else out
-    check(lib().bh_softmax_rows(x.data_ptr(), x.numel(), row_len, inv_temp, out.data_ptr(),
-                                _stream(stream)))
+    fn = lib().bh_softmax_rows_noalloc if noalloc else lib().bh_softmax_rows
+    check(fn(x.data_ptr(), x.numel(), row_len, inv_temp, out.data_ptr(), _stream(stream)))
     return out
 
 

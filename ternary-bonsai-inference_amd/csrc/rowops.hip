@@ -31,6 +31,8 @@
 //     (one float4 per lane) folds a row's partials and writes it.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include <cmath>
 #include <string>
 #include <type_traits>
@@ -622,8 +624,42 @@ int l2_rows_impl(const float *x, float *out, size_t rows, size_t row_len, float 
   return ok();
 }
 
+// Scratch of bh_softmax_rows_noalloc: a fixed device array instead of the
+// library's growable buffer, so that entry point never allocates.  Host code
+// must not pass `scratch` itself to a kernel (in host code the name is a
+// stand-in, not a device address): it uses the address hipGetSymbolAddress
+// returns for the current device, looked up once per device.
+constexpr size_t kNoAllocScratchBytes = size_t{1} << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+char *g_noalloc_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, or nullptr with the status recorded.
+char *noalloc_scratch() {
+  int dev = 0;
+  if (check_hip(hipGetDevice(&dev), "hipGetDevice") != BH_OK) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    fail(BH_ERR_HIP, "softmax_rows_noalloc: device ordinal out of range");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (g_noalloc_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    if (check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                  "softmax_rows_noalloc: hipGetSymbolAddress") != BH_OK)
+      return nullptr;
+    g_noalloc_ptr[dev] = static_cast<char *>(p);
+  }
+  return g_noalloc_ptr[dev];
+}
+
+// Wide-row softmax: stats pass then write pass.  `fixed` (with `fixed_cap`
+// bytes) is the no-allocation entry point's scratch; nullptr takes the
+// library's growable per-device buffer.
 int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float inv_t,
-                  hipStream_t st) {
+                  hipStream_t st, char *fixed, size_t fixed_cap) {
   if (rows > kMaxSplitRows)
     return fail(BH_ERR_SHAPE, "softmax_rows: too many wide rows for one launch");
   const bool vec = (row_len % 4 == 0) && aligned16(x) && aligned16(out);
@@ -639,11 +675,22 @@ int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float
   const size_t nparts = rows * nch;
   // scratch: f64 partial sums, then f32 partial maxima
   const size_t off_m = nparts * sizeof(double);
-  char *scratch = static_cast<char *>(device_scratch(off_m + nparts * sizeof(float), kScratchSoftmax, st));
-  if (scratch == nullptr) return BH_ERR_HIP;
+  const size_t need = off_m + nparts * sizeof(float);
+  char *buf;
+  if (fixed != nullptr) {
+    if (need > fixed_cap)
+      return fail(BH_ERR_SHAPE, "softmax_rows_noalloc: " + std::to_string(rows) + " rows of " +
+                                    std::to_string(row_len) + " need " + std::to_string(need) +
+                                    " scratch bytes, above the fixed " +
+                                    std::to_string(fixed_cap));
+    buf = fixed;
+  } else {
+    buf = static_cast<char *>(device_scratch(need, kScratchSoftmax, st));
+    if (buf == nullptr) return BH_ERR_HIP;
+  }
   SplitScratch sc;
-  sc.part_s = reinterpret_cast<double *>(scratch);
-  sc.part_m = reinterpret_cast<float *>(scratch + off_m);
+  sc.part_s = reinterpret_cast<double *>(buf);
+  sc.part_m = reinterpret_cast<float *>(buf + off_m);
   const float4 *x4 = reinterpret_cast<const float4 *>(x);
   BH_LAUNCH(softmax_split_stats_kernel, dim3(static_cast<unsigned>(nch), static_cast<unsigned>(rows)),
             kBlock, 0, st, x4, r4, inv_t, sc);
@@ -717,15 +764,17 @@ extern "C" int bh_silu_l2_norm_rows(const float *x, size_t x_len, size_t row_len
   return l2_rows_impl<true>(x, out, x_len / row_len, row_len, eps, as_stream(stream));
 }
 
-extern "C" int bh_softmax_rows(const float *x, size_t x_len, size_t row_len, float inv_temp,
-                               float *out, bh_stream stream) {
+namespace bh {
+namespace {
+int softmax_impl(const float *x, size_t x_len, size_t row_len, float inv_temp, float *out,
+                 hipStream_t st, bool noalloc) {
+  const char *name = noalloc ? "softmax_rows_noalloc" : "softmax_rows";
   if (row_len == 0 || x_len % row_len != 0)
-    return fail(BH_ERR_SHAPE, "softmax_rows: x len " + std::to_string(x_len) +
+    return fail(BH_ERR_SHAPE, std::string(name) + ": x len " + std::to_string(x_len) +
                                   " not divisible by row_len " + std::to_string(row_len));
   if (x_len == 0) return ok();
-  if (!x || !out) return fail(BH_ERR_ARG, "softmax_rows: null pointer");
+  if (!x || !out) return fail(BH_ERR_ARG, std::string(name) + ": null pointer");
   const size_t rows = x_len / row_len;
-  hipStream_t st = as_stream(stream);
   RowGeom g;
   const bool fits = pick_geom(row_len, g, 2) && aligned16(x) && aligned16(out);
   const bool few_long_rows = rows < 1024 && row_len >= 16384;
@@ -743,5 +792,22 @@ extern "C" int bh_softmax_rows(const float *x, size_t x_len, size_t row_len, flo
   }
   // The split path reads x again in pass 2; each element is read by the same
   // thread just before it writes it, so out == x (in place) is safe there too.
-  return softmax_split(x, out, rows, row_len, inv_temp, st);
+  char *fixed = nullptr;
+  if (noalloc) {
+    fixed = noalloc_scratch();
+    if (fixed == nullptr) return BH_ERR_HIP;
+  }
+  return softmax_split(x, out, rows, row_len, inv_temp, st, fixed, kNoAllocScratchBytes);
+}
+}  // namespace
+}  // namespace bh
+
+extern "C" int bh_softmax_rows(const float *x, size_t x_len, size_t row_len, float inv_temp,
+                               float *out, bh_stream stream) {
+  return softmax_impl(x, x_len, row_len, inv_temp, out, as_stream(stream), false);
+}
+
+extern "C" int bh_softmax_rows_noalloc(const float *x, size_t x_len, size_t row_len,
+                                       float inv_temp, float *out, bh_stream stream) {
+  return softmax_impl(x, x_len, row_len, inv_temp, out, as_stream(stream), true);
 }
