@@ -105,6 +105,7 @@ def test_graph_softmax_survives_scratch_growth(bh, oracle, synth, dev):
     x = _t(xs, dev)
     out = torch.empty_like(x)
     s = torch.cuda.Stream()
+    torch.cuda.synchronize()  # x and out come from the default stream; the calls run on s
     bh.softmax_rows(x, 248320, 1.25, out=out, stream=s)  # eager: scratch exists before capture
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
