@@ -47,10 +47,6 @@ def _load(name: str, path: Path):
     return mod
 
 
-SPIN_CYCLES = 5_000_000           # minimum pre-timing spin, GPU clock cycles (~2 ms)
-SPIN_CYCLES_PER_STEP = 100_000    # ~40 us of spin per timed launch
-
-
 def n_sets(bytes_per_set: int, max_sets: int = 32) -> int:
     return max(1, min(max_sets, -(-ROTATE_BYTES // max(1, bytes_per_set))))
 
@@ -58,8 +54,13 @@ def n_sets(bytes_per_set: int, max_sets: int = 32) -> int:
 def time_launches(launch, n_rot: int, steps: int, warmup: int, stream) -> float:
     """Average ms per launch.  The W warmup launches run eagerly; the K timed
     launches are captured into one HIP graph (so the Python/ctypes launch
-    cost does not space them out) and replayed once between two HIP events
-    recorded on the launch stream, with synchronisation on both sides."""
+    cost does not space them out).  The graph is replayed once untimed
+    (upload), then replayed again untimed directly before the timed replay,
+    which sits between two HIP events recorded on the launch stream, with
+    synchronisation on both sides.  The untimed replay keeps the GPU busy
+    with the same kernel while the host submits the timed one, so the timed
+    launches neither wait on the host nor start from an idle (clocked-down)
+    memory system."""
     import torch
     for i in range(max(1, warmup)):
         launch(i % n_rot)
@@ -73,11 +74,7 @@ def time_launches(launch, n_rot: int, steps: int, warmup: int, stream) -> float:
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        # hold the stream in a spin (before the start event) long enough for
-        # the host to submit all K launches of the graph: the runtime submits
-        # graph launches at up to ~40 us each, and a kernel that starts late
-        # because the host has not submitted it yet is not kernel time
-        torch.cuda._sleep(max(SPIN_CYCLES, SPIN_CYCLES_PER_STEP * steps))
+        graph.replay()  # untimed: runs while the timed replay is submitted
         e0.record(stream)
         graph.replay()
         e1.record(stream)

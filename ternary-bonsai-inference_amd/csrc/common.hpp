@@ -177,9 +177,16 @@ __device__ __forceinline__ float4 load_stream(const float4 *p) {
   const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
   return make_float4(v.x, v.y, v.z, v.w);
 }
+#ifndef BH_STORE_SC1
+#define BH_STORE_SC1 0
+#endif
 __device__ __forceinline__ void store_stream(float4 *p, float4 v) {
   f32x4 t = {v.x, v.y, v.z, v.w};
+#if BH_STORE_SC1
+  asm volatile("global_store_dwordx4 %0, %1, off sc1 nt" ::"v"(p), "v"(t) : "memory");
+#else
   __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
+#endif
 }
 
 // ---------------------------------------------------------------------------
