@@ -186,19 +186,23 @@ __global__ __launch_bounds__(1024) void rms_rows_kernel(
     v[i] = (L.live && c < r4) ? x4[c] : f4_zero();
   }
   if constexpr (ADD) {
+    // the residual's loads go out with x's, before any use
     const float4 *r4p = reinterpret_cast<const float4 *>(r) + off;
     float4 *s4 = reinterpret_cast<float4 *>(sum_out) + off;
+    float4 rv[VPT];
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
       const int c = L.gl + i * L.stride;
-      if (L.live && c < r4) {
-        const float4 a = r4p[c];
-        v[i].x += a.x;
-        v[i].y += a.y;
-        v[i].z += a.z;
-        v[i].w += a.w;
-        store_stream(s4 + c, v[i]);
-      }
+      rv[i] = (L.live && c < r4) ? r4p[c] : f4_zero();
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int c = L.gl + i * L.stride;
+      v[i].x += rv[i].x;
+      v[i].y += rv[i].y;
+      v[i].z += rv[i].z;
+      v[i].w += rv[i].w;
+      if (L.live && c < r4) store_stream(s4 + c, v[i]);
     }
   }
   float ss = 0.0f;
@@ -338,18 +342,21 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(const float *x, floa
   const float4 *x4 = reinterpret_cast<const float4 *>(x) + off;
   const float ninf = -INFINITY;
 
+  // loads first, all in flight together; scale after
   float4 v[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int c = L.gl + i * L.stride;
+    v[i] = (L.live && c < r4) ? x4[c] : make_float4(ninf, ninf, ninf, ninf);
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = L.gl + i * L.stride;
     if (L.live && c < r4) {
-      v[i] = x4[c];
       v[i].x *= inv_t;
       v[i].y *= inv_t;
       v[i].z *= inv_t;
       v[i].w *= inv_t;
-    } else {
-      v[i] = make_float4(ninf, ninf, ninf, ninf);
     }
   }
   float m = ninf;
@@ -439,11 +446,18 @@ __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float
   const size_t end = (r + 1) * r4;
   const float ninf = -INFINITY;
   float4 v[kSplitVPT];
+  // all loads in flight before the first use (lanes past the row's end
+  // re-read its last float4 and are masked below); a load whose value is
+  // used inside its own branch gets a wait of its own
+#pragma unroll
+  for (int i = 0; i < kSplitVPT; ++i) {
+    const size_t c = base + threadIdx.x + i * kBlock;
+    v[i] = x[c < end ? c : end - 1];
+  }
 #pragma unroll
   for (int i = 0; i < kSplitVPT; ++i) {
     const size_t c = base + threadIdx.x + i * kBlock;
     if (c < end) {
-      v[i] = x[c];
       v[i].x *= inv_t;
       v[i].y *= inv_t;
       v[i].z *= inv_t;
