@@ -372,30 +372,15 @@ def measure(name, wl, steps, warmup, stream, extra=None):
 # CPU baseline: the oracle (C restatement of the reference), 1 thread
 # ---------------------------------------------------------------------------
 
-def cpu_baseline(bh, synth, oracle, seconds: float):
-    """Time oracle.qk_norm_rope (src/forward.rs:237-270 restated) on the same
-    config, repeating the 2048-token batch until `seconds` have passed: once on
-    one thread (the reference's decode thread), then row-parallel over the
-    host's cores for a quarter of that time (an upper bound for a threaded
-    CPU path; the C call releases the GIL, tokens are split into contiguous
-    slices, one per thread)."""
+def _time_cpu(run, n_units: int, seconds: float):
+    """Repeat run(lo, hi) over the whole sample on one thread for `seconds`,
+    then split by units over the host's threads (the C oracle releases the
+    GIL) for a quarter of that: (units/s one thread, units/s threaded,
+    threads, repetitions one thread, repetitions threaded)."""
     import concurrent.futures
-    import numpy as np
-    n_tok, nq, nk, hd = 2048, 24, 4, 256
-    r = synth.Rng(1)
-    q = r.normal(n_tok * nq * hd).reshape(n_tok, nq, hd)
-    k = r.normal(n_tok * nk * hd).reshape(n_tok, nk, hd)
-    wq, wk = r.normal(hd, 1.0, 0.1), r.normal(hd, 1.0, 0.1)
-    pos = synth.positions(n_tok)
-    nbytes = (q.nbytes + k.nbytes) * 2 + 2 * hd * 4
-
-    def run(lo, hi):
-        oracle.qk_norm_rope(q[lo:hi], k[lo:hi], wq, wk, pos[lo:hi], nq, nk, hd, 64, bh.SECTIONS,
-                            1e7, 1e-6)
-
     reps, t0 = 0, time.perf_counter()
     while True:
-        run(0, n_tok)
+        run(0, n_units)
         reps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
@@ -404,8 +389,8 @@ def cpu_baseline(bh, synth, oracle, seconds: float):
         n_thr = len(os.sched_getaffinity(0))
     except AttributeError:
         n_thr = os.cpu_count() or 1
-    n_thr = max(1, min(n_thr, 16))  # the GPU box's CPU share is 16 cores
-    cuts = [n_tok * i // n_thr for i in range(n_thr + 1)]
+    n_thr = max(1, min(n_thr, 16, n_units))  # the GPU box's CPU share is 16 cores
+    cuts = [n_units * i // n_thr for i in range(n_thr + 1)]
     reps_mt, t1 = 0, time.perf_counter()
     with concurrent.futures.ThreadPoolExecutor(n_thr) as pool:
         while True:
@@ -414,27 +399,115 @@ def cpu_baseline(bh, synth, oracle, seconds: float):
             el_mt = time.perf_counter() - t1
             if el_mt >= seconds / 4:
                 break
-    return {"value": round(nbytes * reps / el / 1e9, 4), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"oracle qk_norm_rope on the full config-2 batch (2048 tokens x 28 heads),"
-                      f" {reps} repetitions in {el:.1f} s, 1 thread",
-            "rows_per_s": round(n_tok * reps / el, 1),
-            "upper_bound_mt": {"value": round(nbytes * reps_mt / el_mt / 1e9, 4), "unit": "GB/s",
-                               "cores": n_thr,
-                               "sample": f"same batch split over {n_thr} threads by token, "
-                                         f"{reps_mt} repetitions in {el_mt:.1f} s"}}
+    return n_units * reps / el, n_units * reps_mt / el_mt, n_thr, reps, reps_mt
+
+
+def _cpu_entry(name, run, n_units, bytes_per_unit, rows_per_unit, seconds, sample):
+    ups, ups_mt, n_thr, reps, reps_mt = _time_cpu(run, n_units, seconds)
+    return {"config": name, "value": round(ups * bytes_per_unit / 1e9, 4), "unit": "GB/s",
+            "cores": 1, "kind": "port", "rows_per_s": round(ups * rows_per_unit, 1),
+            "sample": f"{sample}, {reps} repetitions in {seconds:.0f} s, 1 thread",
+            "upper_bound_mt": {"value": round(ups_mt * bytes_per_unit / 1e9, 4), "unit": "GB/s",
+                               "cores": n_thr, "rows_per_s": round(ups_mt * rows_per_unit, 1),
+                               "sample": f"same sample split over {n_thr} threads, "
+                                         f"{reps_mt} repetitions"}}
+
+
+def cpu_baseline(bh, synth, oracle, seconds: float):
+    """Time oracle.qk_norm_rope (src/forward.rs:237-270 restated) on the same
+    config, repeating the 2048-token batch until `seconds` have passed: once on
+    one thread (the reference's decode thread), then row-parallel over the
+    host's cores for a quarter of that time (an upper bound for a threaded
+    CPU path; the C call releases the GIL, tokens are split into contiguous
+    slices, one per thread)."""
+    n_tok, nq, nk, hd = 2048, 24, 4, 256
+    r = synth.Rng(1)
+    q = r.normal(n_tok * nq * hd).reshape(n_tok, nq, hd)
+    k = r.normal(n_tok * nk * hd).reshape(n_tok, nk, hd)
+    wq, wk = r.normal(hd, 1.0, 0.1), r.normal(hd, 1.0, 0.1)
+    pos = synth.positions(n_tok)
+    per_tok = (nq + nk) * hd * 4 * 2
+
+    def run(lo, hi):
+        oracle.qk_norm_rope(q[lo:hi], k[lo:hi], wq, wk, pos[lo:hi], nq, nk, hd, 64, bh.SECTIONS,
+                            1e7, 1e-6)
+
+    e = _cpu_entry("config 2", run, n_tok, per_tok, 1, seconds,
+                   "oracle qk_norm_rope on the full config-2 batch (2048 tokens x 28 heads)")
+    e.pop("config")
+    return e
+
+
+def cpu_baselines_other(bh, synth, oracle, seconds: float):
+    """The CPU oracle (the reference's algorithm restated in C, one thread,
+    then split by rows over the host's threads) on each other config of the
+    benchmark, each on a bounded sample of its rows (said per entry);
+    GB/s counts the config's algorithmic bytes per row."""
+    import numpy as np
+    out = []
+    # config 1: rms_norm_rows [512, 5120] (src/kernels.rs:97-122)
+    r = synth.Rng(0)
+    x1, w1 = r.normal(512 * 5120).reshape(512, 5120), r.normal(5120, 1.0, 0.1)
+    out.append(_cpu_entry(
+        "config 1 rms_norm_rows [512,5120]",
+        lambda lo, hi: oracle.rms_norm_rows(x1[lo:hi], w1, 5120, 1e-6), 512, 5120 * 8, 1,
+        seconds, "oracle rms_norm_rows on all 512 rows"))
+    # config 3: GDN prep [T, 6144] x 48 heads (src/forward.rs:497-507, 524, 539-540, 379)
+    T3 = 512
+    r = synth.Rng(2)
+    conv, z, y = (r.normal(T3 * 6144).reshape(T3, 6144) for _ in range(3))
+    dt, beta = r.normal(T3 * 48, 0.0, 0.5).reshape(T3, 48), r.normal(T3 * 48).reshape(T3, 48)
+    bias = r.normal(48, 0.0, 0.5)
+    A = -np.exp(2 * r.uniform(48)).astype(np.float32)
+    per3 = 6144 * 4 * 2 + 48 * 4 * 2 + 48 * 4 * 2 + 6144 * 4 * 3
+
+    def run3(lo, hi):
+        oracle.silu_l2_part(conv[lo:hi], 6144, 128, 1e-6)
+        oracle.unary(4, z[lo:hi], y[lo:hi])
+        oracle.gdn_gate_prep(dt[lo:hi], bias, A, beta[lo:hi])
+    out.append(_cpu_entry("config 3 gdn_prep [4096,6144]", run3, T3, per3, 1, seconds,
+                          f"oracle silu_l2_part + sigmoid gate + gdn_gate_prep on {T3} of the "
+                          "4096 tokens"))
+    # config 4a: softmax_rows [64, 248320] at temperature 0.7 (src/kernels.rs:175-202)
+    r = synth.Rng(3)
+    n4a = 8 * 248320
+    x4 = r.normal(n4a, 0.0, 3.0)
+    x4[r.uniform(n4a) < 0.01] += np.float32(10.0)
+    x4 = x4.reshape(8, 248320)
+    inv_t = float(np.float32(1.0) / np.float32(0.7))
+    out.append(_cpu_entry("config 4a softmax [64,248320] temp 0.7",
+                          lambda lo, hi: oracle.softmax_rows(x4[lo:hi], 248320, inv_t), 8,
+                          248320 * 8, 1, seconds, "oracle softmax_rows on 8 of the 64 rows"))
+    # config 4b: causal softmax rows [24*2048, 2048]
+    r = synth.Rng(4)
+    xb = r.normal(2048 * 2048, 0.0, 2.0).reshape(2048, 2048)
+    xb[np.triu(np.ones((2048, 2048), bool), 1)] = -np.inf
+    out.append(_cpu_entry("config 4b softmax causal [24*2048,2048]",
+                          lambda lo, hi: oracle.softmax_rows(xb[lo:hi], 2048), 2048, 2048 * 8, 1,
+                          seconds, "oracle softmax_rows on one head's 2048 causal rows"))
+    # config 5: gather + first RMSNorm (src/forward.rs:691, 701-702)
+    tab = synth.pq2_table(synth.Rng(5), 16384, 5120)
+    ids = (synth.Rng(6).u64(1024) % np.uint64(16384)).astype(np.uint32)
+    w5 = synth.Rng(7).normal(5120, 1.0, 0.1)
+    per5 = 1360 + 4 + 2 * 5120 * 4
+    out.append(_cpu_entry("config 5 pq2_gather_rms [8192 ids, 248320x5120]",
+                          lambda lo, hi: oracle.embed_gather(tab, 5120, 16384, ids[lo:hi], w5,
+                                                             1e-6), 1024, per5, 1, seconds,
+                          "oracle embed_gather + rms on 1024 ids from a 16384-row table"))
+    return out
 
 
 def load_traffic():
-    """HBM bytes per launch of the headline kernel from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE runs, if they have been recorded."""
-    p = REPO / "profiles" / "traffic_qk_norm_rope.json"
+    """HBM bytes per step of every bench entry (name -> bytes) from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this bench
+    (profiles/traffic_all_configs.json, commands inside), if recorded."""
+    p = REPO / "profiles" / "traffic_all_configs.json"
     if not p.exists():
-        return None
+        return {}
     try:
-        return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-    except (ValueError, OSError):
-        return None
+        return {e["entry"]: e["hbm_bytes"] for e in json.loads(p.read_text())["entries"]}
+    except (ValueError, OSError, KeyError):
+        return {}
 
 
 def main() -> int:
@@ -502,6 +575,7 @@ def main() -> int:
                 ("rms_norm_rows T=8192", rows_wl[8192]),
                 ("qk_norm_rope T=4096", lambda: wl_qk_norm_rope(bh, synth, dev, stream, 4096)),
                 ("qk_norm_rope T=8192", lambda: wl_qk_norm_rope(bh, synth, dev, stream, 8192)),
+                ("gdn_prep_fused T=2048", lambda: wl_gdn_prep(bh, synth, dev, stream, 2048)),
                 ("gdn_prep_fused T=4096", lambda: wl_gdn_prep(bh, synth, dev, stream)),
                 ("gdn_prep_fused + conv1d T=4096",
                  lambda: wl_gdn_prep(bh, synth, dev, stream, with_conv=True)),
@@ -511,6 +585,7 @@ def main() -> int:
                                     spikes=True)),
                 ("softmax causal [24*2048,2048]",
                  lambda: wl_softmax(bh, synth, dev, stream, 24 * 2048, 2048, 1.0, causal=True)),
+                ("pq2_gather_rms T=2048", lambda: wl_gather_rms(bh, synth, dev, stream, 2048)),
                 ("pq2_gather_rms T=8192", lambda: wl_gather_rms(bh, synth, dev, stream)),
                 ("gdn_step decode T=1", lambda: wl_gdn_step(bh, synth, dev, stream, 1)),
                 ("gdn_step T=256", lambda: wl_gdn_step(bh, synth, dev, stream, 256)),
@@ -542,7 +617,14 @@ def main() -> int:
     if args.cpu_seconds > 0:
         oracle = _load("bonsai_oracle", REPO / "oracle" / "oracle.py")
         cpu = cpu_baseline(bh, synth, oracle, args.cpu_seconds)
+        if not args.headline_only:
+            cpu["other_configs"] = cpu_baselines_other(bh, synth, oracle,
+                                                       max(1.0, args.cpu_seconds / 4))
 
+    traffic = load_traffic()
+    for k in kernels:
+        if k["kernel"] in traffic:
+            k["traffic"] = traffic[k["kernel"]]
     ms = head["ms"]
     line = {
         "metric": "achieved HBM GB/s (% of 8 TB/s) per fused kernel; rows/s at T=2048",
@@ -564,7 +646,7 @@ def main() -> int:
         "rows_per_s": head["rows_per_s"],
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["GBps"] / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic()},
+                     "traffic": traffic.get("qk_norm_rope")},
         "cpu_baseline": cpu,
         "kernels": kernels,
     }
