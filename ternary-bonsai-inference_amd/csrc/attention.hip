@@ -31,7 +31,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -374,6 +376,395 @@ __global__ __launch_bounds__(64 * kCombWaves) void attn_combine_kernel(const flo
   }
 }
 
+// ---- multi-query path (matrix cores) ---------------------------------------
+//
+// Many query tokens at once (prefill, verification): block (c, t, g) takes
+// position chunk c, q-row tile t and kv head g; the tile's rows are
+// (query i, head g*REP + r) for 128 consecutive row numbers i*REP + r, so one
+// K/V tile staged in LDS serves every q head of the kv head and every query
+// of the tile.  Both products run on v_mfma_f32_16x16x32_f16 in transposed
+// form -- S^T = K Q^T (positions x rows), O^T = V^T P^T (dims x rows) -- so
+// the lane that holds a row's scores (row l % 16, eight positions) holds
+// exactly that row's P fragment for the next product and that row's output
+// dims: no transposes, and the softmax state of a row sits in the four lanes
+// l % 16 + 16 g, combined with two permlane swaps.
+//
+// f32 inputs need more than f16's 11 bits: every operand is split into
+// hi = f16(x') and lo = f16(x' - hi) (22 significant bits) and a product is
+// hi*hi + hi*lo + lo*hi, accumulated in f32 (an f16 cache is exact in f16:
+// its lo parts are zero and skipped).  The splits are made safe by powers of
+// two: a q row is scaled so its largest |q| lies in [2^13, 2^14), each
+// staged K position row likewise, each staged V tile as a whole, and P by
+// 2^14.  The scores are unscaled exactly before the softmax (then times
+// 1/sqrtf(hd)); each tile's P.V product is formed from zero and added to the
+// f32 output accumulators, unscaled, as they take the online-softmax
+// correction.  Results match the reference's f32 arithmetic to ~1e-7
+// relative (sums in another order).
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+constexpr int kMqThreads = 512; // 8 waves
+constexpr int kMqRows = 128;    // q rows per block: 8 waves x 16
+constexpr int kMqTile = 32;     // positions per tile
+constexpr int kKStride = 264;   // halves per staged K row (256 + 8: no bank conflicts)
+constexpr int kVStride = 40;    // halves per staged V^T row (32 + 8)
+constexpr int kMqMinRows = 48;  // q rows per kv head from which this path is taken
+
+struct MqArgs {
+  const float *q;
+  const void *kc, *vc;
+  float *pm, *pl, *pacc;  // chunk partials [n_q][n_head][n_chunks] (+ [hd])
+  size_t pos0, kv_stride, chunk;
+  int n_head, n_q, rep, n_chunks, n_kv;
+  float scale;
+};
+
+// max over the four lanes l % 16 + 16 g (one row): permlane swaps
+__device__ __forceinline__ float rows4_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// 2^e as a float for e <= 127; 0 below the normal range
+__device__ __forceinline__ float pow2f(int e) {
+  return e < -126 ? 0.0f : __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+
+// exponent that puts the largest magnitude m in [2^13, 2^14); 0 for 0 or non-finite m
+__device__ __forceinline__ int split_shift(float m) {
+  if (!(m > 0.0f) || !isfinite(m)) return 0;
+  return 13 - ilogbf(m);
+}
+
+// scale exponent of a V tile: its largest |v| into [2^13, 2^14), kept
+// where 2^(vs - 14) stays a normal float
+__device__ __forceinline__ int v_shift(float m) {
+  if (!(m > 0.0f) || !isfinite(m)) return 0;
+  const int e = ilogbf(m) - 13;
+  return e < -112 ? -112 : (e > 114 ? 114 : e);
+}
+
+__device__ __forceinline__ void split_hl(float x, _Float16 &h, _Float16 &l) {
+  h = static_cast<_Float16>(x);
+  l = static_cast<_Float16>(x - static_cast<float>(h));
+}
+
+// Column of position p (0..31) in a staged V^T row: the eight positions a
+// lane group g feeds one P.V step -- 4g .. 4g+3 and 16+4g .. 16+4g+3, the
+// positions its S^T fragment holds -- sit in columns 8g .. 8g+7, so the
+// fragment is one 16-byte LDS read.
+__device__ __forceinline__ int vcol(int p) { return p < 16 ? 8 * (p >> 2) + (p & 3) : 8 * ((p - 16) >> 2) + 4 + (p & 3); }
+
+template <bool F16>
+__global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 sKh[kMqTile * kKStride];
+  __shared__ __attribute__((aligned(16))) _Float16 sKl[F16 ? 8 : kMqTile * kKStride];
+  __shared__ __attribute__((aligned(16))) _Float16 sVh[kHd * kVStride];
+  __shared__ __attribute__((aligned(16))) _Float16 sVl[F16 ? 8 : kHd * kVStride];
+  __shared__ __attribute__((aligned(16))) _Float16 sQl[kMqRows * kKStride];  // q lo fragments
+  __shared__ float sKs[kMqTile];  // 2^-b of each staged K row
+  __shared__ unsigned sVmax[2];   // bits of a tile's largest |v| (non-negative floats order as ints), by tile parity
+  // XCD-aware numbering: workgroups go to the 8 XCDs round robin by id, so
+  // the row tiles of one (chunk, kv head) get ids 8 apart -- the same XCD,
+  // dispatched together -- and share the K/V tiles in that XCD's L2.
+  const int R = a.n_q * a.rep;
+  const int tiles_r = (R + kMqRows - 1) / kMqRows;
+  int c, t, g;
+  {
+    const int b = blockIdx.x;
+    const int n_groups = a.n_chunks * a.n_kv;  // (chunk, kv head) pairs
+    const int full = n_groups / 8 * 8;         // groups placed 8 at a time
+    const int x = b % 8, jb = b / 8;
+    int q;
+    if (jb < (full / 8) * tiles_r) {
+      q = (jb / tiles_r) * 8 + x;
+      t = jb % tiles_r;
+    } else {  // the last n_groups % 8 groups, in plain order
+      const int rest = b - full * tiles_r;
+      q = full + rest / tiles_r;
+      t = rest % tiles_r;
+    }
+    c = q % a.n_chunks;
+    g = q / a.n_chunks;
+  }
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, grp = l >> 4;
+  const int rho = t * kMqRows + w * 16 + r16;
+  const bool valid = rho < R;
+  const int qi = valid ? rho / a.rep : 0;
+  const int head = g * a.rep + (valid ? rho % a.rep : 0);
+  const size_t limit = valid ? a.pos0 + qi + 1 : 0;  // this row sees positions < limit
+  const int last_row = (t + 1) * kMqRows - 1 < R - 1 ? (t + 1) * kMqRows - 1 : R - 1;
+  const size_t lim_blk = a.pos0 + last_row / a.rep + 1;
+  const size_t beg = static_cast<size_t>(c) * a.chunk;
+  const size_t end = beg + a.chunk < lim_blk ? beg + a.chunk : lim_blk;
+  const size_t part = (static_cast<size_t>(qi) * a.n_head + head) * a.n_chunks + c;
+  if (beg >= end) {  // no position of this chunk is visible to the tile
+    if (valid) {
+      if (grp == 0) {
+        a.pm[part] = -INFINITY;
+        a.pl[part] = 0.0f;
+      }
+      f32x4 *acc = reinterpret_cast<f32x4 *>(a.pacc + part * kHd);
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) acc[4 * dt + grp] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    return;
+  }
+
+  // q row fragments: dims 32 s + 8 grp .. +7 of row rho, scaled and split
+  half8 qh[8];  // the lo parts go to LDS (registers hold the next tile's K/V)
+  _Float16 *qlrow = sQl + (w * 16 + r16) * kKStride + 8 * grp;
+  int qa = 0;
+  {
+    const f32x4 *qr = reinterpret_cast<const f32x4 *>(
+        a.q + (static_cast<size_t>(qi) * a.n_head + head) * kHd + 8 * grp);
+    f32x4 v[16];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      v[2 * s] = valid ? qr[8 * s] : f32x4{0.f, 0.f, 0.f, 0.f};
+      v[2 * s + 1] = valid ? qr[8 * s + 1] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+    qa = split_shift(rows4_max(m));
+    const float f = ldexpf(1.0f, qa);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 x = v[2 * s + h];
+        _Float16 a0, a1, a2, a3, b0, b1, b2, b3;
+        split_hl(x.x * f, a0, b0);
+        split_hl(x.y * f, a1, b1);
+        split_hl(x.z * f, a2, b2);
+        split_hl(x.w * f, a3, b3);
+        qh[s][4 * h + 0] = a0; qh[s][4 * h + 1] = a1; qh[s][4 * h + 2] = a2; qh[s][4 * h + 3] = a3;
+        half4v lo4;
+        lo4[0] = b0; lo4[1] = b1; lo4[2] = b2; lo4[3] = b3;
+        *reinterpret_cast<half4v *>(qlrow + 32 * s + 4 * h) = lo4;
+      }
+    }
+  }
+  const float qunscale = ldexpf(a.scale, -qa);  // scores: S' * 2^-a * 2^-b * (1/sqrtf(hd))
+
+  f32x4 o[16];
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float run_m = -INFINITY, run_l = 0.0f;
+  // the accumulators are in units of 2^(14 - vs_cur); vs_cur only grows
+  // within a block, so changing the unit never scales a value up
+  int vs_cur = -112;
+  if (tid == 0) {
+    sVmax[0] = 0u;
+    sVmax[1] = 0u;
+  }
+  __syncthreads();
+  int parity = 0;
+
+  const size_t head_off = static_cast<size_t>(g) * kHd;
+  // staging: K position sp, dims 16 kpart .. +15 (16 lanes per position);
+  // V dims vd, vd + 64, vd + 128, vd + 192 of positions 4 vpg .. +3 (a
+  // wave's lanes read 256 consecutive bytes per load, and their V^T stores
+  // go to consecutive rows: no LDS bank conflicts)
+  const int sp = tid >> 4, kpart = tid & 15;
+  const int vd = tid & 63, vpg = tid >> 6;
+  // this lane's share of a tile: K position sp, dims 16 kpart .. +15; V
+  // positions 4 vpg .. +3 at dims vd + 64 i.  Registers hold the next
+  // tile's share while the current one is multiplied.
+  using KReg = typename std::conditional<F16, uint4[2], f32x4[4]>::type;
+  using VElt = typename std::conditional<F16, uint16_t, float>::type;
+  KReg kr;
+  VElt vr[4][4];
+  auto fetch = [&](size_t t0) {
+    const int nt = static_cast<int>(end - t0 < kMqTile ? end - t0 : kMqTile);
+    const size_t krow = (t0 + (sp < nt ? sp : nt - 1)) * a.kv_stride + head_off + 16 * kpart;
+    const VElt *vcp = static_cast<const VElt *>(a.vc);
+    if constexpr (F16) {
+      const uint16_t *kcp = static_cast<const uint16_t *>(a.kc);
+      kr[0] = *reinterpret_cast<const uint4 *>(kcp + krow);
+      kr[1] = *reinterpret_cast<const uint4 *>(kcp + krow + 8);
+    } else {
+      const float *kcp = static_cast<const float *>(a.kc);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) kr[k] = *reinterpret_cast<const f32x4 *>(kcp + krow + 4 * k);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int pj = 4 * vpg + jj;
+      const size_t e = (t0 + (pj < nt ? pj : nt - 1)) * a.kv_stride + head_off + vd;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vr[jj][i] = vcp[e + 64 * i];
+    }
+  };
+  fetch(beg);
+  for (size_t t0 = beg; t0 < end; t0 += kMqTile) {
+    const int nt = static_cast<int>(end - t0 < kMqTile ? end - t0 : kMqTile);
+    const int vc0 = vcol(4 * vpg);  // the 4 columns of this lane's positions
+    if constexpr (F16) {
+      const uint4 k0 = kr[0], k1 = kr[1];
+      uint4 *kd = reinterpret_cast<uint4 *>(sKh + sp * kKStride + 16 * kpart);
+      kd[0] = k0;
+      kd[1] = k1;
+      if (kpart == 0) sKs[sp] = 1.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        half4v col;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) col[jj] = __builtin_bit_cast(_Float16, vr[jj][i]);
+        *reinterpret_cast<half4v *>(sVh + (vd + 64 * i) * kVStride + vc0) = col;
+      }
+      __syncthreads();
+    } else {
+      float km = 0.0f, vm = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        km = fmaxf(km, fmaxf(fmaxf(fabsf(kr[k].x), fabsf(kr[k].y)), fmaxf(fabsf(kr[k].z), fabsf(kr[k].w))));
+        vm = fmaxf(vm, fmaxf(fmaxf(fabsf(vr[k][0]), fabsf(vr[k][1])), fmaxf(fabsf(vr[k][2]), fabsf(vr[k][3]))));
+      }
+      km = lane_group_reduce<16>(km, FMaxOp{});
+      vm = lane_group_reduce<64>(vm, FMaxOp{});
+      if (l == 0) atomicMax(&sVmax[parity], __float_as_uint(vm));
+      const int kb = split_shift(km);
+      const float kf = ldexpf(1.0f, kb);
+      _Float16 *khp = sKh + sp * kKStride + 16 * kpart;
+      _Float16 *klp = sKl + sp * kKStride + 16 * kpart;
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        half8 hv, lv;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const f32x4 x = kr[2 * k2 + k];
+          _Float16 h, lo;
+          split_hl(x.x * kf, h, lo); hv[4 * k + 0] = h; lv[4 * k + 0] = lo;
+          split_hl(x.y * kf, h, lo); hv[4 * k + 1] = h; lv[4 * k + 1] = lo;
+          split_hl(x.z * kf, h, lo); hv[4 * k + 2] = h; lv[4 * k + 2] = lo;
+          split_hl(x.w * kf, h, lo); hv[4 * k + 3] = h; lv[4 * k + 3] = lo;
+        }
+        *reinterpret_cast<half8 *>(khp + 8 * k2) = hv;
+        *reinterpret_cast<half8 *>(klp + 8 * k2) = lv;
+      }
+      if (kpart == 0) sKs[sp] = ldexpf(1.0f, -kb);
+      __syncthreads();  // sVmax[parity] complete
+      const int vst = v_shift(__uint_as_float(sVmax[parity]));
+      const int vs = vst > vs_cur ? vst : vs_cur;
+      const float vf = ldexpf(1.0f, -vs);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        half4v ch, cl;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          _Float16 h, lo;
+          split_hl(vr[jj][i] * vf, h, lo);
+          ch[jj] = h;
+          cl[jj] = lo;
+        }
+        *reinterpret_cast<half4v *>(sVh + (vd + 64 * i) * kVStride + vc0) = ch;
+        *reinterpret_cast<half4v *>(sVl + (vd + 64 * i) * kVStride + vc0) = cl;
+      }
+      __syncthreads();
+    }
+    if (t0 + kMqTile < end) fetch(t0 + kMqTile);  // the next tile, in flight during this one
+    int vs = vs_cur;
+    if constexpr (!F16) {
+      const int vst = v_shift(__uint_as_float(sVmax[parity]));
+      vs = vst > vs_cur ? vst : vs_cur;
+      // the other slot was last read before the previous tile's final
+      // barrier and is next written after this tile's
+      if (tid == 0) sVmax[parity ^ 1] = 0u;
+      parity ^= 1;
+    } else {
+      vs = 0;
+    }
+
+    // S^T = K' Q'^T: lane holds row r16, positions 16 ct + 4 grp + i
+    f32x4 st[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      const _Float16 *kh = sKh + (16 * ct + r16) * kKStride + 8 * grp;
+      const _Float16 *kl = sKl + (F16 ? 0 : (16 * ct + r16) * kKStride + 8 * grp);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const half8 ka = *reinterpret_cast<const half8 *>(kh + 32 * s);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            ka, *reinterpret_cast<const half8 *>(qlrow + 32 * s), acc, 0, 0, 0);
+        if constexpr (!F16) {
+          const half8 kb = *reinterpret_cast<const half8 *>(kl + 32 * s);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb, qh[s], acc, 0, 0, 0);
+        }
+      }
+      st[ct] = acc;
+    }
+    // scores, masked: causal limit of the row, the tile's valid positions
+    float sc[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pj = 16 * ct + 4 * grp + i;
+        const bool vis = pj < nt && t0 + pj < limit;
+        const float x = st[ct][i] * sKs[pj] * qunscale;
+        sc[4 * ct + i] = vis ? x : -INFINITY;
+        tmax = fmaxf(tmax, sc[4 * ct + i]);
+      }
+    tmax = rows4_max(tmax);
+    const float m_new = fmaxf(run_m, tmax);
+    const bool none = m_new == -INFINITY;
+    const float corr = none ? 1.0f : exp_hw(run_m - m_new);
+    float psum = 0.0f;
+    half8 ph, pl;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float p = none ? 0.0f : exp_hw(sc[k] - m_new);
+      psum += p;
+      _Float16 h, lo;
+      split_hl(p * 16384.0f, h, lo);
+      ph[k] = h;
+      pl[k] = lo;
+    }
+    run_l = run_l * corr + rows4_sum(psum);
+    run_m = m_new;
+    // accumulators: softmax correction and the change of unit (never up)
+    const float ocorr = F16 ? corr : corr * pow2f(vs_cur - vs);
+    vs_cur = vs;
+    // O^T += V'^T P*^T: A = V^T rows 16 dt + r16, columns 8 grp .. +7
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const half8 va = *reinterpret_cast<const half8 *>(sVh + (16 * dt + r16) * kVStride + 8 * grp);
+      f32x4 acc = o[dt] * ocorr;
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, acc, 0, 0, 0);
+      if constexpr (!F16) {
+        const half8 vb = *reinterpret_cast<const half8 *>(sVl + (16 * dt + r16) * kVStride + 8 * grp);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(vb, ph, acc, 0, 0, 0);
+      }
+      o[dt] = acc;
+    }
+    __syncthreads();  // the staged tile is consumed
+  }
+  if (valid) {
+    if (grp == 0) {
+      a.pm[part] = run_m;
+      a.pl[part] = run_l;
+    }
+    const float u = F16 ? 1.0f / 16384.0f : pow2f(vs_cur - 14);
+    f32x4 *acc = reinterpret_cast<f32x4 *>(a.pacc + part * kHd);
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) acc[4 * dt + grp] = o[dt] * u;
+  }
+}
+
 // ---- generic path ----------------------------------------------------------
 
 struct GenericArgs {
@@ -456,6 +847,27 @@ int launch_decode(const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
 }
 
 template <class T>
+// Resident blocks of the multi-query kernel on this device (per cache type).
+size_t mq_capacity(bool f16) {
+  static std::mutex mu;
+  static size_t cap[64][2] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  size_t &c = cap[dev][f16 ? 1 : 0];
+  if (c == 0) {
+    int per_cu = 0, cus = 0;
+    const hipError_t e1 =
+        f16 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mq_kernel<true>, kMqThreads, 0)
+            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_mq_kernel<false>, kMqThreads, 0);
+    if (e1 != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        per_cu <= 0 || cus <= 0)
+      return 256;
+    c = static_cast<size_t>(per_cu) * static_cast<size_t>(cus);
+  }
+  return c;
+}
+
 int decode_dispatch(int rep, const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
   switch (rep) {
     case 1: return launch_decode<1, T>(a, n_kv, n_q, st);
@@ -526,6 +938,47 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
   const bool fast = hd == static_cast<size_t>(kHd) && decode_rep(rep) && aligned16(q) &&
                     (reinterpret_cast<uintptr_t>(k_cache) % (4 * esz)) == 0 &&
                     (reinterpret_cast<uintptr_t>(v_cache) % (4 * esz)) == 0;
+  if (fast && n_q * rep >= static_cast<size_t>(kMqMinRows)) {
+    // many queries: matrix-core path, about two blocks per CU over (chunk,
+    // row tile, kv head); chunks of whole tiles
+    const size_t R = n_q * rep;
+    const size_t tiles_r = (R + kMqRows - 1) / kMqRows;
+    if (tiles_r > 65535 || n_kv > 65535) return fail(BH_ERR_SHAPE, "attention: too many queries");
+    // chunks per (row tile, kv head): the most that keep every block resident
+    // in one round (a second partial round would double the time)
+    const size_t cap = mq_capacity(f16);
+    const size_t want = cap / (tiles_r * n_kv) > 0 ? cap / (tiles_r * n_kv) : 1;
+    const size_t ptiles = (n_max + kMqTile - 1) / kMqTile;
+    const size_t per = (ptiles + want - 1) / want;
+    const size_t chunk = per * kMqTile;
+    const size_t n_chunks = (n_max + chunk - 1) / chunk;
+    if (n_chunks > 65535) return fail(BH_ERR_SHAPE, "attention: too many positions");
+    size_t rows = 0, sbytes = 0;
+    if (!mul_size(n_q, n_head, n_chunks, &rows) || !mul_size(rows, kHd + 2, 4, &sbytes))
+      return fail(BH_ERR_SHAPE, "attention: scratch size overflows");
+    float *scratch = static_cast<float *>(device_scratch(sbytes, kScratchAttention, st));
+    if (scratch == nullptr) return BH_ERR_HIP;
+    MqArgs m{q, k_cache, v_cache, scratch, scratch + rows, scratch + 2 * rows, pos0, kv_stride,
+             chunk, static_cast<int>(n_head), static_cast<int>(n_q), static_cast<int>(rep),
+             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale};
+    // 1-D grid of (chunk, kv head, row tile) in XCD-aware order (the kernel
+    // decodes it)
+    const size_t nb = n_chunks * n_kv * tiles_r;
+    if (nb > 0x7fffffffu) return fail(BH_ERR_SHAPE, "attention: too many blocks");
+    const dim3 grid(static_cast<unsigned>(nb));
+    if (f16)
+      BH_LAUNCH(attn_mq_kernel<true>, grid, kMqThreads, 0, st, m);
+    else
+      BH_LAUNCH(attn_mq_kernel<false>, grid, kMqThreads, 0, st, m);
+    const dim3 cgrid(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims);
+    if (n_chunks >= 64)
+      BH_LAUNCH(attn_combine_kernel<16>, cgrid, 1024, 0, st, m.pm, m.pl, m.pacc,
+                static_cast<int>(n_chunks), kHd, out);
+    else
+      BH_LAUNCH(attn_combine_kernel<4>, cgrid, 256, 0, st, m.pm, m.pl, m.pacc,
+                static_cast<int>(n_chunks), kHd, out);
+    return ok();
+  }
   if (fast) {
     // chunks of whole tiles: about 512 blocks over (chunk, kv head) for one
     // query, 2048 over (chunk, kv head, query) for several.  Measured at ctx

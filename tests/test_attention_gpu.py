@@ -161,3 +161,32 @@ def test_store_then_attend_token_loop(bh, oracle, synth, dev):
     assert rel_err(np.concatenate(outs), ref) <= TOL
     batch = _h(bh.attention(_t(q, dev), 0, dk, dv, n_kv))
     assert rel_err(batch, ref) <= TOL
+
+
+@pytest.mark.parametrize("n_q,pos0,f16,n_head,n_kv,vscale,qscale", [
+    (64, 4032, False, 24, 4, 1.0, 2.0),    # the bench's prefill case
+    (64, 4032, True, 24, 4, 1.0, 2.0),
+    (50, 17, False, 24, 4, 1.0, 2.0),      # ragged row tiles and position tiles
+    (9, 300, False, 16, 2, 1.0, 2.0),      # grouping 8
+    (40, 100, False, 8, 8, 1.0, 2.0),      # grouping 1
+    (16, 500, False, 24, 4, 3e6, 1e-3),    # large v (scaled-down tiles), small q
+    (16, 500, False, 24, 4, 1e-6, 10.0),   # tiny v, peaked attention (logits ~ N(0, 10^2))
+    (33, 2000, True, 12, 4, 1.0, 0.05),    # f16 cache, near-flat attention
+])
+def test_attention_multi_query_matrix_cores(bh, oracle, synth, dev, n_q, pos0, f16, n_head, n_kv,
+                                            vscale, qscale):
+    """Many queries per kv head take the matrix-core path (f16 hi/lo
+    products with power-of-two scaling); <= 1e-5 against the oracle's
+    per-token loop, on magnitudes that stress the splits."""
+    hd = 256
+    _say("attention mq", n_q, pos0, "f16" if f16 else "f32", n_head, n_kv, vscale, qscale)
+    q, kc, vc = _case(synth, n_q, pos0, n_head, n_kv, hd, 700 + n_q + pos0, qscale=qscale)
+    vc = (vc * np.float32(vscale)).astype(np.float32)
+    if f16:
+        kc = kc.astype(np.float16).view(np.uint16)
+        vc = vc.astype(np.float16).view(np.uint16)
+    ref = oracle.attention(q, pos0, kc, vc, n_kv)
+    got = _run(bh, dev, q, pos0, kc, vc, n_kv)
+    err = rel_err(got, ref)
+    _say("  rel", err)
+    assert err <= TOL
