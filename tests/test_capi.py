@@ -286,3 +286,27 @@ def test_attention_scratch_size_does_not_wrap(bh):
     p = ctypes.c_void_p(16)  # never dereferenced: the call fails on the size first
     st = lib.bh_attention(p, 65535, (1 << 40) - 65535, p, p, 0, 65535, 1, 64, p, None)
     assert st == bh.BH_ERR_SHAPE and "overflows" in bh.last_error()
+
+
+def test_rust_ffi_matches_header(bh):
+    """rust/src/hip/mod.rs (the reference-side binding) declares only entry
+    points the header has, each with the header's parameter count."""
+    import re
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    rs = (root / "rust" / "src" / "hip" / "mod.rs").read_text()
+    hdr = re.sub(r"/\*.*?\*/", "", (root / "include" / "bonsai_hip.h").read_text(), flags=re.S)
+    c_params = {}
+    for m in re.finditer(r"\b(?:int|const char \*|size_t)\s*\**\s*(bh_\w+)\s*\(([^)]*)\)\s*;", hdr):
+        args = m.group(2).strip()
+        c_params[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    ext = rs[rs.index('extern "C"'):]
+    ext = ext[:ext.index("\n}\n")]
+    found = 0
+    for m in re.finditer(r"fn (bh_\w+)\(([^)]*)\)", ext):
+        name, args = m.group(1), m.group(2).strip()
+        n = 0 if not args else args.rstrip(",").count(",") + 1
+        assert name in c_params, name
+        assert n == c_params[name], (name, n, c_params[name])
+        found += 1
+    assert found >= 20
