@@ -846,7 +846,6 @@ int launch_decode(const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
   return ok();
 }
 
-template <class T>
 // Resident blocks of the multi-query kernel on this device (per cache type).
 size_t mq_capacity(bool f16) {
   static std::mutex mu;
@@ -868,6 +867,7 @@ size_t mq_capacity(bool f16) {
   return c;
 }
 
+template <class T>
 int decode_dispatch(int rep, const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
   switch (rep) {
     case 1: return launch_decode<1, T>(a, n_kv, n_q, st);

@@ -1,0 +1,134 @@
+// stream_ceiling -- what plain streaming reaches on this GPU at the bench's
+// sizes: the ceiling the fused kernels are measured against.
+//
+// Times, with HIP events around a replayed HIP graph of 40 launches (the
+// bench's method; eight rotating buffer pairs, larger than the 256 MB
+// Infinity Cache), a one-float4-per-lane copy (the fastest streaming shape
+// found: 256-lane blocks, non-temporal loads, non-temporal stores with or
+// without device scope), a pure read and a pure write of the same bytes, and
+// empty kernels of the fused kernels' grid shapes (the per-launch dispatch
+// cost).  Prints a markdown table; takes the sizes in MiB each way as
+// arguments (defaults: the bench's configs).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#define CK(x)                                                                       \
+  do {                                                                              \
+    hipError_t e_ = (x);                                                            \
+    if (e_ != hipSuccess) {                                                         \
+      std::fprintf(stderr, "%s:%d %s\n", __FILE__, __LINE__, hipGetErrorString(e_)); \
+      std::exit(1);                                                                 \
+    }                                                                               \
+  } while (0)
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <bool DEVICE_SCOPE>
+__device__ __forceinline__ void store_nt(f4v *p, f4v v) {
+  if (DEVICE_SCOPE)
+    asm volatile("global_store_dwordx4 %0, %1, off sc1 nt" ::"v"(p), "v"(v) : "memory");
+  else
+    __builtin_nontemporal_store(v, p);
+}
+
+template <bool DEVICE_SCOPE>
+__global__ __launch_bounds__(256) void copy_kernel(const f4v *__restrict__ in, f4v *__restrict__ out,
+                                                   size_t n4) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n4) store_nt<DEVICE_SCOPE>(out + i, __builtin_nontemporal_load(in + i));
+}
+
+__global__ __launch_bounds__(256) void read_kernel(const f4v *__restrict__ in, f4v *out, size_t n4) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  const f4v v = i < n4 ? __builtin_nontemporal_load(in + i) : f4v{0.f, 0.f, 0.f, 0.f};
+  if (v.x == 1234.5f) out[0] = v;  // never true for the fill below; keeps the load
+}
+
+__global__ __launch_bounds__(256) void write_kernel(f4v *out, size_t n4) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n4) __builtin_nontemporal_store(f4v{1.f, 2.f, 3.f, 4.f}, out + i);
+}
+
+__global__ void empty_kernel(float *p) {
+  if (p != nullptr && threadIdx.x == 100000) p[0] = 1.0f;
+}
+
+int main(int argc, char **argv) {
+  std::vector<size_t> sizes_mib;
+  for (int i = 1; i < argc; ++i) sizes_mib.push_back(std::strtoull(argv[i], nullptr, 10));
+  if (sizes_mib.empty()) sizes_mib = {10, 40, 56, 80, 160, 320};
+  hipStream_t st;
+  CK(hipStreamCreate(&st));
+  hipEvent_t e0, e1;
+  CK(hipEventCreate(&e0));
+  CK(hipEventCreate(&e1));
+  constexpr int kSteps = 40;
+  auto time_graph = [&](auto launch) {
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    CK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal));
+    for (int k = 0; k < kSteps; ++k) launch(k);
+    CK(hipStreamEndCapture(st, &g));
+    CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    CK(hipGraphLaunch(ge, st));
+    CK(hipStreamSynchronize(st));
+    std::vector<double> r;
+    for (int rep = 0; rep < 7; ++rep) {
+      CK(hipGraphLaunch(ge, st));  // keeps the GPU busy while the timed replay is submitted
+      CK(hipEventRecord(e0, st));
+      CK(hipGraphLaunch(ge, st));
+      CK(hipEventRecord(e1, st));
+      CK(hipEventSynchronize(e1));
+      float ms = 0.f;
+      CK(hipEventElapsedTime(&ms, e0, e1));
+      r.push_back(ms * 1000.0 / kSteps);
+    }
+    CK(hipGraphExecDestroy(ge));
+    CK(hipGraphDestroy(g));
+    std::sort(r.begin(), r.end());
+    return r[r.size() / 2];
+  };
+  std::printf("| launch | us per launch |\n|---|---:|\n");
+  const unsigned shapes[][2] = {{1, 64}, {2048, 640}, {4096, 448}, {28672, 256}};
+  for (const auto &sh : shapes)
+    std::printf("| empty kernel, %u blocks of %u lanes | %.2f |\n", sh[0], sh[1],
+                time_graph([&](int) { hipLaunchKernelGGL(empty_kernel, dim3(sh[0]), dim3(sh[1]), 0, st, nullptr); }));
+  std::printf("\n| MiB each way | copy nt us | %% of 8 TB/s | copy sc1 nt us | %% | read us | %% | write us | %% |\n");
+  std::printf("|---:|---:|---:|---:|---:|---:|---:|---:|---:|\n");
+  constexpr int kSets = 8;
+  for (size_t mib : sizes_mib) {
+    const size_t bytes = mib << 20, n4 = bytes / 16;
+    std::vector<f4v *> a(kSets), b(kSets);
+    for (int s = 0; s < kSets; ++s) {
+      CK(hipMalloc(&a[s], bytes));
+      CK(hipMalloc(&b[s], bytes));
+      CK(hipMemset(a[s], 1, bytes));
+      CK(hipMemset(b[s], 1, bytes));
+    }
+    const unsigned grid = static_cast<unsigned>((n4 + 255) / 256);
+    const double c0 = time_graph([&](int k) {
+      hipLaunchKernelGGL(copy_kernel<false>, dim3(grid), dim3(256), 0, st, a[k % kSets], b[k % kSets], n4);
+    });
+    const double c1 = time_graph([&](int k) {
+      hipLaunchKernelGGL(copy_kernel<true>, dim3(grid), dim3(256), 0, st, a[k % kSets], b[k % kSets], n4);
+    });
+    const double rd = time_graph([&](int k) {
+      hipLaunchKernelGGL(read_kernel, dim3(grid), dim3(256), 0, st, a[k % kSets], b[k % kSets], n4);
+    });
+    const double wr = time_graph([&](int k) {
+      hipLaunchKernelGGL(write_kernel, dim3(grid), dim3(256), 0, st, b[k % kSets], n4);
+    });
+    auto pct = [](double b_, double us) { return b_ / us / 8e6 * 100.0; };
+    std::printf("| %zu | %.2f | %.1f | %.2f | %.1f | %.2f | %.1f | %.2f | %.1f |\n", mib, c0,
+                pct(2.0 * bytes, c0), c1, pct(2.0 * bytes, c1), rd, pct(bytes, rd), wr, pct(bytes, wr));
+    for (int s = 0; s < kSets; ++s) {
+      CK(hipFree(a[s]));
+      CK(hipFree(b[s]));
+    }
+  }
+  return 0;
+}
