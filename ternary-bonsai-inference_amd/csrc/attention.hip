@@ -721,12 +721,12 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
     tmax = rows4_max(tmax);
     const float m_new = fmaxf(run_m, tmax);
     const bool none = m_new == -INFINITY;
-    const float corr = none ? 1.0f : exp_hw(run_m - m_new);
+    const float corr = exp_hw(none ? 0.0f : run_m - m_new);
     float psum = 0.0f;
     half8 ph, pl;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float p = none ? 0.0f : exp_hw(sc[k] - m_new);
+      const float p = exp_hw(none ? -INFINITY : sc[k] - m_new);
       psum += p;
       _Float16 h, lo;
       split_hl(p * 16384.0f, h, lo);
@@ -739,10 +739,16 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
     const float ocorr = F16 ? corr : corr * pow2f(vs_cur - vs);
     vs_cur = vs;
     // O^T += V'^T P*^T: A = V^T rows 16 dt + r16, columns 8 grp .. +7
+    // (the rescale is skipped when no row of the wave needs it: the running
+    // maxima and the unit settle after the first tiles)
+    if (__builtin_amdgcn_ballot_w64(ocorr != 1.0f) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) o[dt] = o[dt] * ocorr;
+    }
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) {
       const half8 va = *reinterpret_cast<const half8 *>(sVh + (16 * dt + r16) * kVStride + 8 * grp);
-      f32x4 acc = o[dt] * ocorr;
+      f32x4 acc = o[dt];
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, acc, 0, 0, 0);
       if constexpr (!F16) {
@@ -763,6 +769,47 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 16; ++dt) acc[4 * dt + grp] = o[dt] * u;
   }
+}
+
+// Chunk merge of the multi-query path (few chunks, many rows): one block of
+// four waves per (query, head) row, wave w owning dims 64 w .. 64 w + 63 (one
+// per lane).  Every wave weighs the chunks itself -- e^(m_c - M) from the
+// chunks' (max, sum) pairs, one chunk per lane, a loop beyond 64 -- then adds
+// the chunks' accumulators, all of a lane's loads in flight together, and
+// divides by the weighted sum.  Chunks with no visible position (max -inf)
+// are left out.
+__global__ __launch_bounds__(256) void attn_merge_rows_kernel(const float *pm, const float *pl,
+                                                              const float *pacc, int n_chunks,
+                                                              float *out) {
+  __shared__ float s_w[4][64];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const size_t row = blockIdx.x;
+  const float *m = pm + row * n_chunks;
+  const float *l = pl + row * n_chunks;
+  const float *acc = pacc + row * n_chunks * static_cast<size_t>(kHd) + 64 * w + lane;
+  float big = -INFINITY;
+  for (int c = lane; c < n_chunks; c += 64) big = fmaxf(big, m[c]);
+  big = wave_max(big);
+  float den = 0.0f, num = 0.0f;
+  for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+    const int c = c0 + lane;
+    const float mc = c < n_chunks ? m[c] : -INFINITY;
+    const float lc = c < n_chunks ? l[c] : 0.0f;
+    const float wc = mc != -INFINITY ? expf(mc - big) : 0.0f;
+    den += lc * wc;
+    s_w[w][lane] = wc;  // read back by this wave only
+    __builtin_amdgcn_wave_barrier();
+    const int cn = n_chunks - c0 < 64 ? n_chunks - c0 : 64;
+#pragma unroll 16
+    for (int k = 0; k < cn; ++k) {
+      const float a = acc[static_cast<size_t>(c0 + k) * kHd];
+      const float wk = s_w[w][k];
+      num += wk != 0.0f ? a * wk : 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();  // weights consumed before the next tile's
+  }
+  den = wave_sum(den);
+  out[row * kHd + 64 * w + lane] = num / den;
 }
 
 // ---- generic path ----------------------------------------------------------
@@ -970,13 +1017,8 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
       BH_LAUNCH(attn_mq_kernel<true>, grid, kMqThreads, 0, st, m);
     else
       BH_LAUNCH(attn_mq_kernel<false>, grid, kMqThreads, 0, st, m);
-    const dim3 cgrid(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims);
-    if (n_chunks >= 64)
-      BH_LAUNCH(attn_combine_kernel<16>, cgrid, 1024, 0, st, m.pm, m.pl, m.pacc,
-                static_cast<int>(n_chunks), kHd, out);
-    else
-      BH_LAUNCH(attn_combine_kernel<4>, cgrid, 256, 0, st, m.pm, m.pl, m.pacc,
-                static_cast<int>(n_chunks), kHd, out);
+    BH_LAUNCH(attn_merge_rows_kernel, static_cast<unsigned>(n_q * n_head), 256, 0, st, m.pm, m.pl,
+              m.pacc, static_cast<int>(n_chunks), out);
     return ok();
   }
   if (fast) {
