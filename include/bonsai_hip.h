@@ -222,6 +222,16 @@ int bh_gdn_step(const float *q, const float *k, const float *v, const float *gat
 int bh_softmax_rows(const float *x, size_t x_len, size_t row_len,
                     float inv_temp, float *out, bh_stream stream);
 
+/* bh_softmax_rows with options.  flags = 0 is bh_softmax_rows;
+ * BH_SOFTMAX_SAMPLER_NORM normalises as the sampler does
+ * (src/sampler.rs:118-126: inv_sum = 1.0 / sum in f64, out =
+ * (e as f64 * inv_sum) as f32) instead of kernels::softmax_rows'
+ * e * (1 / (f32)sum) (src/kernels.rs:197-200); the two differ by at most
+ * two f32 ulps.  Unknown flags: BH_ERR_ARG. */
+#define BH_SOFTMAX_SAMPLER_NORM 1
+int bh_softmax_rows_ex(const float *x, size_t x_len, size_t row_len,
+                       float inv_temp, int flags, float *out, bh_stream stream);
+
 /* No counterpart in the reference: bh_softmax_rows for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments, kernels and results as

@@ -170,6 +170,14 @@ int or_l2_norm_rows(const float *x, size_t x_len, size_t row_len, float eps, flo
 /* ---- softmax (src/kernels.rs:175-202) ---------------------------------- */
 
 int or_softmax_rows(const float *x, size_t x_len, size_t row_len, float inv_temp, float *out) {
+  return or_softmax_rows_ex(x, x_len, row_len, inv_temp, 0, out);
+}
+
+/* flags & 1: the sampler's normalisation (src/sampler.rs:118-126): the sum
+ * is the same f64 sum of the f32 exponentials, then inv_sum = 1.0 / sum in
+ * f64 and each output is (e as f64 * inv_sum) as f32. */
+int or_softmax_rows_ex(const float *x, size_t x_len, size_t row_len, float inv_temp, int flags,
+                       float *out) {
   if (row_len == 0 || x_len % row_len != 0) return OR_ERR_SHAPE;
   float *y = (float *)malloc(row_len * sizeof(float));
   if (y == NULL) return OR_ERR_SHAPE;
@@ -187,8 +195,13 @@ int or_softmax_rows(const float *x, size_t x_len, size_t row_len, float inv_temp
       dst[i] = e;
       sum += (double)e;
     }
-    float inv = 1.0f / (float)sum;
-    for (size_t i = 0; i < row_len; ++i) dst[i] *= inv;
+    if (flags & 1) {
+      double inv_sum = 1.0 / sum;
+      for (size_t i = 0; i < row_len; ++i) dst[i] = (float)((double)dst[i] * inv_sum);
+    } else {
+      float inv = 1.0f / (float)sum;
+      for (size_t i = 0; i < row_len; ++i) dst[i] *= inv;
+    }
   }
   free(y);
   return OR_OK;

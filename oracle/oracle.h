@@ -52,6 +52,10 @@ int or_add_rms_norm_rows(const float *x, const float *r, size_t x_len, const flo
 int or_l2_norm_rows(const float *x, size_t x_len, size_t row_len, float eps, float *out);
 /* src/kernels.rs:175-202 applied to x * inv_temp (src/sampler.rs:85, 110) */
 int or_softmax_rows(const float *x, size_t x_len, size_t row_len, float inv_temp, float *out);
+/* flags & 1: the sampler's normalisation, (e as f64 * (1.0 / sum)) as f32
+ * (src/sampler.rs:118-126) */
+int or_softmax_rows_ex(const float *x, size_t x_len, size_t row_len, float inv_temp, int flags,
+                       float *out);
 
 /* src/rope.rs:9-70, in place on one head */
 void or_rope_imrope(float *head, size_t head_len, int64_t p_t, int64_t p_h, int64_t p_w,

@@ -36,6 +36,7 @@ _SIG = {
     "or_add_rms_norm_rows": (ctypes.c_int, [_vp, _vp, _sz, _vp, _sz, _sz, _f, _vp, _vp]),
     "or_l2_norm_rows": (ctypes.c_int, [_vp, _sz, _sz, _f, _vp]),
     "or_softmax_rows": (ctypes.c_int, [_vp, _sz, _sz, _f, _vp]),
+    "or_softmax_rows_ex": (ctypes.c_int, [_vp, _sz, _sz, _f, ctypes.c_int, _vp]),
     "or_rope_imrope": (None, [_vp, _sz, _i64, _i64, _i64, _i64, _sz, _i32p, _f]),
     "or_qk_norm_rope": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz,
                                        _sz, _sz, _sz, _i32p, _f, _f]),
@@ -157,10 +158,14 @@ def l2_norm_rows(x, row_len: int, eps: float) -> np.ndarray:
     return out
 
 
-def softmax_rows(x, row_len: int, inv_temp: float = 1.0) -> np.ndarray:
+def softmax_rows(x, row_len: int, inv_temp: float = 1.0, sampler_norm: bool = False) -> np.ndarray:
     x = _c(x)
     out = np.empty_like(x)
-    _st(lib().or_softmax_rows(_p(x), x.size, row_len, inv_temp, _p(out)), "softmax_rows shape")
+    if sampler_norm:
+        _st(lib().or_softmax_rows_ex(_p(x), x.size, row_len, inv_temp, 1, _p(out)),
+            "softmax_rows shape")
+    else:
+        _st(lib().or_softmax_rows(_p(x), x.size, row_len, inv_temp, _p(out)), "softmax_rows shape")
     return out
 
 

@@ -59,6 +59,9 @@ extern "C" {
     pub fn bh_gdn_prep_fused(args: *const GdnPrepArgs, stream: Stream) -> c_int;
     pub fn bh_softmax_rows(x: *const f32, x_len: usize, row_len: usize, inv_temp: f32,
                            out: *mut f32, stream: Stream) -> c_int;
+    // with flags: BH_SOFTMAX_SAMPLER_NORM = 1 normalises as src/sampler.rs:118-126
+    pub fn bh_softmax_rows_ex(x: *const f32, x_len: usize, row_len: usize, inv_temp: f32,
+                              flags: c_int, out: *mut f32, stream: Stream) -> c_int;
     // the same, allocating nothing (fixed library scratch; for graph capture)
     pub fn bh_softmax_rows_noalloc(x: *const f32, x_len: usize, row_len: usize, inv_temp: f32,
                                    out: *mut f32, stream: Stream) -> c_int;

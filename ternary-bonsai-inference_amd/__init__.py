@@ -35,6 +35,8 @@ BH_SOFTPLUS = 2
 BH_SILU_MUL = 3
 BH_SIGMOID_MUL = 4
 
+BH_SOFTMAX_SAMPLER_NORM = 1  # bh_softmax_rows_ex flag
+
 # Ternary-Bonsai-27B constants (reference src/gdev.rs:21-37, src/weights.rs:42-62)
 N_EMBD = 5120
 N_HEAD = 24
@@ -103,6 +105,7 @@ _SIGNATURES = {
     "bh_gdn_prep_fused": (_c_int, [ctypes.POINTER(GdnPrepArgs), _vp]),
     "bh_softmax_rows": (_c_int, [_vp, _c_size, _c_size, _c_float, _vp, _vp]),
     "bh_softmax_rows_noalloc": (_c_int, [_vp, _c_size, _c_size, _c_float, _vp, _vp]),
+    "bh_softmax_rows_ex": (_c_int, [_vp, _c_size, _c_size, _c_float, _c_int, _vp, _vp]),
     "bh_rope_imrope": (_c_int, [_vp, _c_size, _c_size, _c_size, _vp, _c_size,
                                 ctypes.POINTER(ctypes.c_int32), _c_float, _vp]),
     "bh_qk_norm_rope": (_c_int, [ctypes.POINTER(QkNormRopeArgs), _vp]),
@@ -241,12 +244,20 @@ def unary(mode: int, a, b=None, out=None, stream=None):
 
 
 def softmax_rows(x, row_len: int, inv_temp: float = 1.0, out=None, stream=None,
-                 noalloc: bool = False):
-    """bh_softmax_rows, or with noalloc=True bh_softmax_rows_noalloc (fixed
-    library scratch, no device allocation by the library)."""
+                 noalloc: bool = False, sampler_norm: bool = False):
+    """bh_softmax_rows; with noalloc=True bh_softmax_rows_noalloc (fixed
+    library scratch, no device allocation by the library); with
+    sampler_norm=True bh_softmax_rows_ex(BH_SOFTMAX_SAMPLER_NORM), the
+    sampler's f64 normalisation (src/sampler.rs:118-126)."""
     import torch
     _f32(x, "x")
+    if noalloc and sampler_norm:
+        raise ValueError("softmax_rows: noalloc has no sampler normalisation")
     out = torch.empty_like(x) if out is None else out
+    if sampler_norm:
+        check(lib().bh_softmax_rows_ex(x.data_ptr(), x.numel(), row_len, inv_temp,
+                                       BH_SOFTMAX_SAMPLER_NORM, out.data_ptr(), _stream(stream)))
+        return out
     fn = lib().bh_softmax_rows_noalloc if noalloc else lib().bh_softmax_rows
     check(fn(x.data_ptr(), x.numel(), row_len, inv_temp, out.data_ptr(), _stream(stream)))
     return out

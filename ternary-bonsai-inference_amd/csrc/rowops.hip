@@ -328,10 +328,21 @@ __global__ __launch_bounds__(kBlock) void l2_rows_loop_kernel(const float *x, fl
 // Softmax rows
 // ---------------------------------------------------------------------------
 
+// (f32)((f64)e * inv) per element: the sampler's normalisation
+__device__ __forceinline__ float sampler_norm(float e, double inv) {
+  return static_cast<float>(static_cast<double>(e) * inv);
+}
+__device__ __forceinline__ float4 sampler_norm4(float4 e, double inv) {
+  return make_float4(sampler_norm(e.x, inv), sampler_norm(e.y, inv), sampler_norm(e.z, inv),
+                     sampler_norm(e.w, inv));
+}
+
 // y = x * inv_t; m = max(y) (NaN never becomes the max, as `if v > max`);
 // e = expf(y - m); s = sum_f64(e); out = e * (1 / (f32)s)
-// (src/kernels.rs:184-200).  -inf entries give expf(-inf) = 0.
-template <int G, int VPT>
+// (src/kernels.rs:184-200).  -inf entries give expf(-inf) = 0.  With SN
+// (the sampler's normalisation, src/sampler.rs:118-126) out is instead
+// (f32)((f64)e * (1 / s)), the division and the product in f64.
+template <int G, int VPT, bool SN>
 __global__ __launch_bounds__(1024) void softmax_rows_kernel(const float *x, float *out, size_t rows,
                                                             int row_len, float inv_t) {
   __shared__ float lds_m[kMaxWaves];
@@ -385,13 +396,22 @@ __global__ __launch_bounds__(1024) void softmax_rows_kernel(const float *x, floa
     }
   }
   s = row_reduce<G>(s, SumOp{}, lds_s);
-  const float inv = 1.0f / static_cast<float>(s);
   float4 *o4 = reinterpret_cast<float4 *>(out) + off;
+  if constexpr (SN) {
+    const double inv = 1.0 / s;
 #pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int c = L.gl + i * L.stride;
-    if (L.live && c < r4) {
-      store_stream(o4 + c, make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv));
+    for (int i = 0; i < VPT; ++i) {
+      const int c = L.gl + i * L.stride;
+      if (L.live && c < r4) store_stream(o4 + c, sampler_norm4(v[i], inv));
+    }
+  } else {
+    const float inv = 1.0f / static_cast<float>(s);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int c = L.gl + i * L.stride;
+      if (L.live && c < r4) {
+        store_stream(o4 + c, make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv));
+      }
     }
   }
 }
@@ -506,10 +526,12 @@ __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float
 // then each lane writes e^(y - M) * (1 / (f32)S), the reference's output
 // formula (the exponential by exp_hw), for its kSplitWV float4.
 constexpr int kSplitWV = 4;  // measured: 17.6 us vs 20.2 (2) and 21.3 (8) on [64, 248320]
+template <bool SN>
 __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float4 *x, float4 *out,
                                                                      size_t r4, float inv_t,
                                                                      SplitScratch sc, int nch) {
   __shared__ float2 stat;
+  __shared__ double stat_inv;  // 1 / S in f64 (SN)
   const size_t r = blockIdx.y;
   const size_t c0 = static_cast<size_t>(blockIdx.x) * (kBlock * kSplitWV) + threadIdx.x;
   float4 v[kSplitWV];
@@ -528,24 +550,30 @@ __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float
     double S = 0.0;
     for (int i = threadIdx.x; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
     S = lane_group_reduce<64>(S, SumOp{});
-    if (threadIdx.x == 0) stat = make_float2(M, 1.0f / static_cast<float>(S));
+    if (threadIdx.x == 0) {
+      stat = make_float2(M, 1.0f / static_cast<float>(S));
+      if constexpr (SN) stat_inv = 1.0 / S;
+    }
   }
   __syncthreads();
   const float2 st = stat;
 #pragma unroll
   for (int i = 0; i < kSplitWV; ++i) {
     const size_t c = c0 + static_cast<size_t>(i) * kBlock;
-    if (c < r4)
-      store_stream(out + r * r4 + c,
-                   make_float4(exp_hw(v[i].x * inv_t - st.x) * st.y,
-                               exp_hw(v[i].y * inv_t - st.x) * st.y,
-                               exp_hw(v[i].z * inv_t - st.x) * st.y,
-                               exp_hw(v[i].w * inv_t - st.x) * st.y));
+    if (c < r4) {
+      const float4 e = make_float4(exp_hw(v[i].x * inv_t - st.x), exp_hw(v[i].y * inv_t - st.x),
+                                   exp_hw(v[i].z * inv_t - st.x), exp_hw(v[i].w * inv_t - st.x));
+      if constexpr (SN)
+        store_stream(out + r * r4 + c, sampler_norm4(e, stat_inv));
+      else
+        store_stream(out + r * r4 + c, make_float4(e.x * st.y, e.y * st.y, e.z * st.y, e.w * st.y));
+    }
   }
 }
 
 // Looped fallback for rows whose length is not a multiple of 4 or whose
 // pointers are unaligned: one block per row, three sweeps (max, sum, write).
+template <bool SN>
 __global__ __launch_bounds__(kBlock) void softmax_loop_kernel(const float *x, float *out,
                                                               size_t row_len, float inv_t) {
   __shared__ float lm[kBlock / 64];
@@ -561,8 +589,12 @@ __global__ __launch_bounds__(kBlock) void softmax_loop_kernel(const float *x, fl
     s += static_cast<double>(expf(xr[c] * inv_t - m));
   s = group_reduce<kBlock>(s, SumOp{}, ls);
   const float inv = 1.0f / static_cast<float>(s);
+  const double inv_d = 1.0 / s;
   // each element is read by the lane that writes it: in place is safe
-  for (size_t c = threadIdx.x; c < row_len; c += kBlock) orow[c] = expf(xr[c] * inv_t - m) * inv;
+  for (size_t c = threadIdx.x; c < row_len; c += kBlock) {
+    const float e = expf(xr[c] * inv_t - m);
+    orow[c] = SN ? sampler_norm(e, inv_d) : e * inv;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -672,6 +704,7 @@ char *noalloc_scratch() {
 // Wide-row softmax: stats pass then write pass.  `fixed` (with `fixed_cap`
 // bytes) is the no-allocation entry point's scratch; nullptr takes the
 // library's growable per-device buffer.
+template <bool SN>
 int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float inv_t,
                   hipStream_t st, char *fixed, size_t fixed_cap) {
   if (rows > kMaxSplitRows)
@@ -679,7 +712,7 @@ int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float
   const bool vec = (row_len % 4 == 0) && aligned16(x) && aligned16(out);
   if (!vec) {
     if (rows > 0x7fffffffu) return fail(BH_ERR_SHAPE, "softmax_rows: too many rows");
-    BH_LAUNCH(softmax_loop_kernel, static_cast<unsigned>(rows), kBlock, 0, st, x, out, row_len,
+    BH_LAUNCH(softmax_loop_kernel<SN>, static_cast<unsigned>(rows), kBlock, 0, st, x, out, row_len,
               inv_t);
     return ok();
   }
@@ -710,7 +743,7 @@ int softmax_split(const float *x, float *out, size_t rows, size_t row_len, float
             kBlock, 0, st, x4, r4, inv_t, sc);
   const size_t wblocks = (r4 + kBlock * kSplitWV - 1) / (kBlock * kSplitWV);
   if (wblocks > 0x7fffffffu) return fail(BH_ERR_SHAPE, "softmax_rows: row too long");
-  BH_LAUNCH(softmax_split_write_kernel,
+  BH_LAUNCH(softmax_split_write_kernel<SN>,
             dim3(static_cast<unsigned>(wblocks), static_cast<unsigned>(rows)), kBlock, 0, st, x4,
             reinterpret_cast<float4 *>(out), r4, inv_t, sc, static_cast<int>(nch));
   return ok();
@@ -780,6 +813,7 @@ extern "C" int bh_silu_l2_norm_rows(const float *x, size_t x_len, size_t row_len
 
 namespace bh {
 namespace {
+template <bool SN>
 int softmax_impl(const float *x, size_t x_len, size_t row_len, float inv_temp, float *out,
                  hipStream_t st, bool noalloc) {
   const char *name = noalloc ? "softmax_rows_noalloc" : "softmax_rows";
@@ -798,7 +832,7 @@ int softmax_impl(const float *x, size_t x_len, size_t row_len, float inv_temp, f
       constexpr int V_ = decltype(VC)::value;
       unsigned grid, block;
       if (int e = launch_grid(g, rows, &grid, &block)) return e;
-      BH_LAUNCH((softmax_rows_kernel<G_, V_>), grid, block, 0, st, x, out, rows,
+      BH_LAUNCH((softmax_rows_kernel<G_, V_, SN>), grid, block, 0, st, x, out, rows,
                 static_cast<int>(row_len), inv_temp);
       return ok();
     });
@@ -811,17 +845,26 @@ int softmax_impl(const float *x, size_t x_len, size_t row_len, float inv_temp, f
     fixed = noalloc_scratch();
     if (fixed == nullptr) return BH_ERR_HIP;
   }
-  return softmax_split(x, out, rows, row_len, inv_temp, st, fixed, kNoAllocScratchBytes);
+  return softmax_split<SN>(x, out, rows, row_len, inv_temp, st, fixed, kNoAllocScratchBytes);
 }
 }  // namespace
 }  // namespace bh
 
 extern "C" int bh_softmax_rows(const float *x, size_t x_len, size_t row_len, float inv_temp,
                                float *out, bh_stream stream) {
-  return softmax_impl(x, x_len, row_len, inv_temp, out, as_stream(stream), false);
+  return softmax_impl<false>(x, x_len, row_len, inv_temp, out, as_stream(stream), false);
+}
+
+extern "C" int bh_softmax_rows_ex(const float *x, size_t x_len, size_t row_len, float inv_temp,
+                                  int flags, float *out, bh_stream stream) {
+  if ((flags & ~BH_SOFTMAX_SAMPLER_NORM) != 0)
+    return fail(BH_ERR_ARG, "softmax_rows_ex: unknown flags " + std::to_string(flags));
+  if (flags & BH_SOFTMAX_SAMPLER_NORM)
+    return softmax_impl<true>(x, x_len, row_len, inv_temp, out, as_stream(stream), false);
+  return softmax_impl<false>(x, x_len, row_len, inv_temp, out, as_stream(stream), false);
 }
 
 extern "C" int bh_softmax_rows_noalloc(const float *x, size_t x_len, size_t row_len,
                                        float inv_temp, float *out, bh_stream stream) {
-  return softmax_impl(x, x_len, row_len, inv_temp, out, as_stream(stream), true);
+  return softmax_impl<false>(x, x_len, row_len, inv_temp, out, as_stream(stream), true);
 }

@@ -314,6 +314,47 @@ def test_softmax_shift_invariance_and_temperature(oracle):
     assert np.all(np.abs(t.reshape(4, 1024).sum(1) - 1) < 1e-5)
 
 
+def _ulps(a, b):
+    """Distance in f32 ulps of same-sign finite values."""
+    ia = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    ib = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ia - ib)
+
+
+def test_softmax_sampler_norm_is_the_f64_formula(oracle):
+    """src/sampler.rs:108-126: y = logits * inv_t (f32), max, e = exp(y - max)
+    (f32, the C library's expf here as Rust's f32::exp), sum += e as f64,
+    inv_sum = 1.0 / sum, p = (e as f64 * inv_sum) as f32.  Restated with
+    numpy's f64 arithmetic: bit for bit, so a dropped f64 step, an f32
+    reciprocal or a wrong sum shows."""
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    r = np.random.default_rng(12)
+    for row_len, inv_t in ((37, 1.0), (1000, 1.0 / 0.7), (4096, 2.5)):
+        x = (r.standard_normal(3 * row_len) * 3).astype(np.float32)
+        inv_t = np.float32(inv_t)
+        got = oracle.softmax_rows(x, row_len, inv_t, sampler_norm=True)
+        for k in range(3):
+            y = x[k * row_len:(k + 1) * row_len] * inv_t
+            m = y.max()
+            e = np.array([libm.expf(float(v)) for v in (y - m)], np.float32)
+            total = 0.0
+            for v in e:  # the reference's sequential f64 sum
+                total += float(v)
+            want = (e.astype(np.float64) * (1.0 / total)).astype(np.float32)
+            assert np.array_equal(got[k * row_len:(k + 1) * row_len], want)
+            # the f32 reciprocal of kernels::softmax_rows differs somewhere
+            plain = (e * (np.float32(1.0) / np.float32(total))).astype(np.float32)
+            assert not np.array_equal(plain, want) or row_len < 100
+        # the plain normalisation of the same exponentials is within 2 ulps
+        plain = oracle.softmax_rows(x, row_len, inv_t)
+        assert _ulps(plain, got).max() <= 2
+        assert abs(got.reshape(3, -1).astype(np.float64).sum(1) - 1).max() < 1e-6
+
+
 def test_softmax_all_masked_row_is_nan(oracle):
     """An all -inf row gives NaN (exp(-inf - -inf)), as the reference does."""
     y = oracle.softmax_rows(np.full(8, -np.inf, np.float32), 8)

@@ -277,6 +277,27 @@ def test_softmax_shapes(bh, oracle, synth, dev, rows, row_len):
     assert rel_err(got, ref) <= TOL_SOFTMAX
 
 
+@pytest.mark.parametrize("rows,row_len", [(64, 248320), (96, 1000), (5, 1001)])
+def test_softmax_sampler_norm(bh, oracle, synth, dev, rows, row_len):
+    """bh_softmax_rows_ex(BH_SOFTMAX_SAMPLER_NORM): the sampler's f64
+    normalisation (src/sampler.rs:118-126) on the split path (vocabulary
+    rows), the register path and the looped path (odd row length); within
+    2 ulps of the plain normalisation of the same exponentials."""
+    x = synth.Rng(rows + row_len).normal(rows * row_len, 0.0, 3.0)
+    inv_t = np.float32(1.0) / np.float32(0.7)
+    ref = oracle.softmax_rows(x, row_len, inv_t, sampler_norm=True)
+    xt = _t(x, dev)
+    got = _h(bh.softmax_rows(xt, row_len, inv_t, sampler_norm=True))
+    _say("softmax sampler norm", rows, row_len, "rel", rel_err(got, ref))
+    assert rel_err(got, ref) <= TOL_SOFTMAX
+    plain = _h(bh.softmax_rows(xt, row_len, inv_t))
+    d = np.abs(got.view(np.int32).astype(np.int64) - plain.view(np.int32).astype(np.int64))
+    assert d.max() <= 2
+    lib = bh.lib()
+    assert lib.bh_softmax_rows_ex(xt.data_ptr(), xt.numel(), row_len, 1.0, 2,
+                                  xt.data_ptr(), None) == bh.BH_ERR_ARG
+
+
 def test_softmax_mask_safe_and_nan_rows(bh, dev):
     """src/kernels.rs:840-853, plus an all -inf row (NaN, as the reference)."""
     x = np.array([1, 2, 3, -np.inf, 0, 0, 0, 0, -np.inf, -np.inf, -np.inf, -np.inf], np.float32)
