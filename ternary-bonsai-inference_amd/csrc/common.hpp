@@ -57,6 +57,9 @@ constexpr int kScratchSlots = 3;
 void *device_scratch(size_t bytes, int slot, hipStream_t stream);
 // Current size of this device's buffer for `slot` (0 before the first use).
 size_t scratch_bytes(int slot);
+// Compute units of the current device (queried once per device; 256 if the
+// query fails).
+size_t device_cu_count();
 
 // a * b (* c), or false when the product does not fit in size_t.
 inline bool mul_size(size_t a, size_t b, size_t *out) { return !__builtin_mul_overflow(a, b, out); }

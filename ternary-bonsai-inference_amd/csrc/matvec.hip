@@ -1160,20 +1160,6 @@ int launch_i8(const MmI8Args &a, size_t lds_a, hipStream_t st) {
   return ok();
 }
 
-// Compute units of the current device (cached per device).
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 // The integer product for n_tok <= kI8Tok on staged shapes.  Every
 // workgroup turns x into its digit fragments in LDS while its first weight
 // chunks load: no prepare launch, no scratch (ffn_up N=1: 20.3 -> 14.9 us
@@ -1199,7 +1185,7 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
     // is one round over the CUs instead of two (ffn_down N=1, 320 row tiles:
     // 13.7 us, against 20.2 with 8 waves and 14.8 with 4 waves per tile)
     if (n_chunks >= 8 && 2 * (a_bytes + 8 * kStageWaveBytes) > 160 * 1024 &&
-        tiles <= 2 * static_cast<size_t>(cu_count()) && a_bytes + 16 * kStageWaveBytes <= 160 * 1024)
+        tiles <= 2 * device_cu_count() && a_bytes + 16 * kStageWaveBytes <= 160 * 1024)
       return launch_i8<8, 2>(a, lds, st);
     // the most waves per row tile whose grid still runs in one round: a
     // workgroup is 8 waves (8 / ks row tiles), as many per CU as LDS and the
@@ -1207,7 +1193,7 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
     // 512 slots, a 32-workgroup second round)
     const size_t wg_lds = a_bytes + 8 * kStageWaveBytes;
     const size_t per_cu = std::min<size_t>(4, (160 * 1024) / wg_lds);
-    const size_t slots = per_cu * static_cast<size_t>(cu_count());
+    const size_t slots = per_cu * device_cu_count();
     // (a wave count past the chunk count still pays when it shortens the
     // longest chain: 5 chunks over 8 waves are one round trip, over 4 two)
     for (int k = 8; k >= 1; k >>= 1) {
@@ -1230,7 +1216,7 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   const size_t plds = a_bytes + kPRT * kStageWaveBytes;
   const size_t per_cu = std::max<size_t>(1, std::min<size_t>(4, (160 * 1024) / plds));
   const size_t groups = (tiles + kPRT - 1) / kPRT;
-  const size_t G = std::min(groups, per_cu * static_cast<size_t>(cu_count()));
+  const size_t G = std::min(groups, per_cu * device_cu_count());
   if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_persist_kernel<kPRT>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(plds)),

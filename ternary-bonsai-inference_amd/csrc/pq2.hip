@@ -21,8 +21,8 @@
 // one after another in f32 (src/kernels.rs:65-68); on quantised embedding
 // rows that sequence drifts ~1e-5 from any tree-ordered sum, so the fused
 // kernel reproduces the sequence itself.  A block owns kFusedRows rows: its
-// rows are staged in LDS, "producer" waves decode them chunk by chunk (128
-// columns), store the embedding rows and write the f32 squares to an LDS
+// rows are staged in LDS, "producer" waves decode them chunk by chunk (256
+// or 512 columns), store the embedding rows and write the f32 squares to an LDS
 // ring laid out column-major, while one "chain" wave adds them in column
 // order, one row per lane -- the same additions in the same order as the
 // CPU, so the norm output is bit-identical too.  The chain (5120 dependent
@@ -45,6 +45,7 @@ constexpr int kBlock = 256;
 constexpr int kPq2Block = 34;
 constexpr size_t kMaxSeqSmem = 128 * 1024;  // LDS cap of a fused block (gfx950: 160 KB per CU)
 
+
 // Decodes float4 number f (weights 4f..4f+3 of the row) from the staged row.
 __device__ __forceinline__ float4 decode4(const uint8_t *rowb, int f) {
   const int b = f >> 5;  // 32 float4 per 128-weight block
@@ -63,16 +64,15 @@ __device__ __forceinline__ float4 decode4(const uint8_t *rowb, int f) {
 // Fused gather + RMSNorm with the reference's sequential f32 sum of squares:
 // one launch, one block of kFusedThreads lanes per kFusedRows output rows.
 // ---------------------------------------------------------------------------
-constexpr int kFusedRows = 16;             // rows per block = chain lanes
-constexpr int kFusedThreads = 1024;        // wave 0: chain, waves 1..15: producers
-constexpr int kChunkQ = 32;                // float4 columns per chunk (128 weights)
-constexpr int kRingStride = kFusedRows + 1;  // float4 slots per column (padded)
+// Block shapes: kFusedRows rows per block (= chain lanes), kFusedThreads
+// lanes (wave 0 the chain, the others producers) and kChunkQ float4 columns
+// per chunk of the ring (one barrier per chunk).
 
-// LDS of a block: staged packed rows, the f32 scale of every (row, 128-block)
-// and the two-chunk ring of squared weights.
-size_t fused_smem_bytes(size_t row_bytes) {
-  const size_t n_scales = (kFusedRows * (row_bytes / kPq2Block) + 3) & ~static_cast<size_t>(3);
-  return kFusedRows * row_bytes + n_scales * sizeof(float) + 2 * kChunkQ * kRingStride * sizeof(float4);
+// LDS of a block of `rows` rows: staged packed rows, the f32 scale of every
+// (row, 128-block) and the two-chunk ring of squared weights.
+size_t fused_smem_bytes(size_t row_bytes, int rows, int chunk_q) {
+  const size_t n_scales = (rows * (row_bytes / kPq2Block) + 3) & ~static_cast<size_t>(3);
+  return rows * row_bytes + n_scales * sizeof(float) + 2 * chunk_q * (rows + 1) * sizeof(float4);
 }
 
 struct GatherArgs {
@@ -87,7 +87,7 @@ struct GatherArgs {
   float eps;
 };
 
-// Phase 1 (column chunks of 128 weights, ring of squares):
+// Phase 1 (column chunks of 4 kChunkQ weights, ring of squares):
 //   producer waves decode chunk c of all the block's rows, store those
 //   embedding float4 and write their f32 squares to the ring, column-major;
 //   the chain wave (lane = row) adds chunk c-1 in column order -- the same
@@ -96,7 +96,9 @@ struct GatherArgs {
 //   per dependent add, ~21 us for 5120 weights) and runs under the stores.
 // Phase 2: all waves decode the rows again from LDS and store the norm rows
 //   (v * scale) * w (src/kernels.rs:71-73), flat over the block's rows.
+template <int kFusedRows, int kFusedThreads, int kChunkQ>
 __global__ __launch_bounds__(kFusedThreads) void pq2_gather_rms_kernel(GatherArgs a) {
+  constexpr int kRingStride = kFusedRows + 1;  // float4 slots per column (padded)
   extern __shared__ uint4 smem[];
   __shared__ int row_ok[kFusedRows];
   __shared__ float row_scale[kFusedRows];
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(kFusedThreads) void pq2_gather_rms_kernel(GatherArg
       if (c < n_chunks) {
         float4 *dst = ring + (c & 1) * (kChunkQ * kRingStride);
         for (int i = tid - 64; i < kFusedRows * kChunkQ; i += kFusedThreads - 64) {
-          const int r = i / kChunkQ;  // lanes walk a row's 32 columns: 512-byte store runs
+          const int r = i / kChunkQ;  // lanes walk a row's kChunkQ columns: long store runs
           const int q = i - r * kChunkQ;
           const int f = c * kChunkQ + q;
           float4 t = make_float4(0.f, 0.f, 0.f, 0.f);  // adding +0 leaves a sum unchanged
@@ -319,15 +321,31 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
     BH_LAUNCH(pq2_rows_write_kernel, wgrid, 256, 0, st, ga);
     return ok();
   }
-  if (rows_ok && norm && row_bytes % 16 == 0 && fused_smem_bytes(row_bytes) <= kMaxSeqSmem) {
-    const size_t smem = fused_smem_bytes(row_bytes);
-    if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_gather_rms_kernel),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                                              static_cast<int>(smem)),
-                          "hipFuncSetAttribute"))
-      return e;
-    const unsigned fgrid = static_cast<unsigned>((n_ids + kFusedRows - 1) / kFusedRows);
-    BH_LAUNCH(pq2_gather_rms_kernel, fgrid, kFusedThreads, smem, st, ga);
+  if (rows_ok && norm && row_bytes % 16 == 0 && fused_smem_bytes(row_bytes, 16, 128) <= kMaxSeqSmem) {
+    // 16 rows per block while that still gives every CU a block; fewer rows
+    // per block (more blocks) for short batches: the chain's latency is the
+    // same for any number of rows, the rest of a block's work is not.
+    // Measured (us, T=2048 / 8192, chunks of 32 float4): 16 rows x 1024
+    // lanes 39.0 / 70.3, 8 x 1024 34.6 / 81, 8 x 512 37.0 / 70.7, 4 x 512
+    // 35.1 / 85, 4 x 256 38.6 / 69.  Longer chunks (fewer barriers on the
+    // chain's path): 8 rows, chunks of 64 / 128 float4 33.3 / 32.7 at
+    // T=2048; 16 rows, 64: 70.2 at T=8192 (128: 80.5).
+    const size_t cus = device_cu_count();
+    const int rows = n_ids >= 16 * cus ? 16 : (n_ids >= 8 * cus ? 8 : 4);
+    auto launch = [&](auto kern, int r, int threads, int chunk_q) -> int {
+      const size_t smem = fused_smem_bytes(row_bytes, r, chunk_q);
+      if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                static_cast<int>(smem)),
+                            "hipFuncSetAttribute"))
+        return e;
+      const unsigned fgrid = static_cast<unsigned>((n_ids + r - 1) / r);
+      BH_LAUNCH(kern, fgrid, threads, smem, st, ga);
+      return ok();
+    };
+    if (rows == 16) return launch(pq2_gather_rms_kernel<16, 1024, 64>, 16, 1024, 64);
+    if (rows == 8) return launch(pq2_gather_rms_kernel<8, 1024, 128>, 8, 1024, 128);
+    return launch(pq2_gather_rms_kernel<4, 512, 128>, 4, 512, 128);
   } else {
     if (norm) {
       BH_LAUNCH((pq2_gather_loop_kernel<true>), grid, kBlock, 0, st, table, row_bytes,

@@ -5,6 +5,7 @@
 // thread-local string readable through bh_last_error().
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -87,6 +88,19 @@ size_t scratch_bytes(int slot) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   const size_t idx = static_cast<size_t>(dev) * kScratchSlots + slot;
   return idx < g_scratch.size() ? g_scratch[idx].bytes : 0;
+}
+
+size_t device_cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return static_cast<size_t>(n);
 }
 
 }  // namespace bh
