@@ -555,13 +555,6 @@ constexpr int kI8Tok = 4;  // tokens per MFMA (A rows 4t .. 4t + 3)
 typedef int i4v __attribute__((ext_vector_type(4)));
 
 
-// The 16 x values (4 float4) of a lane's item: block columns 16 sub .. +15.
-__device__ __forceinline__ void i8_load_item(const float *xb, int sub, bool live, float4 v[4]) {
-  const float4 *xr = reinterpret_cast<const float4 *>(xb + 16 * sub);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) v[q] = live ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
-}
-
 // The digit fragments of one (token, 128-block): its 8 lanes (sub = 2g + h)
 // each build the three 16-byte fragments (digits d0, d1, d2) of step 2 blk + h
 // for lane group g, block columns 16 (2g + h) .. +15, from xb = x + t * ne0 +
@@ -569,15 +562,18 @@ __device__ __forceinline__ void i8_load_item(const float *xb, int sub, bool live
 // 2^-e; NaN when the block holds a NaN or infinity).  Contains cross-lane
 // steps inside each 8-lane group: all lanes of the wave must call it
 // (dead items with live = false).
-__device__ __forceinline__ void i8_prep_vals(const float4 v[4], bool live, uint4 frag[3],
+__device__ __forceinline__ void i8_prep_item(const float *xb, int sub, bool live, uint4 frag[3],
                                              float2 &fac) {
+  const int g = sub >> 1, h = sub & 1;
+  const float4 *xr = reinterpret_cast<const float4 *>(xb + 16 * (2 * g + h));
   float f[16];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    f[4 * q] = live ? v[q].x : 0.0f;
-    f[4 * q + 1] = live ? v[q].y : 0.0f;
-    f[4 * q + 2] = live ? v[q].z : 0.0f;
-    f[4 * q + 3] = live ? v[q].w : 0.0f;
+    const float4 v = live ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    f[4 * q] = v.x;
+    f[4 * q + 1] = v.y;
+    f[4 * q + 2] = v.z;
+    f[4 * q + 3] = v.w;
   }
   float mx = 0.0f;
   int bad = 0;  // a NaN or infinity in the block
@@ -623,13 +619,6 @@ __device__ __forceinline__ void i8_prep_vals(const float4 v[4], bool live, uint4
   fac = make_float2(__int_as_float(sx), bad ? __builtin_nanf("") : ldexpf(1.0f, -ex));
 }
 
-__device__ __forceinline__ void i8_prep_item(const float *xb, int sub, bool live, uint4 frag[3],
-                                             float2 &fac) {
-  float4 v[4];
-  i8_load_item(xb, sub, live, v);
-  i8_prep_vals(v, live, frag, fac);
-}
-
 struct MmI8Args {
   const uint8_t *w;     // first row of the range
   const float *x;       // [n_tok][ne0], n_tok <= kI8Tok
@@ -646,39 +635,19 @@ __device__ __forceinline__ i4v decode_i8(uint32_t d) {
 // x digits of every (token, block) into LDS, by all `lanes` lanes of the
 // workgroup: uint4 (step * 4 + g) * arows + 4 t + digit, block factors at
 // bf[blk * kI8Tok + t].  The trip count is the same for every wave (the
-// prep has cross-lane steps).  The first pass's x values come in `v0`
-// (i8_stage_x_first), loaded before the caller's first weight chunk: loads
-// complete in issue order, so x loaded after the chunk would wait for it.
-__device__ __forceinline__ void i8_item_of(const MmI8Args &a, int item, int &t, int &blk, int &sub,
-                                           bool &live) {
-  const int n_items = a.n_tok * a.nblk * 8;
-  live = item < n_items;
-  const int tb = item >> 3;
-  sub = item & 7;
-  t = live ? tb / a.nblk : 0;
-  blk = live ? tb - t * a.nblk : 0;
-}
-__device__ __forceinline__ void i8_stage_x_first(const MmI8Args &a, float4 v0[4]) {
-  int t, blk, sub;
-  bool live;
-  i8_item_of(a, static_cast<int>(threadIdx.x), t, blk, sub, live);
-  i8_load_item(a.x + static_cast<size_t>(t) * (128 * a.nblk) + 128 * blk, sub, live, v0);
-}
+// prep has cross-lane steps).
 __device__ __forceinline__ void i8_stage_x(const MmI8Args &a, uint4 *smem, float2 *bf, int arows,
-                                           int lanes, const float4 v0[4]) {
+                                           int lanes) {
   const int n_items = a.n_tok * a.nblk * 8;
   for (int base = 0; base < n_items; base += lanes) {
-    int t, blk, sub;
-    bool live_item;
-    i8_item_of(a, base + static_cast<int>(threadIdx.x), t, blk, sub, live_item);
+    const int item = base + static_cast<int>(threadIdx.x);
+    const bool live_item = item < n_items;
+    const int tb = item >> 3, sub = item & 7;
+    const int t = live_item ? tb / a.nblk : 0, blk = live_item ? tb - t * a.nblk : 0;
     uint4 frag[3];
     float2 fac;
-    if (base == 0) {
-      i8_prep_vals(v0, live_item, frag, fac);
-    } else {
-      i8_prep_item(a.x + static_cast<size_t>(t) * (128 * a.nblk) + 128 * blk, sub, live_item, frag,
-                   fac);
-    }
+    i8_prep_item(a.x + static_cast<size_t>(t) * (128 * a.nblk) + 128 * blk, sub, live_item, frag,
+                 fac);
     if (live_item) {
       const int step = 2 * blk + (sub & 1), gg = sub >> 1;
       uint4 *dst = smem + (step * 4 + gg) * arows + 4 * t;
@@ -785,10 +754,8 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   float tot = 0.0f;
   const int n_chunks = a.nblk / kStageBlocks;
   int c = ks;
-  float4 xv0[4];
-  i8_stage_x_first(a, xv0);    // x first: the chunk's loads must not hold it up
   if (c < n_chunks) gload(c);  // the first weight chunk is in flight while x is staged
-  i8_stage_x(a, smem, bf, arows, 64 * kWaves, xv0);
+  i8_stage_x(a, smem, bf, arows, 64 * kWaves);
   __syncthreads();  // x staging visible to every wave
   if (c < n_chunks) {
     lstore();
@@ -887,10 +854,8 @@ __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
     }
   };
 
-  float4 xv0[4];
-  i8_stage_x_first(a, xv0);   // x first: the chunk's loads must not hold it up
   if (n_items > 0) gload(0);  // the first weight chunk is in flight while x is prepared
-  i8_stage_x(a, smem, bf, arows, 64 * RT, xv0);
+  i8_stage_x(a, smem, bf, arows, 64 * RT);
   __syncthreads();  // x staging visible to every wave
   if (n_items > 0) {
     lstore();
