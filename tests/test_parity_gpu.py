@@ -483,6 +483,27 @@ def test_pq2_gather_config5_bit_exact(bh, oracle, synth, dev):
     assert bits_equal(gn, ref_n)
 
 
+@pytest.mark.parametrize("n_ids", [2048, 2050, 4095, 1000, 17])
+def test_pq2_gather_rms_block_shapes(bh, oracle, synth, dev, n_ids):
+    """The fused gather + RMSNorm picks 16, 8 or 4 rows per block by batch
+    size (2048 and 4095 ids: 8-row blocks, 1000 and 17: 4-row blocks on a
+    256-CU device; 2050: a ragged last block): both outputs bit-exact."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(n_ids)
+    table = synth.torch_pq2_table(4096, 5120, dev, generator=g)
+    ids = (synth.Rng(n_ids).u64(n_ids) % np.uint64(4096)).astype(np.uint32)
+    w = synth.Rng(n_ids + 1).normal(5120, 1.0, 0.1)
+    idt = _t(ids, dev)
+    emb, nrm = bh.pq2_embed_gather(table, 5120, 4096, idt, w=_t(w, dev), eps=1e-6)
+    host_rows = _h(table[idt.long()])
+    ref_e, ref_n = oracle.embed_gather(host_rows, 5120, n_ids, np.arange(n_ids, dtype=np.uint32),
+                                       w, 1e-6)
+    _say("gather+rms block shapes", n_ids)
+    assert bits_equal(_h(emb), ref_e)
+    assert bits_equal(_h(nrm), ref_n)
+
+
 def test_pq2_gather_every_f16_scale(bh, oracle, synth, dev):
     """All 65536 f16 scale patterns x all 4 codes (NaN payloads, infinities,
     subnormals, -0.0 from code 1), bit-exact against the x86 reference."""
