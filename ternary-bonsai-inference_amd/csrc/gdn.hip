@@ -180,6 +180,8 @@ struct ChunkLds {
   float gb[2][kChunk];  // gate, beta as loaded
   float eg[kChunk];     // expf(gate)
   float kq[kChunk];     // k . q
+  float kk[kChunk];     // k_t . k_{t+1} (token pairs)
+  float kqn[kChunk];    // k_t . q_{t+1}
 };
 
 template <int ROWS, int VPT>
@@ -219,21 +221,32 @@ __device__ __forceinline__ void store_chunk(ChunkLds<ROWS> &l, const f32x4 (&rqk
 
 // Per-token constants of a staged chunk: 8 lanes per token sum 16 products
 // of k.q each, then an 8-lane DPP tree; lane 0 of the 8 also takes expf.
+// For the next token (within the chunk) the same lanes form k_t . k_{t+1}
+// and k_t . q_{t+1}, which a pair of tokens needs (see the step loop).
 template <int ROWS>
 __device__ __forceinline__ void chunk_constants(ChunkLds<ROWS> &l) {
   const int tid = threadIdx.x;
   const int t = tid / kDotLanes, part = tid % kDotLanes;
+  const int tn = t + 1 < kChunk ? t + 1 : t;
   const float4 *q = l.qk[t][0] + 4 * part;
   const float4 *k = l.qk[t][1] + 4 * part;
-  float s = 0.0f;
+  const float4 *qn = l.qk[tn][0] + 4 * part;
+  const float4 *kn = l.qk[tn][1] + 4 * part;
+  float s = 0.0f, skk = 0.0f, skq = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float4 a = q[i], b = k[i];
+    const float4 a = q[i], b = k[i], c = kn[i], d = qn[i];
     s += (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w);
+    skk += (b.x * c.x + b.y * c.y) + (b.z * c.z + b.w * c.w);
+    skq += (b.x * d.x + b.y * d.y) + (b.z * d.z + b.w * d.w);
   }
   s = row_sum<8>(s);
+  skk = row_sum<8>(skk);
+  skq = row_sum<8>(skq);
   if (part == 0) {
     l.kq[t] = s;
+    l.kk[t] = skk;
+    l.kqn[t] = skq;
     l.eg[t] = expf(l.gb[0][t]);
   }
 }
@@ -311,11 +324,56 @@ __global__ __launch_bounds__(kBlock) void gdn_step128_kernel(GdnStepArgs a) {
       const float out = fmaf(eg, dq, delta * kq) * a.scale;
       if (sub == 0) attn[static_cast<size_t>(t) * a.h_v * kFast] = out;
     };
-    // two tokens per pass: the state stays in the same registers
-    for (int t = 0; t < nt; t += 2) {
-      step(t);
-      if (t + 1 < nt) step(t + 1);
-    }
+    // two tokens from one state: all four row dots (k and q of both tokens)
+    // against the state before the pair, the second token's through
+    //   M' . x = eg (M . x) + delta (k . x)   (M' the state after the first)
+    // with k . k' and k . q' from the chunk constants, then one update
+    //   M'' = (eg eg') M + (eg' delta) k + delta' k'
+    // -- the reference's sequence regrouped again (rounding only), half the
+    // dependent steps and three operations per state float instead of four
+    auto step2 = [&](int t) {
+      f32x4 k0[S::kVec], q0[S::kVec], k1[S::kVec], q1[S::kVec];
+      const f32x4 *k0p = reinterpret_cast<const f32x4 *>(lds.qk[t][1]) + S::kVec * sub;
+      const f32x4 *q0p = reinterpret_cast<const f32x4 *>(lds.qk[t][0]) + S::kVec * sub;
+      const f32x4 *k1p = reinterpret_cast<const f32x4 *>(lds.qk[t + 1][1]) + S::kVec * sub;
+      const f32x4 *q1p = reinterpret_cast<const f32x4 *>(lds.qk[t + 1][0]) + S::kVec * sub;
+#pragma unroll
+      for (int i = 0; i < S::kVec; ++i) {
+        k0[i] = k0p[i];
+        q0[i] = q0p[i];
+        k1[i] = k1p[i];
+        q1[i] = q1p[i];
+      }
+      const float eg0 = lds.eg[t], eg1 = lds.eg[t + 1];
+      const float b0 = lds.gb[1][t], b1 = lds.gb[1][t + 1];
+      const float v0 = lds.v[t][rl], v1 = lds.v[t + 1][rl];
+      const float kq0 = lds.kq[t], kq1 = lds.kq[t + 1], kk = lds.kk[t], kqn = lds.kqn[t];
+      const float a0 = row_sum<L>(part_dot<S::kVec>(m, k0));
+      const float c0 = row_sum<L>(part_dot<S::kVec>(m, q0));
+      const float a1 = row_sum<L>(part_dot<S::kVec>(m, k1));
+      const float c1 = row_sum<L>(part_dot<S::kVec>(m, q1));
+      const float delta0 = fmaf(-eg0, a0, v0) * b0;
+      const float out0 = fmaf(eg0, c0, delta0 * kq0) * a.scale;
+      const float mk1 = fmaf(eg0, a1, delta0 * kk);   // M' . k'
+      const float mq1 = fmaf(eg0, c1, delta0 * kqn);  // M' . q'
+      const float delta1 = fmaf(-eg1, mk1, v1) * b1;
+      const float out1 = fmaf(eg1, mq1, delta1 * kq1) * a.scale;
+      const float e01 = eg0 * eg1, d0 = eg1 * delta0;
+#pragma unroll
+      for (int i = 0; i < S::kVec; ++i) {
+        m[4 * i] = fmaf(k1[i].x, delta1, fmaf(k0[i].x, d0, e01 * m[4 * i]));
+        m[4 * i + 1] = fmaf(k1[i].y, delta1, fmaf(k0[i].y, d0, e01 * m[4 * i + 1]));
+        m[4 * i + 2] = fmaf(k1[i].z, delta1, fmaf(k0[i].z, d0, e01 * m[4 * i + 2]));
+        m[4 * i + 3] = fmaf(k1[i].w, delta1, fmaf(k0[i].w, d0, e01 * m[4 * i + 3]));
+      }
+      if (sub == 0) {
+        attn[static_cast<size_t>(t) * a.h_v * kFast] = out0;
+        attn[static_cast<size_t>(t + 1) * a.h_v * kFast] = out1;
+      }
+    };
+    int t = 0;
+    for (; t + 1 < nt; t += 2) step2(t);
+    if (t < nt) step(t);
   }
 #pragma unroll
   for (int i = 0; i < S::kVec; ++i)
