@@ -12,7 +12,8 @@
 // the whole token batch: per token the lanes take both row dots from the
 // state before the token (a depth-3 tree in the lane, then a DPP tree over
 // the 16 lanes; see token_step for the algebra), update the row and store
-// one output; the state is read and written once per call.
+// one output; batches go two tokens per update (the step loop of
+// gdn_step128_kernel); the state is read and written once per call.
 // A block's 16 rows share one head, so a block stages the token inputs (q
 // and k of the head, v of its rows, gate, beta) 32 tokens at a time in LDS.
 // The reference sums the 128 products of a dot in index order; the tree
