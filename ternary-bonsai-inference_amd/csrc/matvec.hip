@@ -696,13 +696,213 @@ __device__ __forceinline__ float i8_chunk(const uint8_t *stage, const uint4 *al,
   return tot;
 }
 
+// ---------------------------------------------------------------------------
+// One-token integer product (n_tok == 1): the four lane groups of an MFMA
+// work on four different 128-blocks.
+//
+// A 16x16x64 step sums 16 k-slots from each lane group g.  With one token,
+// A row m = 4 j + d carries digit d of block 4 Q + j of quad Q (four blocks)
+// in the k-slots of lane group j and zeros in the other groups, so step s
+// (0..7) of a quad takes code dword s of block 4 Q + g from lane group g of
+// every weight row, and lane (n, g) ends the quad holding the four digit
+// sums of its own block.  The per-block combine then runs once per quad on
+// all 64 lanes (16 rows x 4 blocks), and only the 16 lanes with m / 4 == g
+// read A fragments (the others keep zeros).
+//
+// x side: each 128-block is scaled by the power of two 2^e that puts its
+// largest |x| in [2^21, 2^22) and rounded to integers X (|X| <= 2^22, 22
+// significant bits), written as four signed base-64 digits
+// X = 64^3 d0 + 64^2 d1 + 64 d2 + d3 (|d0| <= 17, d1..d3 in [-32, 31]).  Codes: byte i of a code dword holds
+// codes 4i .. 4i+3 at bits 0-1, 2-3, 4-5, 6-7.  The masks w & 0x03030303
+// and w & 0x0C0C0C0C give c and 4c per byte (classes 0 and 1), and the same
+// masks of w >> 4 give classes 2 and 3; fragment dword k = class k.  The A
+// digit of a class-0 or class-2 slot is 4 d (fits int8), of a class-1 or
+// class-3 slot d, so every product is 4 d c and each digit sum D_d is 4
+// times sum_j d_j code_j.  H = 64 D0 + D1 and L = 64 D2 + D3 are exact
+// multiples of 4, so
+//     V = 4096 (H >> 2) + (L >> 2) = sum_j X_j code_j
+// (|V| <= 2^22 * 3 * 128 < 2^31), and V - sum_j X_j = sum_j X_j (code_j - 1)
+// exactly in i32; converted to f32 once and multiplied by 2^-e (exact), it
+// is the block sum the reference adds as scale * block_acc
+// (src/kernels.rs:651).
+// ---------------------------------------------------------------------------
+
+// The four digit fragments of step s of one 128-block: lane s of an aligned
+// group of 8 lanes (one block) converts columns 16 s .. 16 s + 15 of
+// xb = x + 128 * blk; every lane of the 8 gets the block factor {bits of
+// sum X, 2^-e} (NaN factor when the block holds a NaN or infinity).
+// Contains cross-lane steps inside each 8-lane group: all lanes of the wave
+// must call it (dead items with live = false).
+__device__ __forceinline__ void q1_load_item(const float *xb, int s, bool live, float (&f)[16]) {
+  const float4 *xr = reinterpret_cast<const float4 *>(xb + 16 * s);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4 v = live ? xr[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+    f[4 * q] = v.x;
+    f[4 * q + 1] = v.y;
+    f[4 * q + 2] = v.z;
+    f[4 * q + 3] = v.w;
+  }
+}
+__device__ __forceinline__ void q1_digits(float (&f)[16], uint4 frag[4], float2 &fac) {
+  float mx = 0.0f;
+  int bad = 0;  // a NaN or infinity in the block
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const bool fin = __builtin_isfinite(f[c]);
+    bad |= !fin;
+    f[c] = fin ? f[c] : 0.0f;
+    mx = fmaxf(mx, fabsf(f[c]));
+  }
+  mx = lane_group_reduce<8>(mx, MaxOp());
+  bad = lane_group_reduce<8>(bad, SumOp());
+  int ex = 0;
+  if (mx > 0.0f) {
+    int k;
+    (void)frexpf(mx, &k);  // mx = f * 2^k, f in [0.5, 1): mx * 2^(22-k) in [2^21, 2^22)
+    ex = 22 - k;
+    ex = ex > 126 ? 126 : ex;  // tiny blocks round toward zero; 2^-e stays normal
+  }
+  const float sc = ldexpf(1.0f, ex);
+  // X + kBias has the unsigned base-64 digits d + 32 (each in [0, 63]) of
+  // the balanced digits d of X; they are packed as bytes first and turned
+  // into the int8 A values per dword: 4 d = (4 (d + 32)) ^ 0x80 for classes
+  // 0 and 2, and d = (d + 32) ^ 0x20 with bit 5 of the result copied into
+  // bits 6 and 7 (the sign of a negative d) for classes 1 and 3
+  constexpr uint32_t kBias = 32u * (1u + 64u + 4096u + 262144u);
+  uint32_t dg[4][4] = {};
+  int sx = 0;
+#pragma unroll
+  for (int c = 0; c < 16; ++c) {
+    const int X = static_cast<int>(rintf(f[c] * sc));  // |X| <= 2^22
+    sx += X;
+    const uint32_t u = static_cast<uint32_t>(X) + kBias;  // in [0, 2^24)
+    const int k = c & 3, i = c >> 2;  // class k, byte i: column 4 i + k of the step
+#pragma unroll
+    for (int d = 0; d < 4; ++d) dg[d][k] |= __builtin_amdgcn_ubfe(u, 6 * (3 - d), 6) << (8 * i);
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if ((k & 1) == 0) {
+        dg[d][k] = (dg[d][k] << 2) ^ 0x80808080u;
+      } else {
+        const uint32_t t = dg[d][k] ^ 0x20202020u, sgn = t & 0x20202020u;
+        dg[d][k] = t | (sgn << 1) | (sgn << 2);
+      }
+    }
+  }
+  sx = lane_group_reduce<8>(sx, SumOp());
+#pragma unroll
+  for (int d = 0; d < 4; ++d) frag[d] = make_uint4(dg[d][0], dg[d][1], dg[d][2], dg[d][3]);
+  fac = make_float2(__int_as_float(sx), bad ? __builtin_nanf("") : ldexpf(1.0f, -ex));
+}
+__device__ __forceinline__ void q1_prep_item(const float *xb, int s, bool live, uint4 frag[4],
+                                             float2 &fac) {
+  float f[16];
+  q1_load_item(xb, s, live, f);
+  q1_digits(f, frag, fac);
+}
+
+// Digit fragments of x into LDS by all `lanes` lanes of the workgroup:
+// uint4 (8 Q + s) * 16 + 4 j + d for block 4 Q + j, step s, digit d; block
+// factors at bf[blk].  The trip count is the same for every wave.  `f0`
+// holds this lane's x values of the first pass, loaded by q1_load_x0 before
+// the weight loads so that waiting for x does not wait for them.
+__device__ __forceinline__ void q1_load_x0(const MmI8Args &a, float (&f0)[16]) {
+  const int item = static_cast<int>(threadIdx.x);
+  const bool live_item = item < a.nblk * 8;
+  q1_load_item(a.x + 128 * (live_item ? item >> 3 : 0), item & 7, live_item, f0);
+}
+__device__ __forceinline__ void q1_stage_x(const MmI8Args &a, uint4 *smem, float2 *bf, int lanes,
+                                           float (&f0)[16]) {
+  const int n_items = a.nblk * 8;
+  for (int base = 0; base < n_items; base += lanes) {
+    const int item = base + static_cast<int>(threadIdx.x);
+    const bool live_item = item < n_items;
+    const int blk = live_item ? item >> 3 : 0, s = item & 7;
+    uint4 frag[4];
+    float2 fac;
+    if (base == 0) {
+      q1_digits(f0, frag, fac);
+    } else {
+      float f[16];
+      q1_load_item(a.x + 128 * blk, s, live_item, f);
+      q1_digits(f, frag, fac);
+    }
+    if (live_item) {
+      uint4 *dst = smem + (8 * (blk >> 2) + s) * 16 + 4 * (blk & 3);
+      dst[0] = frag[0];
+      dst[1] = frag[1];
+      dst[2] = frag[2];
+      dst[3] = frag[3];
+      if (s == 0) bf[blk] = fac;
+    }
+  }
+}
+
+__device__ __forceinline__ i4v decode_q1(uint32_t w) {
+  const uint32_t t = w >> 4;
+  return i4v{static_cast<int>(w & 0x03030303u), static_cast<int>(w & 0x0C0C0C0Cu),
+             static_cast<int>(t & 0x03030303u), static_cast<int>(t & 0x0C0C0C0Cu)};
+}
+
+// One 8-block chunk (two quads) of a wave's 16-row tile from its LDS stage
+// into the lane's running sum (blocks b0 + 4 q + g of row n).  `av` holds the
+// A fragments; lanes with act == false never load them and keep zeros.
+__device__ __forceinline__ float q1_chunk(const uint8_t *stage, const uint4 *al, const float2 *bf,
+                                          bool act, int n, int g, int b0, float tot, i4v (&av)[8]) {
+  const uint8_t *rowp = stage + n * kStageStride;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int jl = 4 * q + g;         // this lane group's block within the chunk
+    const int o = kPq2Blk * jl + 2;   // its first code byte in the staged row
+    const uint32_t *rw = reinterpret_cast<const uint32_t *>(rowp + (o & ~3));
+    const uint32_t sh = static_cast<uint32_t>(o & 3);  // 2 for even blocks, 0 for odd
+    uint32_t r[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) r[i] = rw[i];  // the ninth is read past odd blocks' codes, unused
+    const float sc = static_cast<float>(
+        __builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(rowp + kPq2Blk * jl)));
+    const int quad = (b0 >> 2) + q;
+    if (act) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) av[s] = __builtin_bit_cast(i4v, al[(8 * quad + s) * 16]);
+    }
+    const float2 f = bf[b0 + jl];
+    i4v acc = i4v{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const uint32_t w = __builtin_amdgcn_alignbyte(r[s + 1], r[s], sh);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[s], decode_q1(w), acc, 0, 0, 0);
+    }
+    const int hi = ((acc[0] << 6) + acc[1]) >> 2, lo = ((acc[2] << 6) + acc[3]) >> 2;
+    const int v = (hi << 12) + lo - __float_as_int(f.x);
+    const float blk_sum = static_cast<float>(v) * f.y;  // times 2^-e: exact
+    tot = fmaf(blk_sum, sc, tot);  // src/kernels.rs:651: acc += scale * block_acc
+  }
+  return tot;
+}
+
+// Sum of the four lane groups' partials (blocks = g mod 4) of a row, the same
+// bits on every lane.  All lanes of the wave must be active.
+__device__ __forceinline__ float q1_row_total(float tot) {
+  float lo, hi;
+  lane_swap<16>(tot, lo, hi);
+  tot = lo + hi;
+  lane_swap<32>(tot, lo, hi);
+  return lo + hi;
+}
+
 // Workgroup = RT row tiles x KS waves each; wave (rt, ks) streams the chunks
 // c = ks, ks + KS, ... of row tile blockIdx.x * RT + rt through its private
 // LDS stage, and the KS partial sums of a tile are added in ks order at the
 // end.  The fragments of the (single) token group and its block factors are
 // copied to LDS once per workgroup, only the A rows of live tokens.
-template <int KS, int RT>
-__global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
+template <int KS, int RT, bool Q1>
+__global__ __launch_bounds__(64 * KS * RT) __attribute__((amdgpu_waves_per_eu(4)))
+void pq2_i8_kernel(MmI8Args a) {
   constexpr int kWaves = KS * RT;
   extern __shared__ uint4 smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -712,13 +912,19 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   const int nsteps = 2 * a.nblk;
 
   const int arows = 4 * a.n_tok;  // live A rows (n_tok <= kI8Tok)
-  const int total = nsteps * 4 * arows;
+  const int total = Q1 ? nsteps * 16 : nsteps * 4 * arows;
   float2 *bf = reinterpret_cast<float2 *>(smem + total);
-  const size_t a_words = static_cast<size_t>(total) + (static_cast<size_t>(a.nblk) * kI8Tok + 1) / 2;
+  const size_t a_words = static_cast<size_t>(total) +
+                         (Q1 ? (static_cast<size_t>(a.nblk) + 1) / 2
+                             : (static_cast<size_t>(a.nblk) * kI8Tok + 1) / 2);
   // rows of absent tokens and the unused fourth digit row feed D rows that
   // are never read: any in-bounds fragment will do
-  const uint4 *al = smem + g * arows + (n < arows ? n : (n & 3));
-  const float2 *bl = bf + g;
+  const uint4 *al = Q1 ? smem + n : smem + g * arows + (n < arows ? n : (n & 3));
+  const float2 *bl = Q1 ? bf : bf + g;
+  const bool act = (n >> 2) == g;  // one-token form: lanes that carry A data
+  i4v av[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) av[s] = i4v{0, 0, 0, 0};
   uint8_t *stage = reinterpret_cast<uint8_t *>(smem + a_words) + wave * kStageWaveBytes;
 
   const uint8_t *src[kStageLoads];
@@ -728,7 +934,9 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   for (int k = 0; k < kStageLoads; ++k) {
     const int idx = lane + 64 * k;
     live[k] = idx < 16 * kStageF4;
-    const int r = live[k] ? idx / kStageF4 : 0, c16 = live[k] ? idx % kStageF4 : 0;
+    // lanes past the stage read the last piece again (a load with no branch
+    // keeps the compiler's wait counts exact) and store nothing
+    const int r = live[k] ? idx / kStageF4 : 15, c16 = live[k] ? idx % kStageF4 : kStageF4 - 1;
     int row = row0 + r;
     row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
     src[k] = a.w + static_cast<size_t>(row) * a.row_bytes + 16 * c16;
@@ -738,7 +946,7 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   auto gload = [&](int chunk) {
 #pragma unroll
     for (int k = 0; k < kStageLoads; ++k)
-      if (live[k]) regs[k] = *reinterpret_cast<const uint4 *>(src[k] + static_cast<size_t>(chunk) * kStageRowBytes);
+      regs[k] = *reinterpret_cast<const uint4 *>(src[k] + static_cast<size_t>(chunk) * kStageRowBytes);
   };
   auto lstore = [&]() {
 #pragma unroll
@@ -754,8 +962,13 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   float tot = 0.0f;
   const int n_chunks = a.nblk / kStageBlocks;
   int c = ks;
-  if (c < n_chunks) gload(c);  // the first weight chunk is in flight while x is staged
-  i8_stage_x(a, smem, bf, arows, 64 * kWaves);
+  float xf0[16];
+  if constexpr (Q1) q1_load_x0(a, xf0);  // x before the weights: its wait does not cover them
+  gload(c < n_chunks ? c : n_chunks - 1);  // in flight while x is staged (waves without a chunk re-read one)
+  if constexpr (Q1)
+    q1_stage_x(a, smem, bf, 64 * kWaves, xf0);
+  else
+    i8_stage_x(a, smem, bf, arows, 64 * kWaves);
   __syncthreads();  // x staging visible to every wave
   if (c < n_chunks) {
     lstore();
@@ -764,7 +977,10 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   for (; c < n_chunks; c += KS) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    tot = i8_chunk(stage, al, bl, arows, n, g, c * kStageBlocks, tot);
+    if constexpr (Q1)
+      tot = q1_chunk(stage, al, bl, act, n, g, c * kStageBlocks, tot, av);
+    else
+      tot = i8_chunk(stage, al, bl, arows, n, g, c * kStageBlocks, tot);
     if (c + KS < n_chunks) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -774,6 +990,7 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
   }
 
   const int row = row0 + n;
+  if constexpr (Q1) tot = q1_row_total(tot);
   if constexpr (KS > 1) {
     __syncthreads();  // every wave is done with its stage: reuse the LDS
     float *part = reinterpret_cast<float *>(smem);
@@ -797,18 +1014,24 @@ __global__ __launch_bounds__(64 * KS * RT) void pq2_i8_kernel(MmI8Args a) {
 // boundaries -- and writes each tile's outputs when its last chunk is done.
 // No prepare launch, no scratch, no later rounds of workgroups each repeating
 // the x preparation.
-template <int RT>
+template <int RT, bool Q1>
 __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
   extern __shared__ uint4 smem[];
   const int lane = threadIdx.x & 63, rt = threadIdx.x >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int nsteps = 2 * a.nblk;
   const int arows = 4 * a.n_tok;
-  const int total = nsteps * 4 * arows;
+  const int total = Q1 ? nsteps * 16 : nsteps * 4 * arows;
   float2 *bf = reinterpret_cast<float2 *>(smem + total);
-  const size_t a_words = static_cast<size_t>(total) + (static_cast<size_t>(a.nblk) * kI8Tok + 1) / 2;
-  const uint4 *al = smem + g * arows + (n < arows ? n : (n & 3));
-  const float2 *bl = bf + g;
+  const size_t a_words = static_cast<size_t>(total) +
+                         (Q1 ? (static_cast<size_t>(a.nblk) + 1) / 2
+                             : (static_cast<size_t>(a.nblk) * kI8Tok + 1) / 2);
+  const uint4 *al = Q1 ? smem + n : smem + g * arows + (n < arows ? n : (n & 3));
+  const float2 *bl = Q1 ? bf : bf + g;
+  const bool act = (n >> 2) == g;  // one-token form: lanes that carry A data
+  i4v av[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) av[s] = i4v{0, 0, 0, 0};
   uint8_t *stage = reinterpret_cast<uint8_t *>(smem + a_words) + rt * kStageWaveBytes;
 
   const int n_chunks = a.nblk / kStageBlocks;
@@ -825,8 +1048,10 @@ __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
   for (int k = 0; k < kStageLoads; ++k) {
     const int idx = lane + 64 * k;
     live[k] = idx < 16 * kStageF4;
-    r_of[k] = live[k] ? idx / kStageF4 : 0;
-    c16_of[k] = live[k] ? idx % kStageF4 : 0;
+    // lanes past the stage read the last piece again (a load with no branch
+    // keeps the compiler's wait counts exact) and store nothing
+    r_of[k] = live[k] ? idx / kStageF4 : 15;
+    c16_of[k] = live[k] ? idx % kStageF4 : kStageF4 - 1;
     dst[k] = r_of[k] * kStageStride + 16 * c16_of[k];
   }
   uint4 regs[kStageLoads];
@@ -834,13 +1059,10 @@ __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
     const int tile = item_tile(q), c = q % n_chunks;
 #pragma unroll
     for (int k = 0; k < kStageLoads; ++k) {
-      if (live[k]) {
-        int row = tile * 16 + r_of[k];
-        row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
-        regs[k] = *reinterpret_cast<const uint4 *>(a.w + static_cast<size_t>(row) * a.row_bytes +
-                                                   16 * c16_of[k] +
-                                                   static_cast<size_t>(c) * kStageRowBytes);
-      }
+      int row = tile * 16 + r_of[k];
+      row = row < a.n_rows ? row : a.n_rows - 1;  // tail rows read a valid row, store nothing
+      regs[k] = *reinterpret_cast<const uint4 *>(a.w + static_cast<size_t>(row) * a.row_bytes +
+                                                 16 * c16_of[k] + static_cast<size_t>(c) * kStageRowBytes);
     }
   };
   auto lstore = [&]() {
@@ -854,8 +1076,13 @@ __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
     }
   };
 
-  if (n_items > 0) gload(0);  // the first weight chunk is in flight while x is prepared
-  i8_stage_x(a, smem, bf, arows, 64 * RT);
+  float xf0[16];
+  if constexpr (Q1) q1_load_x0(a, xf0);  // x before the weights: its wait does not cover them
+  gload(0);  // in flight while x is prepared (every workgroup of the grid has a tile group)
+  if constexpr (Q1)
+    q1_stage_x(a, smem, bf, 64 * RT, xf0);
+  else
+    i8_stage_x(a, smem, bf, arows, 64 * RT);
   __syncthreads();  // x staging visible to every wave
   if (n_items > 0) {
     lstore();
@@ -866,9 +1093,13 @@ __global__ __launch_bounds__(64 * RT) void pq2_i8_persist_kernel(MmI8Args a) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int c = q % n_chunks;
-    tot = i8_chunk(stage, al, bl, arows, n, g, c * kStageBlocks, tot);
+    if constexpr (Q1)
+      tot = q1_chunk(stage, al, bl, act, n, g, c * kStageBlocks, tot, av);
+    else
+      tot = i8_chunk(stage, al, bl, arows, n, g, c * kStageBlocks, tot);
     if (c == n_chunks - 1) {  // the tile's last chunk: its outputs are final
       const int row = item_tile(q) * 16 + n;
+      if constexpr (Q1) tot = q1_row_total(tot);
       if (g < a.n_tok && row < a.n_rows) a.y[static_cast<size_t>(g) * a.y_stride + row] = tot;
       tot = 0.0f;
     }
@@ -1146,17 +1377,17 @@ int launch_staged(const MmArgs &a, hipStream_t st) {
   return ok();
 }
 
-template <int KS, int RT = 8 / KS>
+template <int KS, int RT = 8 / KS, bool Q1 = false>
 int launch_i8(const MmI8Args &a, size_t lds_a, hipStream_t st) {
   const int tiles = (a.n_rows + 15) / 16;
   const unsigned gx = static_cast<unsigned>((tiles + RT - 1) / RT);
   const size_t lds = lds_a + static_cast<size_t>(KS * RT) * kStageWaveBytes;
-  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT>),
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_kernel<KS, RT, Q1>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(lds)),
                         "hipFuncSetAttribute"))
     return e;
-  BH_LAUNCH((pq2_i8_kernel<KS, RT>), gx, 64 * KS * RT, lds, st, a);
+  BH_LAUNCH((pq2_i8_kernel<KS, RT, Q1>), gx, 64 * KS * RT, lds, st, a);
   return ok();
 }
 
@@ -1167,8 +1398,10 @@ int launch_i8(const MmI8Args &a, size_t lds_a, hipStream_t st) {
 // workgroup per tile group, and small matrices split each row tile's chunks
 // over KS waves so the grid still holds a few thousand waves; beyond that
 // (the LM head) a persistent grid of one round walks the tiles, so the x
-// preparation is not repeated by later rounds of workgroups.
+// preparation is not repeated by later rounds of workgroups.  Q1 selects the
+// one-token layout (four blocks per MFMA, see q1_chunk) for n_tok == 1.
 constexpr size_t kI8RoundTiles = 4096;
+template <bool Q1>
 int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n_tok, float *y,
            size_t a_bytes, hipStream_t st) {
   const int nblk = static_cast<int>(ne0 / 128);
@@ -1186,7 +1419,7 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
     // 13.7 us, against 20.2 with 8 waves and 14.8 with 4 waves per tile)
     if (n_chunks >= 8 && 2 * (a_bytes + 8 * kStageWaveBytes) > 160 * 1024 &&
         tiles <= 2 * device_cu_count() && a_bytes + 16 * kStageWaveBytes <= 160 * 1024)
-      return launch_i8<8, 2>(a, lds, st);
+      return launch_i8<8, 2, Q1>(a, lds, st);
     // the most waves per row tile whose grid still runs in one round: a
     // workgroup is 8 waves (8 / ks row tiles), as many per CU as LDS and the
     // wave limit allow (ffn_up N=1: 4 waves per tile made 544 workgroups for
@@ -1205,10 +1438,10 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
       }
     }
     switch (ks) {
-      case 8: return launch_i8<8>(a, lds, st);
-      case 4: return launch_i8<4>(a, lds, st);
-      case 2: return launch_i8<2>(a, lds, st);
-      default: return launch_i8<1>(a, lds, st);
+      case 8: return launch_i8<8, 1, Q1>(a, lds, st);
+      case 4: return launch_i8<4, 2, Q1>(a, lds, st);
+      case 2: return launch_i8<2, 4, Q1>(a, lds, st);
+      default: return launch_i8<1, 8, Q1>(a, lds, st);
     }
   }
   // many row tiles: the persistent kernel, one round of 8-wave workgroups
@@ -1217,12 +1450,12 @@ int pq2_i8(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   const size_t per_cu = std::max<size_t>(1, std::min<size_t>(4, (160 * 1024) / plds));
   const size_t groups = (tiles + kPRT - 1) / kPRT;
   const size_t G = std::min(groups, per_cu * device_cu_count());
-  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_persist_kernel<kPRT>),
+  if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_i8_persist_kernel<kPRT, Q1>),
                                             hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(plds)),
                         "hipFuncSetAttribute"))
     return e;
-  BH_LAUNCH(pq2_i8_persist_kernel<kPRT>, static_cast<unsigned>(G), 64 * kPRT, plds, st, a);
+  BH_LAUNCH((pq2_i8_persist_kernel<kPRT, Q1>), static_cast<unsigned>(G), 64 * kPRT, plds, st, a);
   return ok();
 }
 
@@ -1293,12 +1526,17 @@ int pq2_mm(const uint8_t *w, size_t ne0, size_t n_rows, const float *x, size_t n
   }
   const bool stageable = nblk % kStageBlocks == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
                          bh_pq2_row_bytes(ne0) % 16 == 0;
+  if (stageable && n_tok == 1) {
+    // LDS: 16 uint4 per MFMA step (two steps per block), a float2 per block
+    const size_t a_bytes = 2 * nblk * 16 * sizeof(uint4) + (nblk * sizeof(float2) + 15) / 16 * 16;
+    if (a_bytes <= kLdsABytes) return pq2_i8<true>(w, ne0, n_rows, x, n_tok, y, a_bytes, st);
+  }
   if (stageable && n_tok <= static_cast<size_t>(kI8Tok)) {
     // LDS: the live A rows of every step, the block factors (float2 per
     // block and token slot), rounded to whole uint4
     const size_t a_bytes = 2 * nblk * 4 * (4 * n_tok) * sizeof(uint4) +
                            (nblk * kI8Tok * sizeof(float2) + 15) / 16 * 16;
-    if (a_bytes <= kLdsABytes) return pq2_i8(w, ne0, n_rows, x, n_tok, y, a_bytes, st);
+    if (a_bytes <= kLdsABytes) return pq2_i8<false>(w, ne0, n_rows, x, n_tok, y, a_bytes, st);
   }
   if (stageable && n_tok > static_cast<size_t>(kI8Tok)) return pq2_gemm_i8(w, ne0, n_rows, x, n_tok, y, st);
   const int n_ksteps = static_cast<int>(ne0 / 32);

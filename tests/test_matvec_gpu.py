@@ -75,6 +75,8 @@ def test_matmul_reference_case(bh, oracle, synth, dev):
     (17408, 512, 0),      # ffn_down's row width (136 blocks)
     (17408, 333, 1),      # the same, odd tile count and a ragged tail (two tiles per workgroup)
     (5120, 1000, 3),      # ragged rows, offset range
+    (5120, 16, 0), (5120, 17, 1),  # one tile; two tiles, the second one row
+    (4096, 700, 0), (6144, 333, 2), (8192, 5000, 1),  # whole-tile form at 8 and 12 waves; 16-wave rows
     (128, 33, 0), (256, 1, 5),
     (300, 70, 2),         # partial last block: generic path
     (100, 5, 0),
@@ -143,10 +145,12 @@ def test_matvec_many_row_tiles_persistent(bh, oracle, synth, dev, n_tok):
     assert _per_token_err(got, ref) <= TOL
 
 
-def test_matmul_dynamic_range(bh, oracle, synth, dev):
+@pytest.mark.parametrize("ne0,single", [(2048, False), (2048, True), (5120, True)])
+def test_matmul_dynamic_range(bh, oracle, synth, dev, ne0, single):
     """Tokens of magnitude 1e-30 .. 1e30, outliers, and zero tokens: the
-    per-token power-of-two scaling keeps every token at the bar."""
-    ne0, n_rows = 2048, 300
+    per-block power-of-two scaling keeps every token at the bar, in one
+    call or one token per call (the one-token forms)."""
+    n_rows = 300
     table = synth.pq2_table(synth.Rng(11), n_rows, ne0)
     r = synth.Rng(12)
     rows = [r.normal(ne0) * np.float32(s) for s in (1e-30, 1e-6, 1.0, 1e4, 1e30)]
@@ -158,7 +162,12 @@ def test_matmul_dynamic_range(bh, oracle, synth, dev):
     rows.append(tiny)
     x = np.stack(rows).astype(np.float32)
     ref = oracle.pq2_matmul_n(table, ne0, n_rows, x)
-    got = _h(bh.pq2_matmul_n(_dev_table(table, dev), ne0, n_rows, _t(x, dev)))
+    tab = _dev_table(table, dev)
+    if single:
+        got = np.stack([_h(bh.pq2_matmul_n(tab, ne0, n_rows, _t(x[t], dev))).reshape(-1)
+                        for t in range(x.shape[0])])
+    else:
+        got = _h(bh.pq2_matmul_n(tab, ne0, n_rows, _t(x, dev)))
     for t in range(x.shape[0]):
         if not np.any(ref[t]):
             assert not np.any(got[t]), t
@@ -183,6 +192,21 @@ def test_matmul_nonfinite_x(bh, oracle, synth, dev):
     assert not np.any(np.isfinite(got[2]))
     for t in (0, 3):
         assert rel_err(got[t], ref[t]) <= TOL
+
+
+@pytest.mark.parametrize("ne0", [1024, 5120])
+def test_matvec_nonfinite_x(bh, oracle, synth, dev, ne0):
+    """One token (the one-token forms): a NaN makes every output NaN, an
+    infinity makes every output non-finite."""
+    n_rows = 100
+    table = synth.pq2_table(synth.Rng(15), n_rows, ne0)
+    tab = _dev_table(table, dev)
+    for bad, check in ((np.nan, np.isnan), (np.inf, lambda v: ~np.isfinite(v))):
+        x = synth.Rng(16).normal(ne0)
+        x[ne0 // 3] = bad
+        ref = oracle.pq2_matmul_n(table, ne0, n_rows, x)
+        got = _h(bh.pq2_matmul_n(tab, ne0, n_rows, _t(x, dev)))
+        assert np.all(check(ref)) and np.all(check(got))
 
 
 def test_matmul_repeated_shrinking_calls(bh, oracle, synth, dev):
