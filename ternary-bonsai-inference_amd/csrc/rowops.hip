@@ -534,6 +534,16 @@ __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float
   __shared__ double stat_inv;  // 1 / S in f64 (SN)
   const size_t r = blockIdx.y;
   const size_t c0 = static_cast<size_t>(blockIdx.x) * (kBlock * kSplitWV) + threadIdx.x;
+  // wave 0 requests the row's chunk states before its x loads: loads return
+  // in order, so the fold does not wait for the x data
+  float pm0 = -INFINITY;
+  double ps0 = 0.0;
+  const float *pm = sc.part_m + r * nch;
+  const double *ps = sc.part_s + r * nch;
+  if (threadIdx.x < 64 && static_cast<int>(threadIdx.x) < nch) {
+    pm0 = pm[threadIdx.x];
+    ps0 = ps[threadIdx.x];
+  }
   float4 v[kSplitWV];
 #pragma unroll
   for (int i = 0; i < kSplitWV; ++i) {
@@ -542,13 +552,11 @@ __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float
   }
   if (threadIdx.x < 64) {
     const MaxOp mx;
-    const float *pm = sc.part_m + r * nch;
-    const double *ps = sc.part_s + r * nch;
-    float M = -INFINITY;
-    for (int i = threadIdx.x; i < nch; i += 64) M = mx(M, pm[i]);
+    float M = mx(-INFINITY, pm0);  // the reference's `if v > max` ignores a NaN state
+    for (int i = threadIdx.x + 64; i < nch; i += 64) M = mx(M, pm[i]);
     M = lane_group_reduce<64>(M, mx);
-    double S = 0.0;
-    for (int i = threadIdx.x; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
+    double S = static_cast<int>(threadIdx.x) < nch ? ms_scaled(MaxSum{pm0, ps0}, M) : 0.0;
+    for (int i = threadIdx.x + 64; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
     S = lane_group_reduce<64>(S, SumOp{});
     if (threadIdx.x == 0) {
       stat = make_float2(M, 1.0f / static_cast<float>(S));
