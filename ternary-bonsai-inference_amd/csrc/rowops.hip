@@ -456,28 +456,27 @@ struct SplitScratch {
   float *part_m;   // [rows][nch]
 };
 
-__global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float4 *x, size_t r4,
-                                                                     float inv_t, SplitScratch sc) {
-  __shared__ float lm[kBlock / 64];
-  __shared__ double ls[kBlock / 64];
-  const size_t r = blockIdx.y;
-  const int nch = gridDim.x;
-  const size_t base = r * r4 + blockIdx.x * kSplitChunk4;
+// Chunk c of row r to (max, sum of e^(y - max)) in every lane of the block;
+// v keeps the chunk's y = x * inv_t (padding lanes -inf).  Every lane of the
+// block must call it (two block reductions).
+__device__ __forceinline__ void split_chunk_stats(const float4 *x, size_t r4, float inv_t, size_t r,
+                                                  int c, float4 (&v)[kSplitVPT], float *lm,
+                                                  double *ls, float &m_out, double &s_out) {
+  const size_t base = r * r4 + static_cast<size_t>(c) * kSplitChunk4;
   const size_t end = (r + 1) * r4;
   const float ninf = -INFINITY;
-  float4 v[kSplitVPT];
   // all loads in flight before the first use (lanes past the row's end
   // re-read its last float4 and are masked below); a load whose value is
   // used inside its own branch gets a wait of its own
 #pragma unroll
   for (int i = 0; i < kSplitVPT; ++i) {
-    const size_t c = base + threadIdx.x + i * kBlock;
-    v[i] = x[c < end ? c : end - 1];
+    const size_t e = base + threadIdx.x + i * kBlock;
+    v[i] = x[e < end ? e : end - 1];
   }
 #pragma unroll
   for (int i = 0; i < kSplitVPT; ++i) {
-    const size_t c = base + threadIdx.x + i * kBlock;
-    if (c < end) {
+    const size_t e = base + threadIdx.x + i * kBlock;
+    if (e < end) {
       v[i].x *= inv_t;
       v[i].y *= inv_t;
       v[i].z *= inv_t;
@@ -496,7 +495,7 @@ __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float
     m = mx(m, v[i].w);
   }
   m = group_reduce<kBlock>(m, mx, lm);
-  double s = 0.0;
+  double sum = 0.0;
   if (m != ninf) {
     // masked (-inf) and padding entries give exp_hw(-inf) = 0
     float q[kSplitVPT];
@@ -504,18 +503,53 @@ __global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float
     for (int i = 0; i < kSplitVPT; ++i)
       q[i] = (exp_hw(v[i].x - m) + exp_hw(v[i].y - m)) + (exp_hw(v[i].z - m) + exp_hw(v[i].w - m));
 #pragma unroll
-    for (int i = 0; i < kSplitVPT; ++i) s += static_cast<double>(q[i]);
+    for (int i = 0; i < kSplitVPT; ++i) sum += static_cast<double>(q[i]);
   } else {
     // a chunk with no number above -inf adds 0, unless it holds a NaN
     // (which the reference's sum carries through)
 #pragma unroll
     for (int i = 0; i < kSplitVPT; ++i)
-      if (isnan(v[i].x) || isnan(v[i].y) || isnan(v[i].z) || isnan(v[i].w)) s = NAN;
+      if (isnan(v[i].x) || isnan(v[i].y) || isnan(v[i].z) || isnan(v[i].w)) sum = NAN;
   }
-  s = group_reduce<kBlock>(s, SumOp{}, ls);
+  s_out = group_reduce<kBlock>(sum, SumOp{}, ls);
+  m_out = m;
+}
+
+__global__ __launch_bounds__(kBlock) void softmax_split_stats_kernel(const float4 *x, size_t r4,
+                                                                     float inv_t, SplitScratch sc) {
+  __shared__ float lm[kBlock / 64];
+  __shared__ double ls[kBlock / 64];
+  const size_t r = blockIdx.y;
+  const int nch = gridDim.x;
+  float4 v[kSplitVPT];
+  float m;
+  double sum;
+  split_chunk_stats(x, r4, inv_t, r, static_cast<int>(blockIdx.x), v, lm, ls, m, sum);
   if (threadIdx.x == 0) {
     sc.part_m[r * nch + blockIdx.x] = m;
-    sc.part_s[r * nch + blockIdx.x] = s;
+    sc.part_s[r * nch + blockIdx.x] = sum;
+  }
+}
+
+// The fold of a row's nch chunk states into (M, 1/(f32)S) (and 1/S in f64
+// for SN) by one wave: lane i takes chunks i, i + 64, ..., then a fixed
+// shuffle tree, so every block that folds a row gets the same bits.  m0/s0
+// are chunk `lane`'s state (loaded early by the caller, -inf/0 past nch);
+// load(i) returns the state of chunk i >= 64.
+template <bool SN, class Load>
+__device__ __forceinline__ void split_fold(int nch, float m0, double s0, Load load, float2 &stat,
+                                           double &stat_inv) {
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  const MaxOp mx;
+  float M = mx(-INFINITY, m0);  // the reference's `if v > max` ignores a NaN state
+  for (int i = lane + 64; i < nch; i += 64) M = mx(M, load(i).m);
+  M = lane_group_reduce<64>(M, mx);
+  double S = lane < nch ? ms_scaled(MaxSum{m0, s0}, M) : 0.0;
+  for (int i = lane + 64; i < nch; i += 64) S += ms_scaled(load(i), M);
+  S = lane_group_reduce<64>(S, SumOp{});
+  if (lane == 0) {
+    stat = make_float2(M, 1.0f / static_cast<float>(S));
+    if constexpr (SN) stat_inv = 1.0 / S;
   }
 }
 
@@ -550,19 +584,8 @@ __global__ __launch_bounds__(kBlock) void softmax_split_write_kernel(const float
     const size_t c = c0 + static_cast<size_t>(i) * kBlock;
     if (c < r4) v[i] = load_stream(x + r * r4 + c);
   }
-  if (threadIdx.x < 64) {
-    const MaxOp mx;
-    float M = mx(-INFINITY, pm0);  // the reference's `if v > max` ignores a NaN state
-    for (int i = threadIdx.x + 64; i < nch; i += 64) M = mx(M, pm[i]);
-    M = lane_group_reduce<64>(M, mx);
-    double S = static_cast<int>(threadIdx.x) < nch ? ms_scaled(MaxSum{pm0, ps0}, M) : 0.0;
-    for (int i = threadIdx.x + 64; i < nch; i += 64) S += ms_scaled(MaxSum{pm[i], ps[i]}, M);
-    S = lane_group_reduce<64>(S, SumOp{});
-    if (threadIdx.x == 0) {
-      stat = make_float2(M, 1.0f / static_cast<float>(S));
-      if constexpr (SN) stat_inv = 1.0 / S;
-    }
-  }
+  if (threadIdx.x < 64)
+    split_fold<SN>(nch, pm0, ps0, [&](int i) { return MaxSum{pm[i], ps[i]}; }, stat, stat_inv);
   __syncthreads();
   const float2 st = stat;
 #pragma unroll
