@@ -180,12 +180,21 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
     return;
   }
   const int grp = tid / kQkLanes, sub = tid % kQkLanes;
-  // the group's q rows in LDS (REP x 256 floats, the kv head's q heads are
-  // consecutive): registers go to the K and V tiles instead
+  // the group's q rows go to LDS (REP x 256 floats, the kv head's q heads
+  // are consecutive), so registers go to the K and V tiles.  They are loaded
+  // here and stored to LDS only after the first tile's K (and V) loads are
+  // issued: the tile's loads do not wait for q's round trip.
+  constexpr int kQ4 = REP * kHd / 4;
+  constexpr int kQPer = (kQ4 + kBlock - 1) / kBlock;
+  f32x4 qreg[kQPer];
   {
     const f32x4 *qg = reinterpret_cast<const f32x4 *>(
         a.q + (static_cast<size_t>(i) * a.n_head + g * REP) * kHd);
-    for (int o = tid; o < REP * kHd / 4; o += kBlock) s_q[o] = qg[o];
+#pragma unroll
+    for (int u = 0; u < kQPer; ++u) {
+      const int o = tid + u * kBlock;
+      qreg[u] = qg[o < kQ4 ? o : kQ4 - 1];
+    }
   }
   float run_m[kSlots], run_l[kSlots];
 #pragma unroll
@@ -209,6 +218,13 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
       const size_t e0 = (p < end ? p : end - 1) * a.kv_stride + head_off + kQkPer * sub;
 #pragma unroll
       for (int x = 0; x < kQkPer / 4; ++x) kr[pass][x] = Kv<T>::load4(kc, e0 + 4 * x);
+    }
+    if (t0 == beg) {
+#pragma unroll
+      for (int u = 0; u < kQPer; ++u) {
+        const int o = tid + u * kBlock;
+        if (o < kQ4) s_q[o] = qreg[u];
+      }
     }
     __syncthreads();  // s_q written (first tile), while the K rows are in flight
 #pragma unroll
@@ -240,7 +256,9 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
       }
     }
     // the wave's V rows of the tile: issued now (the K registers are free) so
-    // their latency overlaps the softmax step and its barriers
+    // their latency overlaps the softmax step and its barriers (issued with
+    // the K rows instead, one round trip per tile, they measured slower:
+    // ctx 4096 14.0 -> 15.7 us, ctx 32768 55 -> 60 us)
     const int nt = static_cast<int>(end - t0 < static_cast<size_t>(TILE) ? end - t0 : TILE);
     f32x4 vr[TILE / 4];
 #pragma unroll
@@ -311,8 +329,8 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
 }
 
 // out[i][h][d] = sum_c acc_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M), chunks
-// with m_c = -inf left out.  Block (h, i, z) of kCombWaves waves (16 for
-// many chunks, 4 for few) writes dims
+// with m_c = -inf left out.  Block (h, i, z) of kCombWaves waves (16; more than 128
+// chunks, the single-round-trip form below takes fewer) writes dims
 // 64z .. 64z + 63 of row (i, h): the chunk weights e^(m_c - M) are computed
 // once per block into LDS (in tiles of kCombTile chunks), wave w takes
 // chunks w, w + kCombWaves, ... with one lane per dim (loads unconditional,
@@ -373,6 +391,65 @@ __global__ __launch_bounds__(64 * kCombWaves) void attn_combine_kernel(const flo
       nsum += s_red[i][lane];
     }
     out[row * hd + dd] = nsum * (1.0f / dsum);
+  }
+}
+
+// The same merge for at most kCombWaves * kCombPer chunks in one round trip:
+// every load of the block is issued first -- wave w's accumulators of chunks
+// w, w + kCombWaves, ... (kCombPer per lane, one lane per dim) and thread c's
+// (max, sum) of chunk c -- then the block's max, the chunk weights (LDS) and
+// the weighted sum are formed from registers.  The general kernel above
+// waits for the maxima, then the sums, then the accumulators.
+template <int kCombWaves, int kCombPer>
+__global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_kernel(const float *pm,
+                                                                     const float *pl,
+                                                                     const float *pacc,
+                                                                     int n_chunks, float *out) {
+  constexpr int kMax = kCombWaves * kCombPer;
+  static_assert(kMax <= 64 * kCombWaves, "one (max, sum) pair per thread");
+  __shared__ float s_w[kMax];
+  __shared__ float s_red[kCombWaves][kCombDims];
+  __shared__ float s_m[kCombWaves];
+  __shared__ float s_l[kCombWaves];
+  const size_t row = static_cast<size_t>(blockIdx.y) * gridDim.x + blockIdx.x;  // i * n_head + h
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const float *acc = pacc + row * n_chunks * static_cast<size_t>(kHd) + blockIdx.z * kCombDims + lane;
+  float av[kCombPer];
+#pragma unroll
+  for (int k = 0; k < kCombPer; ++k) {
+    const int c = w + kCombWaves * k;
+    av[k] = acc[static_cast<size_t>(c < n_chunks ? c : n_chunks - 1) * kHd];
+  }
+  const float mc = tid < n_chunks ? pm[row * n_chunks + tid] : -INFINITY;
+  const float lc = tid < n_chunks ? pl[row * n_chunks + tid] : 0.0f;
+  float big = wave_max(mc);
+  if (lane == 0) s_m[w] = big;
+  __syncthreads();
+  big = s_m[0];
+#pragma unroll
+  for (int i = 1; i < kCombWaves; ++i) big = fmaxf(big, s_m[i]);
+  const float wc = mc != -INFINITY ? expf(mc - big) : -1.0f;  // -1: left out
+  if (tid < kMax) s_w[tid] = wc;
+  const float den = wave_sum(wc != -1.0f ? lc * wc : 0.0f);
+  if (lane == 0) s_l[w] = den;
+  __syncthreads();
+  float num = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kCombPer; ++k) {
+    const int c = w + kCombWaves * k;
+    const float wk = c < n_chunks ? s_w[c] : -1.0f;
+    num += wk != -1.0f ? av[k] * wk : 0.0f;
+  }
+  s_red[w][lane] = num;
+  __syncthreads();
+  if (w == 0) {
+    float dsum = s_l[0], nsum = s_red[0][lane];
+#pragma unroll
+    for (int i = 1; i < kCombWaves; ++i) {
+      dsum += s_l[i];
+      nsum += s_red[i][lane];
+    }
+    out[row * kHd + blockIdx.z * kCombDims + lane] = nsum * (1.0f / dsum);
   }
 }
 
@@ -1066,11 +1143,14 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
                                                static_cast<int>(n_q), st);
     if (e) return e;
     const dim3 cgrid(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims);
-    if (n_chunks >= 64)
-      BH_LAUNCH(attn_combine_kernel<16>, cgrid, 1024, 0, st, a.pm, a.pl, a.pacc,
-                static_cast<int>(n_chunks), kHd, out);
+    if (n_chunks <= 32)
+      BH_LAUNCH((attn_combine1_kernel<4, 8>), cgrid, 256, 0, st, a.pm, a.pl, a.pacc,
+                static_cast<int>(n_chunks), out);
+    else if (n_chunks <= 128)
+      BH_LAUNCH((attn_combine1_kernel<16, 8>), cgrid, 1024, 0, st, a.pm, a.pl, a.pacc,
+                static_cast<int>(n_chunks), out);
     else
-      BH_LAUNCH(attn_combine_kernel<4>, cgrid, 256, 0, st, a.pm, a.pl, a.pacc,
+      BH_LAUNCH(attn_combine_kernel<16>, cgrid, 1024, 0, st, a.pm, a.pl, a.pacc,
                 static_cast<int>(n_chunks), kHd, out);
     return ok();
   }
