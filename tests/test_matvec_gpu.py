@@ -177,12 +177,14 @@ def test_matmul_dynamic_range(bh, oracle, synth, dev, ne0, single):
         assert err <= TOL, t
 
 
-def test_matmul_nonfinite_x(bh, oracle, synth, dev):
+@pytest.mark.parametrize("ne0,n_tok", [(512, 4), (1024, 20)])
+def test_matmul_nonfinite_x(bh, oracle, synth, dev, ne0, n_tok):
     """A NaN in a token makes every output of that token NaN (0 * NaN is
-    NaN); an infinity makes them non-finite; other tokens are unaffected."""
-    ne0, n_rows = 512, 64
+    NaN); an infinity makes them non-finite; other tokens are unaffected
+    (the integer form for 4 tokens, the shared-x f16 form for 20)."""
+    n_rows = 64
     table = synth.pq2_table(synth.Rng(13), n_rows, ne0)
-    x = synth.Rng(14).normal(4 * ne0).reshape(4, ne0)
+    x = synth.Rng(14).normal(n_tok * ne0).reshape(n_tok, ne0)
     x[1, 77] = np.nan
     x[2, 300] = np.inf
     ref = oracle.pq2_matmul_n(table, ne0, n_rows, x)
@@ -190,7 +192,7 @@ def test_matmul_nonfinite_x(bh, oracle, synth, dev):
     assert np.all(np.isnan(ref[1])) and np.all(np.isnan(got[1]))
     assert np.array_equal(np.isfinite(got[2]), np.isfinite(ref[2]))
     assert not np.any(np.isfinite(got[2]))
-    for t in (0, 3):
+    for t in [0] + list(range(3, n_tok)):
         assert rel_err(got[t], ref[t]) <= TOL
 
 
