@@ -53,6 +53,19 @@ __global__ __launch_bounds__(256) void write_kernel(f4v *out, size_t n4) {
   if (i < n4) __builtin_nontemporal_store(f4v{1.f, 2.f, 3.f, 4.f}, out + i);
 }
 
+// Write-only shapes of a kernel that stages rows and loops: a block of B
+// lanes writes one contiguous region of `per_block` float4s, one float4 per
+// lane per iteration (the fused gather + RMSNorm writes 2 x 16 rows of 20 KB
+// per 1024-lane block this way).
+template <int B>
+__global__ __launch_bounds__(B) void write_loop_kernel(f4v *out, size_t n4, size_t per_block) {
+  const size_t base = static_cast<size_t>(blockIdx.x) * per_block;
+  for (size_t k = threadIdx.x; k < per_block; k += B) {
+    const size_t i = base + k;
+    if (i < n4) __builtin_nontemporal_store(f4v{1.f, 2.f, 3.f, 4.f}, out + i);
+  }
+}
+
 // N(0,1)-like values (sum of four hashed uniforms, scaled to unit variance):
 // random mantissa bits, like the bench's inputs, where hipMemset's constant
 // bytes toggle no data lines.
@@ -119,6 +132,8 @@ int main(int argc, char **argv) {
   std::printf("\n| MiB each way | copy nt us | %% of 8 TB/s | copy sc1 nt us | %% | copy nt, N(0,1) data us | %% | read us | %% | write us | %% |\n");
   std::printf("|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|\n");
   constexpr int kSets = 8;
+  struct LoopRow { size_t mib; double a, b, c, d; };
+  std::vector<LoopRow> loops;
   for (size_t mib : sizes_mib) {
     const size_t bytes = mib << 20, n4 = bytes / 16;
     std::vector<f4v *> a(kSets), b(kSets);
@@ -150,6 +165,21 @@ int main(int argc, char **argv) {
     const double cr = time_graph([&](int k) {
       hipLaunchKernelGGL(copy_kernel<false>, dim3(grid), dim3(256), 0, st, a[k % kSets], b[k % kSets], n4);
     });
+    // looped writers: 1024-lane blocks over 40 KB (one float4 per lane, the
+    // gather's per-row burst) and 640 KB (its 16 embedding + 16 norm rows);
+    // 256-lane blocks over 4 KB (the flat writer's shape, as a loop of one)
+    // and 64 KB
+    auto wl = [&](auto kern, int lanes, size_t per_block) {
+      const unsigned nb = static_cast<unsigned>((n4 + per_block - 1) / per_block);
+      return time_graph([&](int k) {
+        hipLaunchKernelGGL(kern, dim3(nb), dim3(lanes), 0, st, b[k % kSets], n4, per_block);
+      });
+    };
+    const double wl1 = wl(write_loop_kernel<1024>, 1024, 2560);   // 40 KB
+    const double wl2 = wl(write_loop_kernel<1024>, 1024, 40960);  // 640 KB
+    const double wl3 = wl(write_loop_kernel<256>, 256, 256);      // 4 KB
+    const double wl4 = wl(write_loop_kernel<256>, 256, 4096);     // 64 KB
+    loops.push_back({mib, wl1, wl2, wl3, wl4});
     auto pct = [](double b_, double us) { return b_ / us / 8e6 * 100.0; };
     std::printf("| %zu | %.2f | %.1f | %.2f | %.1f | %.2f | %.1f | %.2f | %.1f | %.2f | %.1f |\n", mib, c0,
                 pct(2.0 * bytes, c0), c1, pct(2.0 * bytes, c1), cr, pct(2.0 * bytes, cr), rd, pct(bytes, rd), wr, pct(bytes, wr));
@@ -157,6 +187,14 @@ int main(int argc, char **argv) {
       CK(hipFree(a[s]));
       CK(hipFree(b[s]));
     }
+  }
+  std::printf("\n| MiB written | 1024-lane blocks x 40 KB us | %% | 1024 x 640 KB us | %% | 256 x 4 KB us | %% | 256 x 64 KB us | %% |\n");
+  std::printf("|---:|---:|---:|---:|---:|---:|---:|---:|---:|\n");
+  for (const auto &r : loops) {
+    const double by = static_cast<double>(r.mib << 20);
+    auto pc = [&](double us) { return by / us / 8e6 * 100.0; };
+    std::printf("| %zu | %.2f | %.1f | %.2f | %.1f | %.2f | %.1f | %.2f | %.1f |\n", r.mib, r.a, pc(r.a), r.b,
+                pc(r.b), r.c, pc(r.c), r.d, pc(r.d));
   }
   return 0;
 }
