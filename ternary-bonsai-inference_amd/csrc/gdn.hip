@@ -143,7 +143,9 @@ __global__ __launch_bounds__(kBlock) void gdn_step128_direct_kernel(GdnStepArgs 
 // no branches.  A row goes to L lanes of 128 / L floats: L = 16 gives 1536
 // waves for the model's 6144 rows (two waves on the busiest SIMDs hide each
 // other's latency); L = 8 halves the cross-lane work but leaves one wave
-// per SIMD with its dependency chain exposed.
+// per SIMD with its dependency chain exposed; L = 32 (3072 waves, a
+// permlane swap more per row dot) measured slower at T=256: 82-84 us
+// against 73-74.
 constexpr int kChunk = 32;
 constexpr size_t kDirectMax = 4;  // token counts that skip the LDS staging
 constexpr int kStagedLanes = 16;  // measured faster than 8 on MI355X
