@@ -57,6 +57,8 @@ def _run(bh, dev, q, pos0, kc, vc, n_kv):
     (1, 4095, False), (1, 4095, True), (1, 130, True),
     (1, 9000, False), (1, 20000, True),   # one query, chunks of several tiles (ragged last chunk)
     (3, 100, False),     # a few tokens at once (speculative verification)
+    (3, 63, False),      # query 0 sees no position of the last chunk (merged as empty)
+    (5, 4093, False),    # several queries over several merge groups
     (17, 0, False),      # a causal batch from the first position
     (64, 2000, True),
 ])

@@ -134,3 +134,28 @@ def test_graph_softmax_survives_scratch_growth(bh, oracle, synth, dev):
                                oracle.softmax_rows(big[r].cpu().numpy(), row)) < 2e-5, r
             del big, bout
             torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("n_q,pos0", [(1, 4095), (3, 63)])
+def test_graph_attention_decode(bh, synth, dev, n_q, pos0):
+    """The decode attention merges its chunks inside the launch (device-scope
+    arrival counters that the last arriver resets): every replay, with eager
+    calls in between, reproduces the eager result bit for bit (the merge
+    order does not depend on which block arrives last)."""
+    import torch
+    n_head, n_kv, hd = 24, 4, 256
+    r = synth.Rng(77 + n_q)
+    n = pos0 + n_q
+    q = _t(r.normal(n_q * n_head * hd).reshape(n_q, n_head, hd).astype(np.float32), dev)
+    kc = _t(r.normal(n * n_kv * hd).reshape(n, n_kv * hd).astype(np.float32), dev)
+    vc = _t(r.normal(n * n_kv * hd).reshape(n, n_kv * hd).astype(np.float32), dev)
+
+    def make_out():
+        return [torch.empty_like(q)]
+
+    def run(s, outs=None):
+        outs = outs or make_out()
+        bh.attention(q, pos0, kc, vc, n_kv, out=outs[0], stream=s)
+        return outs
+
+    _replay_check(make_out, run, dev)
