@@ -145,6 +145,18 @@ def test_matvec_many_row_tiles_persistent(bh, oracle, synth, dev, n_tok):
     assert _per_token_err(got, ref) <= TOL
 
 
+def test_matvec_lm_head_width_many_tiles(bh, oracle, synth, dev):
+    """One token, the LM head's row width (5120) and more than 4096 row
+    tiles with a ragged tail: the many-tile one-token path."""
+    ne0, n_rows = 5120, 4096 * 16 + 77
+    _say("lm-head width", n_rows)
+    table = synth.pq2_table(synth.Rng(23), n_rows, ne0)
+    x = synth.Rng(24).normal(ne0).reshape(1, ne0)
+    ref = oracle.pq2_matmul_n(table, ne0, n_rows, x)
+    got = _h(bh.pq2_matmul_n(_dev_table(table, dev), ne0, n_rows, _t(x, dev)))
+    assert _per_token_err(got, ref) <= TOL
+
+
 @pytest.mark.parametrize("ne0,single", [(2048, False), (2048, True), (5120, True)])
 def test_matmul_dynamic_range(bh, oracle, synth, dev, ne0, single):
     """Tokens of magnitude 1e-30 .. 1e30, outliers, and zero tokens: the
