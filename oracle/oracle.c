@@ -458,6 +458,285 @@ int or_attention(const float *q, size_t n_q, size_t pos0, const void *k_cache,
   return OR_OK;
 }
 
+/* ---- planar-quantized KV cache (src/kvquant.rs) -------------------------- */
+
+/* erf by Abramowitz & Stegun 7.1.26, src/kvquant.rs:34-44 */
+static double pq_erf(double x) {
+  double sign = x < 0.0 ? -1.0 : 1.0;
+  x = fabs(x);
+  double t = 1.0 / (1.0 + 0.3275911 * x);
+  double y = 1.0 - (((((1.061405429 * t - 1.453152027) * t) + 1.421413741) * t - 0.284496736) * t +
+                    0.254829592) *
+                       t * exp(-x * x);
+  return sign * y;
+}
+static double pq_cdf(double x, double sigma) {
+  return 0.5 * (1.0 + pq_erf(x / (sigma * 1.4142135623730951)));
+}
+static double pq_pdf(double x, double sigma) {
+  return exp(-(x * x) / (2.0 * sigma * sigma)) / (sigma * sqrt(2.0 * 3.141592653589793));
+}
+static double pq_m1(double a, double b, double sigma) {
+  return sigma * sigma * (pq_pdf(a, sigma) - pq_pdf(b, sigma));
+}
+
+/* solve_lloyd_max + codebook, src/kvquant.rs:58-118: sigma = 1/sqrt(d),
+ * 2^bits centroids started evenly over +-3.5 sigma, edges at midpoints and
+ * +-12 sigma, up to 300 updates c_i = E[X | edge_i < X < edge_i+1] (kept
+ * when the cell's mass is <= 1e-15), stopping when no centroid moves by
+ * 1e-12; then rounded to f32. */
+void or_planar_codebook(size_t d, unsigned bits, float *out) {
+  size_t n = (size_t)1 << bits;
+  double sigma = 1.0 / sqrt((double)d);
+  double lo = -3.5 * sigma, hi = 3.5 * sigma, outer = 12.0 * sigma;
+  double c[256], nx[256], e[257];
+  for (size_t i = 0; i < n; ++i) c[i] = lo + (hi - lo) * ((double)i + 0.5) / (double)n;
+  for (int it = 0; it < 300; ++it) {
+    e[0] = -outer;
+    for (size_t i = 0; i + 1 < n; ++i) e[i + 1] = (c[i] + c[i + 1]) / 2.0;
+    e[n] = outer;
+    double shift = 0.0;
+    for (size_t i = 0; i < n; ++i) {
+      double mass = pq_cdf(e[i + 1], sigma) - pq_cdf(e[i], sigma);
+      nx[i] = mass > 1e-15 ? pq_m1(e[i], e[i + 1], sigma) / mass : c[i];
+    }
+    for (size_t i = 0; i < n; ++i) {
+      double dlt = fabs(nx[i] - c[i]);
+      if (dlt > shift) shift = dlt;
+      c[i] = nx[i];
+    }
+    if (shift < 1e-12) break;
+  }
+  for (size_t i = 0; i < n; ++i) out[i] = (float)c[i];
+}
+
+/* kvquant_expected_distortion, src/kvquant.rs:854-880 */
+double or_planar_distortion(size_t d, unsigned bits) {
+  size_t n = (size_t)1 << bits;
+  double sigma = 1.0 / sqrt((double)d), outer = 12.0 * sigma;
+  float c[256];
+  double e[257], dist = 0.0;
+  or_planar_codebook(d, bits, c);
+  e[0] = -outer;
+  for (size_t i = 0; i + 1 < n; ++i) e[i + 1] = ((double)c[i] + (double)c[i + 1]) / 2.0;
+  e[n] = outer;
+  for (size_t i = 0; i < n; ++i) {
+    double a = e[i], b = e[i + 1], c0 = (double)c[i];
+    double mass = pq_cdf(b, sigma) - pq_cdf(a, sigma);
+    double m1 = pq_m1(a, b, sigma);
+    double m2 = sigma * sigma * (mass + a * pq_pdf(a, sigma) - b * pq_pdf(b, sigma));
+    dist += m2 - 2.0 * c0 * m1 + c0 * c0 * mass;
+  }
+  return (double)(float)dist;
+}
+
+/* givens_table, src/kvquant.rs:124-146: splitmix64 from state 42, u =
+ * (r >> 11) / 2^53, t = 2 pi u in f64, (cos t, sin t) rounded to f32. */
+void or_planar_givens(size_t d, float *c, float *s) {
+  uint64_t st = 42;
+  for (size_t i = 0; i < (d + 1) / 2; ++i) {
+    uint64_t z = (st += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    double u = (double)(z >> 11) / 9007199254740992.0;
+    double t = u * 6.283185307179586;
+    c[i] = (float)cos(t);
+    s[i] = (float)sin(t);
+  }
+}
+
+/* packed_bytes(hd_padded, bits), src/kvquant.rs:182-184, 332-334 */
+size_t or_planar_packed_len(size_t hd, unsigned bits) {
+  size_t hp = (hd + 1) / 2 * 2;
+  return (hp * bits + 7) / 8;
+}
+
+/* pack_idx / unpack_idx, src/kvquant.rs:150-330.  For the rows here (an
+ * even count, and a multiple of 8 for 3 bits) every layout the reference
+ * picks -- 8-coordinate groups in 3 bytes for 3 bits, single planes for 1,
+ * 2 and 4 bits, the LSB-first bitstream otherwise -- places coordinate i at
+ * bits [i bits, (i + 1) bits) of the little-endian byte string; the
+ * bitstream is written directly (the equivalence is a test). */
+void or_planar_pack(const uint8_t *idx, size_t n, unsigned bits, uint8_t *out) {
+  size_t nb = (n * bits + 7) / 8;
+  memset(out, 0, nb);
+  size_t bitpos = 0;
+  for (size_t i = 0; i < n; ++i) {
+    size_t byte = bitpos >> 3;
+    unsigned off = (unsigned)(bitpos & 7);
+    unsigned v = idx[i] & ((1u << bits) - 1u);
+    out[byte] |= (uint8_t)((v << off) & 0xffu);
+    if (off + bits > 8) out[byte + 1] |= (uint8_t)(v >> (8 - off));
+    bitpos += bits;
+  }
+}
+void or_planar_unpack(const uint8_t *packed, size_t n, unsigned bits, uint8_t *out) {
+  unsigned mask = (1u << bits) - 1u;
+  size_t bitpos = 0;
+  for (size_t i = 0; i < n; ++i) {
+    size_t byte = bitpos >> 3;
+    unsigned off = (unsigned)(bitpos & 7);
+    unsigned v = (unsigned)packed[byte] >> off;
+    if (off + bits > 8) v |= (unsigned)packed[byte + 1] << (8 - off);
+    out[i] = (uint8_t)(v & mask);
+    bitpos += bits;
+  }
+}
+
+/* PlanarQuant::rotate, src/kvquant.rs:356-366: pair i (2i, 2i+1) by
+ * (c_i, s_i): [c a - s b, s a + c b] */
+void or_planar_rotate(const float *x, size_t hd, const float *c, const float *s, float *out) {
+  for (size_t i = 0; i < (hd + 1) / 2; ++i) {
+    float a = 2 * i < hd ? x[2 * i] : 0.0f, b = 2 * i + 1 < hd ? x[2 * i + 1] : 0.0f;
+    out[2 * i] = c[i] * a - s[i] * b;
+    out[2 * i + 1] = s[i] * a + c[i] * b;
+  }
+}
+
+/* PlanarQuant::quantize, src/kvquant.rs:381-396 (nearest :341-353: the
+ * first centroid of least |v - c|) */
+void or_planar_quantize(const float *x, size_t hd, unsigned bits, uint8_t *packed, float *norm) {
+  size_t hp = (hd + 1) / 2 * 2, nc = (size_t)1 << bits;
+  float cb[256], gc[128], gs[128], unit[256], rot[256];
+  uint8_t idx[256];
+  or_planar_codebook(hd, bits, cb);
+  or_planar_givens(hd, gc, gs);
+  float ss = 0.0f;
+  for (size_t i = 0; i < hd; ++i) ss += x[i] * x[i];
+  float n = sqrtf(ss);
+  *norm = n;
+  float inv = n > 1e-12f ? 1.0f / n : 0.0f;
+  for (size_t i = 0; i < hp; ++i) unit[i] = i < hd ? x[i] * inv : 0.0f;
+  or_planar_rotate(unit, hp, gc, gs, rot);
+  for (size_t i = 0; i < hp; ++i) {
+    size_t best = 0;
+    float bd = fabsf(rot[i] - cb[0]);
+    for (size_t k = 1; k < nc; ++k) {
+      float dk = fabsf(rot[i] - cb[k]);
+      if (dk < bd) {
+        bd = dk;
+        best = k;
+      }
+    }
+    idx[i] = (uint8_t)best;
+  }
+  or_planar_pack(idx, hp, bits, packed);
+}
+
+/* PlanarQuant::dequantize, src/kvquant.rs:399-413 (rotate_inv :369-378) */
+void or_planar_dequantize(const uint8_t *packed, float norm, size_t hd, unsigned bits, float *out) {
+  size_t hp = (hd + 1) / 2 * 2;
+  float cb[256], gc[128], gs[128], rot[256];
+  uint8_t idx[256];
+  or_planar_codebook(hd, bits, cb);
+  or_planar_givens(hd, gc, gs);
+  or_planar_unpack(packed, hp, bits, idx);
+  for (size_t i = 0; i < hp; ++i) rot[i] = cb[idx[i]];
+  for (size_t i = 0; i < hp / 2; ++i) {
+    float a = rot[2 * i], b = rot[2 * i + 1];
+    float u0 = gc[i] * a + gs[i] * b, u1 = -gs[i] * a + gc[i] * b;
+    if (2 * i < hd) out[2 * i] = u0 * norm;
+    if (2 * i + 1 < hd) out[2 * i + 1] = u1 * norm;
+  }
+}
+
+/* PlanarQuant::dot_rotated_scratch, src/kvquant.rs:444-460: f32 sum in
+ * index order of q_rot[i] * c[idx_i] over i < hd, times the norm */
+float or_planar_dot_rotated(const float *q_rot, const uint8_t *packed, float norm, size_t hd,
+                            unsigned bits) {
+  size_t hp = (hd + 1) / 2 * 2;
+  float cb[256];
+  uint8_t idx[256];
+  or_planar_codebook(hd, bits, cb);
+  or_planar_unpack(packed, hp, bits, idx);
+  float acc = 0.0f;
+  for (size_t i = 0; i < hd; ++i) acc += q_rot[i] * cb[idx[i]];
+  return acc * norm;
+}
+
+/* AttnCache::append_k_quantized / append_v_quantized / append_v,
+ * src/forward.rs:99-118, 128-140: per token and kv head, packed indices at
+ * kq[(pos * n_kv + kv) * packed_len] and the norm at kn[pos * n_kv + kv];
+ * v likewise into vq / vn, or (vq == NULL) as f32 rows into v_f32. */
+void or_kv_store_planar(const float *k, const float *v, size_t n_tok, size_t n_kv, size_t hd,
+                        unsigned bits, uint8_t *kq, float *kn, uint8_t *vq, float *vn,
+                        float *v_f32, size_t pos0) {
+  size_t plen = or_planar_packed_len(hd, bits);
+  for (size_t t = 0; t < n_tok; ++t)
+    for (size_t h = 0; h < n_kv; ++h) {
+      size_t r = (pos0 + t) * n_kv + h;
+      or_planar_quantize(k + (t * n_kv + h) * hd, hd, bits, kq + r * plen, kn + r);
+      if (vq != NULL)
+        or_planar_quantize(v + (t * n_kv + h) * hd, hd, bits, vq + r * plen, vn + r);
+      else
+        memcpy(v_f32 + r * hd, v + (t * n_kv + h) * hd, hd * sizeof(float));
+    }
+}
+
+/* The quantized branches of full_attention_layer, src/forward.rs:296-349:
+ * per q head, q rotated once; score_j = dot_rotated(q_rot, k_j, |k_j|) *
+ * scale; probs = softmax_rows; V quantized: head_out[d] += (p_j |v_j|) *
+ * c[idx_jd] over positions with p_j != 0, then the inverse rotation in
+ * place; V in f32: head_out[d] += p_j * v_j[d].  Token i of n_q sees
+ * positions 0 .. pos0 + i. */
+int or_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *kq,
+                        const float *kn, const uint8_t *vq, const float *vn, const float *v_f32,
+                        unsigned bits, size_t n_head, size_t n_kv, size_t hd, float *out) {
+  if (n_kv == 0 || hd == 0 || hd % 2 != 0 || hd > 256 || n_head % n_kv != 0 || bits < 1 ||
+      bits > 8)
+    return OR_ERR_SHAPE;
+  size_t n_rep = n_head / n_kv, n_max = pos0 + n_q, plen = or_planar_packed_len(hd, bits);
+  float scale = 1.0f / sqrtf((float)hd);
+  float cb[256], gc[128], gs[128], qrot[256], vrot[256];
+  uint8_t idx[256];
+  or_planar_codebook(hd, bits, cb);
+  or_planar_givens(hd, gc, gs);
+  float *scores = (float *)malloc((n_max ? n_max : 1) * sizeof(float));
+  float *probs = (float *)malloc((n_max ? n_max : 1) * sizeof(float));
+  if (scores == NULL || probs == NULL) {
+    free(scores);
+    free(probs);
+    return OR_ERR_SHAPE;
+  }
+  for (size_t i = 0; i < n_q; ++i) {
+    size_t n_pos = pos0 + i + 1;
+    for (size_t hq = 0; hq < n_head; ++hq) {
+      size_t kv = hq / n_rep;
+      or_planar_rotate(q + (i * n_head + hq) * hd, hd, gc, gs, qrot);
+      for (size_t j = 0; j < n_pos; ++j) {
+        size_t r = j * n_kv + kv;
+        scores[j] = or_planar_dot_rotated(qrot, kq + r * plen, kn[r], hd, bits) * scale;
+      }
+      or_softmax_rows(scores, n_pos, n_pos, 1.0f, probs);
+      float *o = out + (i * n_head + hq) * hd;
+      for (size_t d = 0; d < hd; ++d) o[d] = 0.0f;
+      for (size_t j = 0; j < n_pos; ++j) {
+        float pj = probs[j];
+        if (pj == 0.0f) continue;
+        size_t r = j * n_kv + kv;
+        if (vq != NULL) {
+          or_planar_unpack(vq + r * plen, hd, bits, idx);
+          for (size_t d = 0; d < hd; ++d) vrot[d] = cb[idx[d]];
+          float w = pj * vn[r];
+          for (size_t d = 0; d < hd; ++d) o[d] += w * vrot[d];
+        } else {
+          for (size_t d = 0; d < hd; ++d) o[d] += pj * v_f32[r * hd + d];
+        }
+      }
+      if (vq != NULL)
+        for (size_t p2 = 0; p2 < hd / 2; ++p2) {
+          float a = o[2 * p2], b = o[2 * p2 + 1];
+          o[2 * p2] = gc[p2] * a + gs[p2] * b;
+          o[2 * p2 + 1] = -gs[p2] * a + gc[p2] * b;
+        }
+    }
+  }
+  free(scores);
+  free(probs);
+  return OR_OK;
+}
+
 /* ---- PQ2_0 products (src/kernels.rs:233-423) ------------------------------ */
 
 /* row_dot_scalar, src/kernels.rs:633-653: per 128-block an f32 sum of

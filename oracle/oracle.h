@@ -108,6 +108,26 @@ void or_gdn_step(const float *q, const float *k, const float *v, const float *ga
                  const float *beta, float *state, float *attn, size_t n_tok, size_t h_k,
                  size_t h_v, size_t s);
 
+/* Planar-quantized KV cache, src/kvquant.rs (PlanarQuant) and
+ * src/forward.rs:99-112, 128-140, 296-349.  bits 1..8, hd even. */
+void or_planar_codebook(size_t d, unsigned bits, float *out);          /* 2^bits centroids */
+double or_planar_distortion(size_t d, unsigned bits);                  /* expected MSE */
+void or_planar_givens(size_t d, float *c, float *s);                   /* ceil(d/2) pairs */
+size_t or_planar_packed_len(size_t hd, unsigned bits);
+void or_planar_pack(const uint8_t *idx, size_t n, unsigned bits, uint8_t *out);
+void or_planar_unpack(const uint8_t *packed, size_t n, unsigned bits, uint8_t *out);
+void or_planar_rotate(const float *x, size_t hd, const float *c, const float *s, float *out);
+void or_planar_quantize(const float *x, size_t hd, unsigned bits, uint8_t *packed, float *norm);
+void or_planar_dequantize(const uint8_t *packed, float norm, size_t hd, unsigned bits, float *out);
+float or_planar_dot_rotated(const float *q_rot, const uint8_t *packed, float norm, size_t hd,
+                            unsigned bits);
+void or_kv_store_planar(const float *k, const float *v, size_t n_tok, size_t n_kv, size_t hd,
+                        unsigned bits, uint8_t *kq, float *kn, uint8_t *vq, float *vn,
+                        float *v_f32, size_t pos0);
+int or_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *kq,
+                        const float *kn, const uint8_t *vq, const float *vn, const float *v_f32,
+                        unsigned bits, size_t n_head, size_t n_kv, size_t hd, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,20 @@ _SIG = {
     "or_kv_store": (None, [_vp, _vp, _sz, _sz, _vp, _vp, _sz, ctypes.c_int]),
     "or_attention": (ctypes.c_int, [_vp, _sz, _sz, _vp, _vp, ctypes.c_int, _sz, _sz, _sz, _vp]),
     "or_gdn_step": (None, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz]),
+    "or_planar_codebook": (None, [_sz, ctypes.c_uint, _vp]),
+    "or_planar_distortion": (ctypes.c_double, [_sz, ctypes.c_uint]),
+    "or_planar_givens": (None, [_sz, _vp, _vp]),
+    "or_planar_packed_len": (_sz, [_sz, ctypes.c_uint]),
+    "or_planar_pack": (None, [_vp, _sz, ctypes.c_uint, _vp]),
+    "or_planar_unpack": (None, [_vp, _sz, ctypes.c_uint, _vp]),
+    "or_planar_rotate": (None, [_vp, _sz, _vp, _vp, _vp]),
+    "or_planar_quantize": (None, [_vp, _sz, ctypes.c_uint, _vp, _vp]),
+    "or_planar_dequantize": (None, [_vp, _f, _sz, ctypes.c_uint, _vp]),
+    "or_planar_dot_rotated": (_f, [_vp, _vp, _f, _sz, ctypes.c_uint]),
+    "or_kv_store_planar": (None, [_vp, _vp, _sz, _sz, _sz, ctypes.c_uint, _vp, _vp, _vp, _vp, _vp,
+                                  _sz]),
+    "or_attention_planar": (ctypes.c_int, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint,
+                                           _sz, _sz, _sz, _vp]),
     "or_pq2_matmul_n": (None, [_vp, _sz, ctypes.c_uint64, _sz, _vp, _sz, _vp]),
 }
 
@@ -325,4 +339,116 @@ def silu_l2_part(conv, l2_dim: int, head_dim: int, eps: float) -> np.ndarray:
     out = np.empty_like(conv)
     _st(lib().or_silu_l2_part(_p(conv), n_tok, conv_dim, l2_dim, head_dim, eps, _p(out)),
         "silu_l2_part shape")
+    return out
+
+
+# ---- planar-quantized KV cache (src/kvquant.rs) ----------------------------
+
+def planar_codebook(d: int, bits: int) -> np.ndarray:
+    """codebook (src/kvquant.rs:105-118): 2^bits Lloyd-Max centroids, f32."""
+    out = np.empty(1 << bits, np.float32)
+    lib().or_planar_codebook(d, bits, _p(out))
+    return out
+
+
+def planar_distortion(d: int, bits: int) -> float:
+    """kvquant_expected_distortion (src/kvquant.rs:854-880)."""
+    return float(lib().or_planar_distortion(d, bits))
+
+
+def planar_givens(d: int):
+    """givens_table (src/kvquant.rs:124-146): (cos, sin) f32 per pair."""
+    n = (d + 1) // 2
+    c, s = np.empty(n, np.float32), np.empty(n, np.float32)
+    lib().or_planar_givens(d, _p(c), _p(s))
+    return c, s
+
+
+def planar_packed_len(hd: int, bits: int) -> int:
+    return int(lib().or_planar_packed_len(hd, bits))
+
+
+def planar_pack(idx, bits: int) -> np.ndarray:
+    idx = _c(idx, np.uint8)
+    out = np.empty((idx.size * bits + 7) // 8, np.uint8)
+    lib().or_planar_pack(_p(idx), idx.size, bits, _p(out))
+    return out
+
+
+def planar_unpack(packed, n: int, bits: int) -> np.ndarray:
+    packed = _c(packed, np.uint8)
+    if packed.size < (n * bits + 7) // 8:
+        raise OracleShapeError("planar_unpack: packed too short")
+    out = np.empty(n, np.uint8)
+    lib().or_planar_unpack(_p(packed), n, bits, _p(out))
+    return out
+
+
+def planar_rotate(x) -> np.ndarray:
+    """PlanarQuant::rotate (src/kvquant.rs:356-366) with the fixed table."""
+    x = _c(x)
+    c, s = planar_givens(x.size)
+    out = np.empty(x.size + (x.size & 1), np.float32)
+    lib().or_planar_rotate(_p(x), x.size, _p(c), _p(s), _p(out))
+    return out
+
+
+def planar_quantize(x, bits: int):
+    """PlanarQuant::quantize (src/kvquant.rs:381-396): (packed, norm)."""
+    x = _c(x)
+    packed = np.empty(planar_packed_len(x.size, bits), np.uint8)
+    norm = np.empty(1, np.float32)
+    lib().or_planar_quantize(_p(x), x.size, bits, _p(packed), _p(norm))
+    return packed, float(norm[0])
+
+
+def planar_dequantize(packed, norm: float, hd: int, bits: int) -> np.ndarray:
+    """PlanarQuant::dequantize (src/kvquant.rs:399-413)."""
+    packed = _c(packed, np.uint8)
+    out = np.empty(hd, np.float32)
+    lib().or_planar_dequantize(_p(packed), norm, hd, bits, _p(out))
+    return out
+
+
+def planar_dot_rotated(q_rot, packed, norm: float, hd: int, bits: int) -> float:
+    q_rot, packed = _c(q_rot), _c(packed, np.uint8)
+    return float(lib().or_planar_dot_rotated(_p(q_rot), _p(packed), norm, hd, bits))
+
+
+def kv_store_planar(k, v, n_kv: int, hd: int, bits: int, cap: int, pos0: int = 0,
+                    quantize_v: bool = True, caches=None):
+    """AttnCache::append_k_quantized / append_v_quantized / append_v
+    (src/forward.rs:99-140) for rows k, v [n_tok, n_kv * hd] at positions
+    pos0 ..; returns (kq [cap, n_kv, plen] u8, kn [cap, n_kv] f32, vq, vn,
+    v_f32 [cap, n_kv * hd]) -- copies of `caches` when given."""
+    k, v = _c(k), _c(v)
+    n_tok = k.shape[0]
+    plen = planar_packed_len(hd, bits)
+    if caches is None:
+        caches = (np.zeros((cap, n_kv, plen), np.uint8), np.zeros((cap, n_kv), np.float32),
+                  np.zeros((cap, n_kv, plen), np.uint8), np.zeros((cap, n_kv), np.float32),
+                  np.zeros((cap, n_kv * hd), np.float32))
+    kq, kn, vq, vn, vf = (np.ascontiguousarray(a).copy() for a in caches)
+    if k.shape != (n_tok, n_kv * hd) or v.shape != k.shape or pos0 + n_tok > kq.shape[0]:
+        raise OracleShapeError("kv_store_planar shape")
+    lib().or_kv_store_planar(_p(k), _p(v), n_tok, n_kv, hd, bits, _p(kq), _p(kn),
+                             _p(vq) if quantize_v else None, _p(vn) if quantize_v else None,
+                             _p(vf), pos0)
+    return kq, kn, vq, vn, vf
+
+
+def attention_planar(q, pos0: int, kq, kn, vq, vn, v_f32, n_kv: int, bits: int,
+                     quantize_v: bool = True) -> np.ndarray:
+    """The quantized-cache branches of full_attention_layer
+    (src/forward.rs:296-349) for queries q [n_q, n_head, hd] at positions
+    pos0 ..; V from vq / vn when quantize_v, else from v_f32."""
+    q = _c(q)
+    n_q, n_head, hd = q.shape
+    kq, kn = _c(kq, np.uint8), _c(kn)
+    vq, vn, vf = _c(vq, np.uint8), _c(vn), _c(v_f32)
+    out = np.empty_like(q)
+    if lib().or_attention_planar(_p(q), n_q, pos0, _p(kq), _p(kn), _p(vq) if quantize_v else None,
+                                 _p(vn) if quantize_v else None, _p(vf), bits, n_head, n_kv, hd,
+                                 _p(out)) != 0:
+        raise OracleShapeError("attention_planar heads")
     return out
