@@ -28,7 +28,8 @@
  * the softmax tolerance of 2e-5).  The PQ2_0 decode is bit-exact.
  *
  * Threading: every device entry point is re-entrant per stream, except
- * bh_softmax_rows on rows too wide for one workgroup, bh_attention, and the
+ * bh_softmax_rows on rows too wide for one workgroup, bh_attention,
+ * bh_attention_planar, and the
  * PQ2_0 products (bh_pq2_matvec_range, bh_pq2_matmul_n) with more than 4
  * tokens or on shapes outside the integer path, which use per-device
  * scratch buffers: each must not run concurrently with itself on one device.
@@ -199,6 +200,39 @@ int bh_kv_store(const float *k, const float *v, size_t n_tok, size_t n_kv_elems,
 int bh_attention(const float *q, size_t n_q, size_t pos0, const void *k_cache,
                  const void *v_cache, int kv_dtype, size_t n_head, size_t n_kv, size_t hd,
                  float *out, bh_stream stream);
+
+/* Planar-quantized KV cache (src/kvquant.rs, PlanarQuant; BONSAI_KV=planarN
+ * and planarNk).  Per (position, kv head) a cache row holds the norm |x|
+ * (f32) and, for the Givens-rotated unit vector, one Lloyd-Max centroid
+ * index per coordinate packed LSB first at `bits` bits (1..8): kq/vq are
+ * [cap][n_kv][packed_len] bytes, kn/vn [cap][n_kv] f32.  hd = 256 (the
+ * model's head size).  The codebook and rotation table are the reference's
+ * (computed by the library). */
+
+/* Bytes of one packed row: ceil(hd_even * bits / 8) (packed_len,
+ * src/kvquant.rs:332-334). */
+size_t bh_planar_packed_len(size_t hd, unsigned bits);
+
+/* AttnCache::append_k_quantized / append_v_quantized / append_v
+ * (src/forward.rs:99-140): rows k, v [n_tok][n_kv * hd] (f32, 16-byte
+ * aligned) quantized into positions pos0 .. pos0 + n_tok - 1; indices and
+ * norms bit for bit the reference's.  vq = vn = NULL keeps V in f32
+ * (planarNk): v is copied into v_f32 [cap][n_kv * hd].  No scratch. */
+int bh_kv_store_planar(const float *k, const float *v, size_t n_tok, size_t n_kv, size_t hd,
+                       unsigned bits, uint8_t *kq, float *kn, uint8_t *vq, float *vn,
+                       float *v_f32, size_t pos0, bh_stream stream);
+
+/* The quantized-cache branches of full_attention_layer (src/forward.rs
+ * :296-349) for n_q query tokens at positions pos0 ..: q rotated once per
+ * head, score_j = (q_rot . centroids(k_j)) |k_j| / sqrtf(hd), softmax_rows,
+ * V quantized: the (p_j |v_j|)-weighted centroid sum turned back by the
+ * inverse rotation; V in f32 (vq = vn = NULL): p . v_f32.  q, out
+ * [n_q][n_head][hd]; n_head / n_kv in {1, 2, 3, 4, 6, 8}.  Uses library
+ * scratch (like bh_attention). */
+int bh_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *kq,
+                        const float *kn, const uint8_t *vq, const float *vn, const float *v_f32,
+                        unsigned bits, size_t n_head, size_t n_kv, size_t hd, float *out,
+                        bh_stream stream);
 
 /* Gated delta-net recurrence over n_tok tokens (src/gdn.rs:17-77, gdn_step,
  * applied per token; the reference fixes s = 128, h_k = 16, h_v = 48).  Per

@@ -1,7 +1,7 @@
 //! HIP (MI355X / gfx950) versions of the kernels in src/kernels.rs and
 //! src/rope.rs, bound through the C ABI of include/bonsai_hip.h.
 use std::ffi::CStr;
-use std::os::raw::{c_char, c_int, c_void};
+use std::os::raw::{c_char, c_int, c_uint, c_void};
 
 pub type Stream = *mut c_void; // hipStream_t; null = default stream
 
@@ -86,6 +86,14 @@ extern "C" {
     pub fn bh_attention(q: *const f32, n_q: usize, pos0: usize, k_cache: *const c_void,
                         v_cache: *const c_void, kv_dtype: c_int, n_head: usize, n_kv: usize,
                         hd: usize, out: *mut f32, stream: Stream) -> c_int;
+    pub fn bh_planar_packed_len(hd: usize, bits: c_uint) -> usize;
+    pub fn bh_kv_store_planar(k: *const f32, v: *const f32, n_tok: usize, n_kv: usize, hd: usize,
+                              bits: c_uint, kq: *mut u8, kn: *mut f32, vq: *mut u8, vn: *mut f32,
+                              v_f32: *mut f32, pos0: usize, stream: Stream) -> c_int;
+    pub fn bh_attention_planar(q: *const f32, n_q: usize, pos0: usize, kq: *const u8,
+                               kn: *const f32, vq: *const u8, vn: *const f32, v_f32: *const f32,
+                               bits: c_uint, n_head: usize, n_kv: usize, hd: usize, out: *mut f32,
+                               stream: Stream) -> c_int;
     // (remaining bh_* device entry points: see include/bonsai_hip.h)
 }
 

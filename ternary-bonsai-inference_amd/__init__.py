@@ -130,6 +130,11 @@ _SIGNATURES = {
                               _vp, _vp]),
     "bh_gdn_step": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _c_size, _c_size,
                              _c_size, _vp]),
+    "bh_planar_packed_len": (_c_size, [_c_size, ctypes.c_uint]),
+    "bh_kv_store_planar": (_c_int, [_vp, _vp, _c_size, _c_size, _c_size, ctypes.c_uint, _vp, _vp,
+                                    _vp, _vp, _vp, _c_size, _vp]),
+    "bh_attention_planar": (_c_int, [_vp, _c_size, _c_size, _vp, _vp, _vp, _vp, _vp,
+                                     ctypes.c_uint, _c_size, _c_size, _c_size, _vp, _vp]),
     "bh_pq2_matvec_range": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp,
                                      _c_size, _vp, _c_size, _vp]),
     "bh_pq2_matmul_n": (_c_int, [_vp, _c_size, _c_size, ctypes.c_uint64, _c_size, _vp, _c_size,
@@ -374,6 +379,35 @@ def attention(q, pos0: int, k_cache, v_cache, n_kv: int, out=None, stream=None):
     check(lib().bh_attention(q.data_ptr(), n_q, pos0, k_cache.data_ptr(), v_cache.data_ptr(),
                              _kv_dtype(k_cache), n_head, n_kv, hd, out.data_ptr(),
                              _stream(stream)))
+    return out
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def kv_store_planar(k, v, pos0: int, n_kv: int, bits: int, kq, kn, vq=None, vn=None, v_f32=None,
+                    stream=None):
+    """AttnCache::append_k_quantized / append_v_quantized / append_v
+    (src/forward.rs:99-140): rows k, v [n_tok, n_kv * 256] into the planar
+    caches kq [cap, n_kv, plen] u8, kn [cap, n_kv] f32 (and vq / vn, or the
+    f32 v_f32 [cap, n_kv * 256] when vq is None), in place."""
+    n_tok = k.shape[0]
+    check(lib().bh_kv_store_planar(k.data_ptr(), v.data_ptr(), n_tok, n_kv, 256, bits,
+                                   kq.data_ptr(), kn.data_ptr(), _ptr(vq), _ptr(vn), _ptr(v_f32),
+                                   pos0, _stream(stream)))
+
+
+def attention_planar(q, pos0: int, kq, kn, n_kv: int, bits: int, vq=None, vn=None, v_f32=None,
+                     out=None, stream=None):
+    """The quantized-cache branches of full_attention_layer
+    (src/forward.rs:296-349) for q [n_q, n_head, 256] at positions pos0 ..."""
+    import torch
+    n_q, n_head, hd = q.shape
+    out = torch.empty_like(q) if out is None else out
+    check(lib().bh_attention_planar(q.data_ptr(), n_q, pos0, kq.data_ptr(), kn.data_ptr(),
+                                    _ptr(vq), _ptr(vn), _ptr(v_f32), bits, n_head, n_kv, hd,
+                                    out.data_ptr(), _stream(stream)))
     return out
 
 

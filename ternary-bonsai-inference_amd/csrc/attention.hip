@@ -36,6 +36,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "kvquant.hpp"
 
 namespace bh {
 namespace {
@@ -400,11 +401,14 @@ __global__ __launch_bounds__(64 * kCombWaves) void attn_combine_kernel(const flo
 // (max, sum) of chunk c -- then the block's max, the chunk weights (LDS) and
 // the weighted sum are formed from registers.  The general kernel above
 // waits for the maxima, then the sums, then the accumulators.
-template <int kCombWaves, int kCombPer>
-__global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_kernel(const float *pm,
-                                                                     const float *pl,
-                                                                     const float *pacc,
-                                                                     int n_chunks, float *out) {
+// ROT (planar-quantized V, whose sums are formed in rotated space): the
+// merged row is turned back by the inverse Givens rotation of each pair
+// (2i, 2i+1) -- [c a + s b, -s a + c b] (src/kvquant.rs:425-436) -- the
+// partner dimension coming from the neighbouring lane.
+template <int kCombWaves, int kCombPer, bool ROT>
+__device__ __forceinline__ void combine1_body(const float *pm, const float *pl, const float *pacc,
+                                              int n_chunks, float *out, const float *gc,
+                                              const float *gs) {
   constexpr int kMax = kCombWaves * kCombPer;
   static_assert(kMax <= 64 * kCombWaves, "one (max, sum) pair per thread");
   __shared__ float s_w[kMax];
@@ -449,7 +453,249 @@ __global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_kernel(const fl
       dsum += s_l[i];
       nsum += s_red[i][lane];
     }
-    out[row * kHd + blockIdx.z * kCombDims + lane] = nsum * (1.0f / dsum);
+    const float val = nsum * (1.0f / dsum);
+    const int d = static_cast<int>(blockIdx.z) * kCombDims + lane;
+    if constexpr (ROT) {
+      const float other = __shfl_xor(val, 1, 64);
+      const float c = gc[d >> 1], sn = gs[d >> 1];
+      out[row * kHd + d] = (d & 1) == 0 ? c * val + sn * other : -sn * other + c * val;
+    } else {
+      out[row * kHd + d] = val;
+    }
+  }
+}
+
+template <int kCombWaves, int kCombPer>
+__global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_kernel(const float *pm,
+                                                                     const float *pl,
+                                                                     const float *pacc,
+                                                                     int n_chunks, float *out) {
+  combine1_body<kCombWaves, kCombPer, false>(pm, pl, pacc, n_chunks, out, nullptr, nullptr);
+}
+
+template <int kCombWaves, int kCombPer>
+__global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_rot_kernel(
+    const float *pm, const float *pl, const float *pacc, int n_chunks, float *out, PlanarTables tb) {
+  combine1_body<kCombWaves, kCombPer, true>(pm, pl, pacc, n_chunks, out, tb.gc, tb.gs);
+}
+
+// ---- planar-quantized caches (src/forward.rs:296-349, src/kvquant.rs) -------
+//
+// K (and V, unless the cache keeps V in f32: BONSAI_KV=planarNk) hold per
+// (position, kv head) a norm and 256 packed centroid indices of the rotated
+// unit vector (kvquant.hip).  Block (chunk, kv head, query) of 256 lanes:
+// the REP q rows of the kv head are rotated once into LDS (the reference
+// rotates q and dots it against centroids, src/kvquant.rs:444-460); per
+// tile of 32 positions the packed K (and V) rows are staged in LDS and
+// unpacked to one index byte per coordinate; a score is 16 lanes x 16
+// coordinates of q_rot . centroid (DPP row sums) times the norm and
+// 1/sqrt(hd); the running (max, sum) per head and the P.V accumulation
+// follow the f32 decode kernel, the quantized V term being (e_j |v_j|) *
+// centroid (in rotated space).  Chunks merge in attn_combine1_rot_kernel,
+// which also applies the inverse rotation (a V cache in f32 merges plainly).
+constexpr int kPlTile = 32;
+
+struct PlanarArgs {
+  const float *q;
+  const uint8_t *kq;
+  const float *kn;
+  const uint8_t *vq;  // null: V in f32 (vf)
+  const float *vn;
+  const float *vf;
+  float *pm, *pl, *pacc;
+  size_t pos0, chunk;
+  int n_head, n_chunks, n_kv, bits;
+  float scale;
+};
+
+// Unpacks nt rows of 32 * bits bytes (LSB-first indices) from src into one
+// byte per coordinate in dst[row][256]; the block's 256 lanes share the work.
+__device__ __forceinline__ void planar_unpack_tile(const uint8_t *src, uint8_t (*dst)[kPlanarHd], int nt,
+                                                   int bits) {
+  const uint32_t mask = (1u << bits) - 1u;
+  const int plen = 32 * bits;
+  for (int e = threadIdx.x; e < nt * kPlanarHd; e += kBlock) {
+    const int r = e / kPlanarHd, i = e % kPlanarHd;
+    const int bp = i * bits, by = bp >> 3, off = bp & 7;
+    uint32_t v = src[r * plen + by];
+    if (off + bits > 8) v |= static_cast<uint32_t>(src[r * plen + by + 1]) << 8;
+    dst[r][i] = static_cast<uint8_t>((v >> off) & mask);
+  }
+}
+
+template <int REP>
+__global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, PlanarTables tb) {
+  constexpr int kSlots = (REP + 3) / 4;
+  __shared__ float s_c[256];
+  __shared__ float s_q[REP][kPlanarHd];
+  __shared__ uint32_t s_kraw[kPlTile * 64];  // packed rows, up to 256 bytes each
+  __shared__ uint32_t s_vraw[kPlTile * 64];
+  __shared__ uint8_t s_ki[kPlTile][kPlanarHd];
+  __shared__ uint8_t s_vi[kPlTile][kPlanarHd];
+  __shared__ float s_kn[kPlTile], s_vn[kPlTile];
+  __shared__ float s_e[kPlTile][REP];
+  __shared__ float s_corr[REP];
+  __shared__ float s_acc[4][REP][kPlanarHd];
+  const int c = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
+  const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
+  const bool vquant = a.vq != nullptr;
+  const int plen = 32 * a.bits, pw = plen / 4;  // packed row in bytes / dwords
+  const size_t n_pos = a.pos0 + i + 1;
+  const size_t beg = static_cast<size_t>(c) * a.chunk;
+  const size_t end = beg + a.chunk < n_pos ? beg + a.chunk : n_pos;
+  const size_t part0 = (static_cast<size_t>(i) * a.n_head + static_cast<size_t>(g) * REP) * a.n_chunks + c;
+  if (beg >= end) {  // this query has no positions in the chunk
+    if (tid < REP) {
+      a.pm[part0 + static_cast<size_t>(tid) * a.n_chunks] = -INFINITY;
+      a.pl[part0 + static_cast<size_t>(tid) * a.n_chunks] = 0.0f;
+    }
+    for (int o = tid; o < REP * kHd; o += kBlock)
+      a.pacc[(part0 + static_cast<size_t>(o / kHd) * a.n_chunks) * kHd + o % kHd] = 0.0f;
+    return;
+  }
+  s_c[tid] = tb.cent[tid];
+  // q rows of the kv head's REP heads, rotated: pair p of head r
+  for (int o = tid; o < REP * kPlanarHd / 2; o += kBlock) {
+    const int r = o / (kPlanarHd / 2), pp = o % (kPlanarHd / 2);
+    const float2 qa = reinterpret_cast<const float2 *>(
+        a.q + (static_cast<size_t>(i) * a.n_head + g * REP + r) * kPlanarHd)[pp];
+    const float cc = tb.gc[pp], sn = tb.gs[pp];
+    s_q[r][2 * pp] = cc * qa.x - sn * qa.y;  // src/kvquant.rs:356-366
+    s_q[r][2 * pp + 1] = sn * qa.x + cc * qa.y;
+  }
+  float run_m[kSlots], run_l[kSlots];
+#pragma unroll
+  for (int u = 0; u < kSlots; ++u) {
+    run_m[u] = -INFINITY;
+    run_l[u] = 0.0f;
+  }
+  float acc[REP][4];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) acc[r][x] = 0.0f;
+  const int grp = tid / kQkLanes, sub = tid % kQkLanes;
+  const uint32_t *kq32 = reinterpret_cast<const uint32_t *>(a.kq);
+  const uint32_t *vq32 = reinterpret_cast<const uint32_t *>(a.vq);
+
+  for (size_t t0 = beg; t0 < end; t0 += kPlTile) {
+    const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kPlTile) ? end - t0 : kPlTile);
+    __syncthreads();  // the previous tile's LDS is consumed (first tile: s_q, s_c written)
+    for (int o = tid; o < nt * pw; o += kBlock) {
+      const int r = o / pw, x = o % pw;
+      const size_t row = (t0 + r) * a.n_kv + g;
+      s_kraw[o] = kq32[row * pw + x];
+      if (vquant) s_vraw[o] = vq32[row * pw + x];
+    }
+    if (tid < nt) {
+      const size_t row = (t0 + tid) * a.n_kv + g;
+      s_kn[tid] = a.kn[row];
+      if (vquant) s_vn[tid] = a.vn[row];
+    }
+    __syncthreads();
+    planar_unpack_tile(reinterpret_cast<const uint8_t *>(s_kraw), s_ki, nt, a.bits);
+    if (vquant) planar_unpack_tile(reinterpret_cast<const uint8_t *>(s_vraw), s_vi, nt, a.bits);
+    __syncthreads();
+    // scores: 16 lanes per position (16 coordinates each), two passes of 16
+#pragma unroll
+    for (int pass = 0; pass < kPlTile / 16; ++pass) {
+      const int p = pass * 16 + grp;
+      const int pr = p < nt ? p : nt - 1;
+      float cv[16];
+      const uint4 ib = *reinterpret_cast<const uint4 *>(&s_ki[pr][16 * sub]);
+      const uint32_t iw[4] = {ib.x, ib.y, ib.z, ib.w};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) cv[e] = s_c[(iw[e >> 2] >> (8 * (e & 3))) & 0xffu];
+      const float kscale = s_kn[pr] * a.scale;
+#pragma unroll
+      for (int r = 0; r < REP; ++r) {
+        const float *qr = &s_q[r][16 * sub];
+        float s0 = qr[0] * cv[0], s1 = qr[8] * cv[8];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) {
+          s0 = fmaf(qr[e], cv[e], s0);
+          s1 = fmaf(qr[8 + e], cv[8 + e], s1);
+        }
+        const float d = row16_sum(s0 + s1);
+        // src/forward.rs:307: dot_rotated (times the norm) * scale
+        if (sub == 0) s_e[p][r] = p < nt ? d * kscale : -INFINITY;
+      }
+    }
+    // the wave's f32 V rows of the tile (V kept in f32)
+    float4 vr[kPlTile / 4];
+    if (!vquant) {
+#pragma unroll
+      for (int jj = 0; jj < kPlTile / 4; ++jj) {
+        const int j = w + 4 * jj;
+        vr[jj] = reinterpret_cast<const float4 *>(
+            a.vf + ((t0 + (j < nt ? j : nt - 1)) * a.n_kv + g) * kPlanarHd)[lane];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kSlots; ++u) {
+      const int r = w + 4 * u;
+      if (r < REP) {
+        const float sc = lane < kPlTile ? s_e[lane][r] : -INFINITY;
+        const float m_new = fmaxf(run_m[u], wave_max(sc));
+        const bool none = m_new == -INFINITY;
+        const float corr = none ? 1.0f : expf(run_m[u] - m_new);
+        const float e = none ? 0.0f : expf(sc - m_new);
+        if (lane < kPlTile) s_e[lane][r] = e;
+        run_l[u] = run_l[u] * corr + wave_sum(e);
+        run_m[u] = m_new;
+        if (lane == 0) s_corr[r] = corr;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < REP; ++r) {
+      const float cr = s_corr[r];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) acc[r][x] *= cr;
+    }
+    // P.V: lane owns dims 4 lane .. +3, wave w takes positions w, w + 4, ...
+#pragma unroll
+    for (int jj = 0; jj < kPlTile / 4; ++jj) {
+      const int j = w + 4 * jj;
+      if (j < nt) {
+        float4 v;
+        float vs = 1.0f;
+        if (vquant) {
+          const uint32_t ix = *reinterpret_cast<const uint32_t *>(&s_vi[j][4 * lane]);
+          v = make_float4(s_c[ix & 0xffu], s_c[(ix >> 8) & 0xffu], s_c[(ix >> 16) & 0xffu], s_c[ix >> 24]);
+          vs = s_vn[j];
+        } else {
+          v = vr[jj];
+        }
+#pragma unroll
+        for (int r = 0; r < REP; ++r) {
+          const float e = vquant ? s_e[j][r] * vs : s_e[j][r];  // (p_j |v_j|) (src/forward.rs:344)
+          acc[r][0] = fmaf(e, v.x, acc[r][0]);
+          acc[r][1] = fmaf(e, v.y, acc[r][1]);
+          acc[r][2] = fmaf(e, v.z, acc[r][2]);
+          acc[r][3] = fmaf(e, v.w, acc[r][3]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) s_acc[w][r][4 * lane + x] = acc[r][x];
+#pragma unroll
+  for (int u = 0; u < kSlots; ++u) {
+    const int r = w + 4 * u;
+    if (r < REP && lane == 0) {
+      a.pm[part0 + static_cast<size_t>(r) * a.n_chunks] = run_m[u];
+      a.pl[part0 + static_cast<size_t>(r) * a.n_chunks] = run_l[u];
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < REP * kHd; o += kBlock) {
+    const int r = o / kHd, d = o % kHd;
+    const float sum = (s_acc[0][r][d] + s_acc[1][r][d]) + (s_acc[2][r][d] + s_acc[3][r][d]);
+    a.pacc[(part0 + static_cast<size_t>(r) * a.n_chunks) * kHd + d] = sum;
   }
 }
 
@@ -1170,6 +1416,75 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
   } else {
     BH_LAUNCH(attn_probs_kernel<float>, grid, kBlock, 0, st, a);
     BH_LAUNCH(attn_pv_kernel<float>, grid_pv, kBlock, 0, st, a);
+  }
+  return ok();
+}
+
+extern "C" int bh_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *kq,
+                                   const float *kn, const uint8_t *vq, const float *vn,
+                                   const float *v_f32, unsigned bits, size_t n_head, size_t n_kv,
+                                   size_t hd, float *out, bh_stream stream) {
+  if (bits < 1 || bits > 8) return fail(BH_ERR_ARG, "attention_planar: bits must be 1..8");
+  if (n_kv == 0 || n_head == 0 || n_head % n_kv != 0)
+    return fail(BH_ERR_SHAPE, "attention_planar: n_head " + std::to_string(n_head) +
+                                  " must be a positive multiple of n_kv " + std::to_string(n_kv));
+  if (hd != static_cast<size_t>(kPlanarHd))
+    return fail(BH_ERR_SHAPE, "attention_planar: head_dim must be 256 (got " + std::to_string(hd) + ")");
+  if ((vq == nullptr) != (vn == nullptr))
+    return fail(BH_ERR_ARG, "attention_planar: vq and vn go together (quantized V) or are both null");
+  const size_t rep = n_head / n_kv;
+  if (!decode_rep(rep)) return fail(BH_ERR_ARG, "attention_planar: no kernel for this grouping");
+  if (n_q == 0) return ok();
+  if (!q || !kq || !kn || !out || (vq == nullptr && v_f32 == nullptr))
+    return fail(BH_ERR_ARG, "attention_planar: null pointer");
+  if (!aligned16(q) || (reinterpret_cast<uintptr_t>(kq) & 3u) != 0 ||
+      (vq != nullptr && (reinterpret_cast<uintptr_t>(vq) & 3u) != 0) ||
+      (vq == nullptr && !aligned16(v_f32)))
+    return fail(BH_ERR_ARG, "attention_planar: q and v_f32 16-byte, kq and vq 4-byte aligned");
+  const size_t n_max = pos0 + n_q;
+  if (n_head > 65535 || n_q > 65535 || n_kv > 65535 || n_max > (size_t{1} << 40))
+    return fail(BH_ERR_SHAPE, "attention_planar: sizes out of range");
+  PlanarTables tb;
+  if (!planar_tables(hd, bits, &tb)) return fail(BH_ERR_ARG, "attention_planar: no tables");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // chunks of whole tiles: about 512 blocks for one query, 2048 for several,
+  // and at most 128 chunks (the one-round-trip merge)
+  const size_t blocks = n_q == 1 ? 512 : 2048;
+  const size_t tiles = (n_max + kPlTile - 1) / kPlTile;
+  size_t want = (blocks + n_kv * n_q - 1) / (n_kv * n_q);
+  want = want < 128 ? want : 128;
+  const size_t per = (tiles + want - 1) / want;
+  const size_t chunk = per * kPlTile;
+  const size_t n_chunks = (n_max + chunk - 1) / chunk;
+  size_t rows = 0, sbytes = 0;
+  if (!mul_size(n_q, n_head, n_chunks, &rows) || !mul_size(rows, kHd + 2, 4, &sbytes))
+    return fail(BH_ERR_SHAPE, "attention_planar: scratch size overflows");
+  float *scratch = static_cast<float *>(device_scratch(sbytes, kScratchAttention, st));
+  if (scratch == nullptr) return BH_ERR_HIP;
+  PlanarArgs a{q,       kq,   kn,    vq, vn, v_f32, scratch, scratch + rows, scratch + 2 * rows,
+               pos0,    chunk, static_cast<int>(n_head), static_cast<int>(n_chunks),
+               static_cast<int>(n_kv), static_cast<int>(bits), 1.0f / sqrtf(static_cast<float>(hd))};
+  const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_kv), static_cast<unsigned>(n_q));
+  switch (rep) {
+    case 1: BH_LAUNCH(attn_planar_kernel<1>, grid, kBlock, 0, st, a, tb); break;
+    case 2: BH_LAUNCH(attn_planar_kernel<2>, grid, kBlock, 0, st, a, tb); break;
+    case 3: BH_LAUNCH(attn_planar_kernel<3>, grid, kBlock, 0, st, a, tb); break;
+    case 4: BH_LAUNCH(attn_planar_kernel<4>, grid, kBlock, 0, st, a, tb); break;
+    case 6: BH_LAUNCH(attn_planar_kernel<6>, grid, kBlock, 0, st, a, tb); break;
+    default: BH_LAUNCH(attn_planar_kernel<8>, grid, kBlock, 0, st, a, tb); break;
+  }
+  const dim3 cgrid(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims);
+  const int nc = static_cast<int>(n_chunks);
+  if (vq != nullptr) {
+    if (n_chunks <= 32)
+      BH_LAUNCH((attn_combine1_rot_kernel<4, 8>), cgrid, 256, 0, st, a.pm, a.pl, a.pacc, nc, out, tb);
+    else
+      BH_LAUNCH((attn_combine1_rot_kernel<16, 8>), cgrid, 1024, 0, st, a.pm, a.pl, a.pacc, nc, out, tb);
+  } else {
+    if (n_chunks <= 32)
+      BH_LAUNCH((attn_combine1_kernel<4, 8>), cgrid, 256, 0, st, a.pm, a.pl, a.pacc, nc, out);
+    else
+      BH_LAUNCH((attn_combine1_kernel<16, 8>), cgrid, 1024, 0, st, a.pm, a.pl, a.pacc, nc, out);
   }
   return ok();
 }
