@@ -310,6 +310,48 @@ def wl_attention(bh, synth, dev, stream, n_q, pos0, f16, n_head=24, n_kv=4, hd=2
     return launch, len(sets), bytes_per, n_q, sets
 
 
+def wl_attention_planar(bh, synth, dev, stream, n_q, pos0, bits, quantize_v=True, n_head=24,
+                        n_kv=4, hd=256):
+    """Attention over a planar-quantized KV cache (BONSAI_KV=planarN,
+    src/forward.rs:296-349, src/kvquant.rs) on the model's heads.  The caches
+    are filled by bh_kv_store_planar at setup (untimed).  Algorithmic bytes:
+    the packed rows and norms of K (and V, or V's f32 rows) of positions
+    0 .. pos0+n_q-1 read once, q read and out written once."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(10)
+    n_pos = pos0 + n_q
+    plen = bh.lib().bh_planar_packed_len(hd, bits)
+    kv_bytes = n_pos * n_kv * (plen + 4)
+    bytes_per = kv_bytes + (kv_bytes if quantize_v else n_pos * n_kv * hd * 4) + \
+        2 * n_q * n_head * hd * 4
+    sets = []
+    for _ in range(n_sets(bytes_per)):
+        k = torch.randn((n_pos, n_kv * hd), device=dev, generator=g)
+        v = torch.randn((n_pos, n_kv * hd), device=dev, generator=g)
+        kq = torch.empty((n_pos, n_kv, plen), dtype=torch.uint8, device=dev)
+        kn = torch.empty((n_pos, n_kv), device=dev)
+        vq = torch.empty_like(kq) if quantize_v else None
+        vn = torch.empty_like(kn) if quantize_v else None
+        vf = None if quantize_v else torch.empty((n_pos, n_kv * hd), device=dev)
+        bh.kv_store_planar(k, v, 0, n_kv, bits, kq, kn, vq, vn, vf, stream=stream)
+        del k, v
+        sets.append((torch.randn((n_q, n_head, hd), device=dev, generator=g), kq, kn, vq, vn, vf,
+                     torch.empty((n_q, n_head, hd), device=dev)))
+    torch.cuda.synchronize()
+    lib, sh = bh.lib(), stream.cuda_stream
+    ptr = lambda t: None if t is None else t.data_ptr()
+
+    def launch(i):
+        q, kq, kn, vq, vn, vf, out = sets[i]
+        st = lib.bh_attention_planar(q.data_ptr(), n_q, pos0, kq.data_ptr(), kn.data_ptr(),
+                                     ptr(vq), ptr(vn), ptr(vf), bits, n_head, n_kv, hd,
+                                     out.data_ptr(), sh)
+        if st:
+            bh.check(st)
+    return launch, len(sets), bytes_per, n_q, sets
+
+
 def wl_pq2_matmul(bh, synth, dev, stream, n_rows, ne0, n_tok):
     """kernels::pq2_matmul_n / pq2_matvec_range (src/kernels.rs:283-423):
     Y[n_tok][n_rows] = X[n_tok][ne0] * W^T over a PQ2_0 weight tensor.  Each
@@ -608,6 +650,10 @@ def main() -> int:
                  lambda: wl_attention(bh, synth, dev, stream, 1, 32767, True)),
                 ("attention batch 64 queries ctx=4096 f32",
                  lambda: wl_attention(bh, synth, dev, stream, 64, 4032, False)),
+                ("attention decode ctx=32768 planar4",
+                 lambda: wl_attention_planar(bh, synth, dev, stream, 1, 32767, 4)),
+                ("attention decode ctx=4096 planar4",
+                 lambda: wl_attention_planar(bh, synth, dev, stream, 1, 4095, 4)),
             ]
             products = [  # (name, rows, ne0, tokens): decode matvecs and batched products
                 ("pq2_matvec LM head [248320x5120] N=1", 248320, 5120, 1),

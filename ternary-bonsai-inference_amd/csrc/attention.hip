@@ -483,17 +483,20 @@ __global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_rot_kernel(
 //
 // K (and V, unless the cache keeps V in f32: BONSAI_KV=planarNk) hold per
 // (position, kv head) a norm and 256 packed centroid indices of the rotated
-// unit vector (kvquant.hip).  Block (chunk, kv head, query) of 256 lanes:
-// the REP q rows of the kv head are rotated once into LDS (the reference
-// rotates q and dots it against centroids, src/kvquant.rs:444-460); per
-// tile of 32 positions the packed K (and V) rows are staged in LDS and
-// unpacked to one index byte per coordinate; a score is 16 lanes x 16
-// coordinates of q_rot . centroid (DPP row sums) times the norm and
-// 1/sqrt(hd); the running (max, sum) per head and the P.V accumulation
-// follow the f32 decode kernel, the quantized V term being (e_j |v_j|) *
-// centroid (in rotated space).  Chunks merge in attn_combine1_rot_kernel,
-// which also applies the inverse rotation (a V cache in f32 merges plainly).
-constexpr int kPlTile = 32;
+// unit vector (kvquant.hip).  Block (chunk, kv head, query) of 256 lanes,
+// the f32 decode kernel's layout: the REP q rows of the kv head are rotated
+// once into LDS (the reference rotates q and dots it against centroids,
+// src/kvquant.rs:444-460); per tile of 64 positions a score is 16 lanes x 16
+// coordinates: each lane reads its 2 BITS bytes of the packed row straight
+// from memory (16 lanes read a row's 32 BITS contiguous bytes), looks the 16
+// centroids up in LDS and dots them with q_rot (DPP row sums), times the
+// norm and 1/sqrt(hd).  The running (max, sum) per head and the P.V
+// accumulation follow the f32 decode kernel, the quantized V term being
+// (e_j |v_j|) * centroid: lane l owns dims 4l .. 4l+3, whose 4 BITS index
+// bits it reads from one or two dwords.  Chunks merge in
+// attn_combine1_rot_kernel, which also applies the inverse rotation (a V
+// cache in f32 merges plainly).
+constexpr int kPlTile = 64;
 
 struct PlanarArgs {
   const float *q;
@@ -508,30 +511,14 @@ struct PlanarArgs {
   float scale;
 };
 
-// Unpacks nt rows of 32 * bits bytes (LSB-first indices) from src into one
-// byte per coordinate in dst[row][256]; the block's 256 lanes share the work.
-__device__ __forceinline__ void planar_unpack_tile(const uint8_t *src, uint8_t (*dst)[kPlanarHd], int nt,
-                                                   int bits) {
-  const uint32_t mask = (1u << bits) - 1u;
-  const int plen = 32 * bits;
-  for (int e = threadIdx.x; e < nt * kPlanarHd; e += kBlock) {
-    const int r = e / kPlanarHd, i = e % kPlanarHd;
-    const int bp = i * bits, by = bp >> 3, off = bp & 7;
-    uint32_t v = src[r * plen + by];
-    if (off + bits > 8) v |= static_cast<uint32_t>(src[r * plen + by + 1]) << 8;
-    dst[r][i] = static_cast<uint8_t>((v >> off) & mask);
-  }
-}
-
-template <int REP>
+template <int REP, int BITS>
 __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, PlanarTables tb) {
   constexpr int kSlots = (REP + 3) / 4;
+  constexpr int kPlen = 32 * BITS;         // packed row bytes
+  constexpr uint32_t kMask = (1u << BITS) - 1u;
+  constexpr int kPasses = kPlTile / 16;
   __shared__ float s_c[256];
   __shared__ float s_q[REP][kPlanarHd];
-  __shared__ uint32_t s_kraw[kPlTile * 64];  // packed rows, up to 256 bytes each
-  __shared__ uint32_t s_vraw[kPlTile * 64];
-  __shared__ uint8_t s_ki[kPlTile][kPlanarHd];
-  __shared__ uint8_t s_vi[kPlTile][kPlanarHd];
   __shared__ float s_kn[kPlTile], s_vn[kPlTile];
   __shared__ float s_e[kPlTile][REP];
   __shared__ float s_corr[REP];
@@ -539,7 +526,6 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
   const int c = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
   const bool vquant = a.vq != nullptr;
-  const int plen = 32 * a.bits, pw = plen / 4;  // packed row in bytes / dwords
   const size_t n_pos = a.pos0 + i + 1;
   const size_t beg = static_cast<size_t>(c) * a.chunk;
   const size_t end = beg + a.chunk < n_pos ? beg + a.chunk : n_pos;
@@ -575,38 +561,36 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
 #pragma unroll
     for (int x = 0; x < 4; ++x) acc[r][x] = 0.0f;
   const int grp = tid / kQkLanes, sub = tid % kQkLanes;
-  const uint32_t *kq32 = reinterpret_cast<const uint32_t *>(a.kq);
-  const uint32_t *vq32 = reinterpret_cast<const uint32_t *>(a.vq);
 
   for (size_t t0 = beg; t0 < end; t0 += kPlTile) {
     const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kPlTile) ? end - t0 : kPlTile);
-    __syncthreads();  // the previous tile's LDS is consumed (first tile: s_q, s_c written)
-    for (int o = tid; o < nt * pw; o += kBlock) {
-      const int r = o / pw, x = o % pw;
-      const size_t row = (t0 + r) * a.n_kv + g;
-      s_kraw[o] = kq32[row * pw + x];
-      if (vquant) s_vraw[o] = vq32[row * pw + x];
+    // this lane's 16 K indices of each pass's position: 2 BITS bytes at byte
+    // 2 BITS sub of the packed row (even, so read as BITS halfwords)
+    uint16_t kw[kPasses][BITS];
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int p = pass * 16 + grp;
+      const size_t row = (t0 + (p < nt ? p : nt - 1)) * a.n_kv + g;
+      const uint16_t *src = reinterpret_cast<const uint16_t *>(a.kq + row * kPlen) + BITS * sub;
+#pragma unroll
+      for (int h = 0; h < BITS; ++h) kw[pass][h] = src[h];
     }
     if (tid < nt) {
       const size_t row = (t0 + tid) * a.n_kv + g;
       s_kn[tid] = a.kn[row];
       if (vquant) s_vn[tid] = a.vn[row];
     }
-    __syncthreads();
-    planar_unpack_tile(reinterpret_cast<const uint8_t *>(s_kraw), s_ki, nt, a.bits);
-    if (vquant) planar_unpack_tile(reinterpret_cast<const uint8_t *>(s_vraw), s_vi, nt, a.bits);
-    __syncthreads();
-    // scores: 16 lanes per position (16 coordinates each), two passes of 16
+    __syncthreads();  // s_q / s_c (first tile), s_kn, s_vn; the previous tile's s_e consumed
 #pragma unroll
-    for (int pass = 0; pass < kPlTile / 16; ++pass) {
+    for (int pass = 0; pass < kPasses; ++pass) {
       const int p = pass * 16 + grp;
-      const int pr = p < nt ? p : nt - 1;
-      float cv[16];
-      const uint4 ib = *reinterpret_cast<const uint4 *>(&s_ki[pr][16 * sub]);
-      const uint32_t iw[4] = {ib.x, ib.y, ib.z, ib.w};
+      unsigned __int128 win = 0;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) cv[e] = s_c[(iw[e >> 2] >> (8 * (e & 3))) & 0xffu];
-      const float kscale = s_kn[pr] * a.scale;
+      for (int h = 0; h < BITS; ++h) win |= static_cast<unsigned __int128>(kw[pass][h]) << (16 * h);
+      float cv[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) cv[e] = s_c[static_cast<uint32_t>(win >> (e * BITS)) & kMask];
+      const float kscale = s_kn[p < nt ? p : nt - 1] * a.scale;
 #pragma unroll
       for (int r = 0; r < REP; ++r) {
         const float *qr = &s_q[r][16 * sub];
@@ -621,14 +605,23 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
         if (sub == 0) s_e[p][r] = p < nt ? d * kscale : -INFINITY;
       }
     }
-    // the wave's f32 V rows of the tile (V kept in f32)
+    // the wave's V data of the tile, issued now so its latency overlaps the
+    // softmax step: index bits [4 lane BITS, +4 BITS) of each row (one or two
+    // dwords), or the f32 rows
+    uint32_t vlo[kPlTile / 4], vhi[kPlTile / 4];
     float4 vr[kPlTile / 4];
-    if (!vquant) {
+    const int vbit = 4 * lane * BITS, vdw = vbit >> 5, vsh = vbit & 31;
+    const bool two = vsh + 4 * BITS > 32;
 #pragma unroll
-      for (int jj = 0; jj < kPlTile / 4; ++jj) {
-        const int j = w + 4 * jj;
-        vr[jj] = reinterpret_cast<const float4 *>(
-            a.vf + ((t0 + (j < nt ? j : nt - 1)) * a.n_kv + g) * kPlanarHd)[lane];
+    for (int jj = 0; jj < kPlTile / 4; ++jj) {
+      const int j = w + 4 * jj;
+      const size_t row = (t0 + (j < nt ? j : nt - 1)) * a.n_kv + g;
+      if (vquant) {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.vq + row * kPlen) + vdw;
+        vlo[jj] = src[0];
+        vhi[jj] = two ? src[1] : 0u;
+      } else {
+        vr[jj] = reinterpret_cast<const float4 *>(a.vf + row * kPlanarHd)[lane];
       }
     }
     __syncthreads();
@@ -636,12 +629,12 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
     for (int u = 0; u < kSlots; ++u) {
       const int r = w + 4 * u;
       if (r < REP) {
-        const float sc = lane < kPlTile ? s_e[lane][r] : -INFINITY;
+        const float sc = s_e[lane][r];
         const float m_new = fmaxf(run_m[u], wave_max(sc));
         const bool none = m_new == -INFINITY;
         const float corr = none ? 1.0f : expf(run_m[u] - m_new);
         const float e = none ? 0.0f : expf(sc - m_new);
-        if (lane < kPlTile) s_e[lane][r] = e;
+        s_e[lane][r] = e;
         run_l[u] = run_l[u] * corr + wave_sum(e);
         run_m[u] = m_new;
         if (lane == 0) s_corr[r] = corr;
@@ -662,8 +655,9 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
         float4 v;
         float vs = 1.0f;
         if (vquant) {
-          const uint32_t ix = *reinterpret_cast<const uint32_t *>(&s_vi[j][4 * lane]);
-          v = make_float4(s_c[ix & 0xffu], s_c[(ix >> 8) & 0xffu], s_c[(ix >> 16) & 0xffu], s_c[ix >> 24]);
+          const uint64_t bitsv = ((static_cast<uint64_t>(vhi[jj]) << 32) | vlo[jj]) >> vsh;
+          v = make_float4(s_c[bitsv & kMask], s_c[(bitsv >> BITS) & kMask],
+                          s_c[(bitsv >> (2 * BITS)) & kMask], s_c[(bitsv >> (3 * BITS)) & kMask]);
           vs = s_vn[j];
         } else {
           v = vr[jj];
@@ -697,6 +691,21 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
     const float sum = (s_acc[0][r][d] + s_acc[1][r][d]) + (s_acc[2][r][d] + s_acc[3][r][d]);
     a.pacc[(part0 + static_cast<size_t>(r) * a.n_chunks) * kHd + d] = sum;
   }
+}
+
+template <int REP>
+int launch_planar(const PlanarArgs &a, dim3 grid, const PlanarTables &tb, hipStream_t st) {
+  switch (a.bits) {
+    case 1: BH_LAUNCH((attn_planar_kernel<REP, 1>), grid, kBlock, 0, st, a, tb); break;
+    case 2: BH_LAUNCH((attn_planar_kernel<REP, 2>), grid, kBlock, 0, st, a, tb); break;
+    case 3: BH_LAUNCH((attn_planar_kernel<REP, 3>), grid, kBlock, 0, st, a, tb); break;
+    case 4: BH_LAUNCH((attn_planar_kernel<REP, 4>), grid, kBlock, 0, st, a, tb); break;
+    case 5: BH_LAUNCH((attn_planar_kernel<REP, 5>), grid, kBlock, 0, st, a, tb); break;
+    case 6: BH_LAUNCH((attn_planar_kernel<REP, 6>), grid, kBlock, 0, st, a, tb); break;
+    case 7: BH_LAUNCH((attn_planar_kernel<REP, 7>), grid, kBlock, 0, st, a, tb); break;
+    default: BH_LAUNCH((attn_planar_kernel<REP, 8>), grid, kBlock, 0, st, a, tb); break;
+  }
+  return ok();
 }
 
 // ---- multi-query path (matrix cores) ---------------------------------------
@@ -1465,14 +1474,16 @@ extern "C" int bh_attention_planar(const float *q, size_t n_q, size_t pos0, cons
                pos0,    chunk, static_cast<int>(n_head), static_cast<int>(n_chunks),
                static_cast<int>(n_kv), static_cast<int>(bits), 1.0f / sqrtf(static_cast<float>(hd))};
   const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_kv), static_cast<unsigned>(n_q));
+  int e = BH_OK;
   switch (rep) {
-    case 1: BH_LAUNCH(attn_planar_kernel<1>, grid, kBlock, 0, st, a, tb); break;
-    case 2: BH_LAUNCH(attn_planar_kernel<2>, grid, kBlock, 0, st, a, tb); break;
-    case 3: BH_LAUNCH(attn_planar_kernel<3>, grid, kBlock, 0, st, a, tb); break;
-    case 4: BH_LAUNCH(attn_planar_kernel<4>, grid, kBlock, 0, st, a, tb); break;
-    case 6: BH_LAUNCH(attn_planar_kernel<6>, grid, kBlock, 0, st, a, tb); break;
-    default: BH_LAUNCH(attn_planar_kernel<8>, grid, kBlock, 0, st, a, tb); break;
+    case 1: e = launch_planar<1>(a, grid, tb, st); break;
+    case 2: e = launch_planar<2>(a, grid, tb, st); break;
+    case 3: e = launch_planar<3>(a, grid, tb, st); break;
+    case 4: e = launch_planar<4>(a, grid, tb, st); break;
+    case 6: e = launch_planar<6>(a, grid, tb, st); break;
+    default: e = launch_planar<8>(a, grid, tb, st); break;
   }
+  if (e) return e;
   const dim3 cgrid(static_cast<unsigned>(n_head), static_cast<unsigned>(n_q), kHd / kCombDims);
   const int nc = static_cast<int>(n_chunks);
   if (vq != nullptr) {
