@@ -511,12 +511,17 @@ struct PlanarArgs {
   float scale;
 };
 
-template <int REP, int BITS>
+template <int REP, int BITS, bool VQ>
 __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, PlanarTables tb) {
   constexpr int kSlots = (REP + 3) / 4;
   constexpr int kPlen = 32 * BITS;         // packed row bytes
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   constexpr int kPasses = kPlTile / 16;
+  // a lane's 2 BITS bytes of a packed K row: BITS / 2 dwords (even BITS) or
+  // BITS halfwords, at byte 2 BITS sub
+  constexpr bool kDw = BITS % 2 == 0;
+  constexpr int kWords = kDw ? BITS / 2 : BITS;
+  constexpr int kWordBits = kDw ? 32 : 16;
   __shared__ float s_c[256];
   __shared__ float s_q[REP][kPlanarHd];
   __shared__ float s_kn[kPlTile], s_vn[kPlTile];
@@ -525,7 +530,6 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
   __shared__ float s_acc[4][REP][kPlanarHd];
   const int c = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
-  const bool vquant = a.vq != nullptr;
   const size_t n_pos = a.pos0 + i + 1;
   const size_t beg = static_cast<size_t>(c) * a.chunk;
   const size_t end = beg + a.chunk < n_pos ? beg + a.chunk : n_pos;
@@ -549,6 +553,22 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
     s_q[r][2 * pp] = cc * qa.x - sn * qa.y;  // src/kvquant.rs:356-366
     s_q[r][2 * pp + 1] = sn * qa.x + cc * qa.y;
   }
+  __syncthreads();
+  const int grp = tid / kQkLanes, sub = tid % kQkLanes;
+  // the lane's 16 rotated coordinates of every head stay in registers for
+  // the whole chunk (re-reading them from LDS per position is what bounds a
+  // straightforward version: 16 lanes at a 64-byte stride share few banks)
+  float qreg[REP][16];
+#pragma unroll
+  for (int r = 0; r < REP; ++r)
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) {
+      const float4 v4 = *reinterpret_cast<const float4 *>(&s_q[r][16 * sub + e]);
+      qreg[r][e] = v4.x;
+      qreg[r][e + 1] = v4.y;
+      qreg[r][e + 2] = v4.z;
+      qreg[r][e + 3] = v4.w;
+    }
   float run_m[kSlots], run_l[kSlots];
 #pragma unroll
   for (int u = 0; u < kSlots; ++u) {
@@ -560,68 +580,67 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
   for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int x = 0; x < 4; ++x) acc[r][x] = 0.0f;
-  const int grp = tid / kQkLanes, sub = tid % kQkLanes;
+  const int vbit = 4 * lane * BITS, vdw = vbit >> 5, vsh = vbit & 31;
+  const bool two = vsh + 4 * BITS > 32;
 
   for (size_t t0 = beg; t0 < end; t0 += kPlTile) {
     const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kPlTile) ? end - t0 : kPlTile);
-    // this lane's 16 K indices of each pass's position: 2 BITS bytes at byte
-    // 2 BITS sub of the packed row (even, so read as BITS halfwords)
-    uint16_t kw[kPasses][BITS];
+    uint32_t kw[kPasses][kWords];
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
       const int p = pass * 16 + grp;
       const size_t row = (t0 + (p < nt ? p : nt - 1)) * a.n_kv + g;
-      const uint16_t *src = reinterpret_cast<const uint16_t *>(a.kq + row * kPlen) + BITS * sub;
+      const uint8_t *src = a.kq + row * kPlen + 2 * BITS * sub;
 #pragma unroll
-      for (int h = 0; h < BITS; ++h) kw[pass][h] = src[h];
+      for (int h = 0; h < kWords; ++h)
+        kw[pass][h] = kDw ? reinterpret_cast<const uint32_t *>(src)[h]
+                          : static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(src)[h]);
     }
     if (tid < nt) {
       const size_t row = (t0 + tid) * a.n_kv + g;
       s_kn[tid] = a.kn[row];
-      if (vquant) s_vn[tid] = a.vn[row];
+      if (VQ) s_vn[tid] = a.vn[row];
     }
-    __syncthreads();  // s_q / s_c (first tile), s_kn, s_vn; the previous tile's s_e consumed
+    // the wave's V data of the tile, issued now so its latency overlaps the
+    // scores: index bits [4 lane BITS, +4 BITS) of each row (one or two
+    // dwords), or the f32 rows
+    constexpr int kVj = kPlTile / 4;
+    uint32_t vlo[VQ ? kVj : 1], vhi[VQ ? kVj : 1];
+    float4 vr[VQ ? 1 : kVj];
+#pragma unroll
+    for (int jj = 0; jj < kVj; ++jj) {
+      const int j = w + 4 * jj;
+      const size_t row = (t0 + (j < nt ? j : nt - 1)) * a.n_kv + g;
+      if constexpr (VQ) {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.vq + row * kPlen) + vdw;
+        vlo[jj] = src[0];
+        vhi[jj] = two ? src[1] : 0u;
+      } else {
+        vr[jj] = reinterpret_cast<const float4 *>(a.vf + row * kPlanarHd)[lane];
+      }
+    }
+    __syncthreads();  // s_kn, s_vn; the previous tile's s_e consumed
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
       const int p = pass * 16 + grp;
       unsigned __int128 win = 0;
 #pragma unroll
-      for (int h = 0; h < BITS; ++h) win |= static_cast<unsigned __int128>(kw[pass][h]) << (16 * h);
+      for (int h = 0; h < kWords; ++h) win |= static_cast<unsigned __int128>(kw[pass][h]) << (kWordBits * h);
       float cv[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) cv[e] = s_c[static_cast<uint32_t>(win >> (e * BITS)) & kMask];
       const float kscale = s_kn[p < nt ? p : nt - 1] * a.scale;
 #pragma unroll
       for (int r = 0; r < REP; ++r) {
-        const float *qr = &s_q[r][16 * sub];
-        float s0 = qr[0] * cv[0], s1 = qr[8] * cv[8];
+        float s0 = qreg[r][0] * cv[0], s1 = qreg[r][8] * cv[8];
 #pragma unroll
         for (int e = 1; e < 8; ++e) {
-          s0 = fmaf(qr[e], cv[e], s0);
-          s1 = fmaf(qr[8 + e], cv[8 + e], s1);
+          s0 = fmaf(qreg[r][e], cv[e], s0);
+          s1 = fmaf(qreg[r][8 + e], cv[8 + e], s1);
         }
         const float d = row16_sum(s0 + s1);
         // src/forward.rs:307: dot_rotated (times the norm) * scale
         if (sub == 0) s_e[p][r] = p < nt ? d * kscale : -INFINITY;
-      }
-    }
-    // the wave's V data of the tile, issued now so its latency overlaps the
-    // softmax step: index bits [4 lane BITS, +4 BITS) of each row (one or two
-    // dwords), or the f32 rows
-    uint32_t vlo[kPlTile / 4], vhi[kPlTile / 4];
-    float4 vr[kPlTile / 4];
-    const int vbit = 4 * lane * BITS, vdw = vbit >> 5, vsh = vbit & 31;
-    const bool two = vsh + 4 * BITS > 32;
-#pragma unroll
-    for (int jj = 0; jj < kPlTile / 4; ++jj) {
-      const int j = w + 4 * jj;
-      const size_t row = (t0 + (j < nt ? j : nt - 1)) * a.n_kv + g;
-      if (vquant) {
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.vq + row * kPlen) + vdw;
-        vlo[jj] = src[0];
-        vhi[jj] = two ? src[1] : 0u;
-      } else {
-        vr[jj] = reinterpret_cast<const float4 *>(a.vf + row * kPlanarHd)[lane];
       }
     }
     __syncthreads();
@@ -649,12 +668,12 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
     }
     // P.V: lane owns dims 4 lane .. +3, wave w takes positions w, w + 4, ...
 #pragma unroll
-    for (int jj = 0; jj < kPlTile / 4; ++jj) {
+    for (int jj = 0; jj < kVj; ++jj) {
       const int j = w + 4 * jj;
       if (j < nt) {
         float4 v;
         float vs = 1.0f;
-        if (vquant) {
+        if constexpr (VQ) {
           const uint64_t bitsv = ((static_cast<uint64_t>(vhi[jj]) << 32) | vlo[jj]) >> vsh;
           v = make_float4(s_c[bitsv & kMask], s_c[(bitsv >> BITS) & kMask],
                           s_c[(bitsv >> (2 * BITS)) & kMask], s_c[(bitsv >> (3 * BITS)) & kMask]);
@@ -664,7 +683,7 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
         }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-          const float e = vquant ? s_e[j][r] * vs : s_e[j][r];  // (p_j |v_j|) (src/forward.rs:344)
+          const float e = VQ ? s_e[j][r] * vs : s_e[j][r];  // (p_j |v_j|) (src/forward.rs:344)
           acc[r][0] = fmaf(e, v.x, acc[r][0]);
           acc[r][1] = fmaf(e, v.y, acc[r][1]);
           acc[r][2] = fmaf(e, v.z, acc[r][2]);
@@ -693,19 +712,25 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
   }
 }
 
-template <int REP>
-int launch_planar(const PlanarArgs &a, dim3 grid, const PlanarTables &tb, hipStream_t st) {
+template <int REP, bool VQ>
+int launch_planar_v(const PlanarArgs &a, dim3 grid, const PlanarTables &tb, hipStream_t st) {
   switch (a.bits) {
-    case 1: BH_LAUNCH((attn_planar_kernel<REP, 1>), grid, kBlock, 0, st, a, tb); break;
-    case 2: BH_LAUNCH((attn_planar_kernel<REP, 2>), grid, kBlock, 0, st, a, tb); break;
-    case 3: BH_LAUNCH((attn_planar_kernel<REP, 3>), grid, kBlock, 0, st, a, tb); break;
-    case 4: BH_LAUNCH((attn_planar_kernel<REP, 4>), grid, kBlock, 0, st, a, tb); break;
-    case 5: BH_LAUNCH((attn_planar_kernel<REP, 5>), grid, kBlock, 0, st, a, tb); break;
-    case 6: BH_LAUNCH((attn_planar_kernel<REP, 6>), grid, kBlock, 0, st, a, tb); break;
-    case 7: BH_LAUNCH((attn_planar_kernel<REP, 7>), grid, kBlock, 0, st, a, tb); break;
-    default: BH_LAUNCH((attn_planar_kernel<REP, 8>), grid, kBlock, 0, st, a, tb); break;
+    case 1: BH_LAUNCH((attn_planar_kernel<REP, 1, VQ>), grid, kBlock, 0, st, a, tb); break;
+    case 2: BH_LAUNCH((attn_planar_kernel<REP, 2, VQ>), grid, kBlock, 0, st, a, tb); break;
+    case 3: BH_LAUNCH((attn_planar_kernel<REP, 3, VQ>), grid, kBlock, 0, st, a, tb); break;
+    case 4: BH_LAUNCH((attn_planar_kernel<REP, 4, VQ>), grid, kBlock, 0, st, a, tb); break;
+    case 5: BH_LAUNCH((attn_planar_kernel<REP, 5, VQ>), grid, kBlock, 0, st, a, tb); break;
+    case 6: BH_LAUNCH((attn_planar_kernel<REP, 6, VQ>), grid, kBlock, 0, st, a, tb); break;
+    case 7: BH_LAUNCH((attn_planar_kernel<REP, 7, VQ>), grid, kBlock, 0, st, a, tb); break;
+    default: BH_LAUNCH((attn_planar_kernel<REP, 8, VQ>), grid, kBlock, 0, st, a, tb); break;
   }
   return ok();
+}
+
+template <int REP>
+int launch_planar(const PlanarArgs &a, dim3 grid, const PlanarTables &tb, hipStream_t st) {
+  return a.vq != nullptr ? launch_planar_v<REP, true>(a, grid, tb, st)
+                         : launch_planar_v<REP, false>(a, grid, tb, st);
 }
 
 // ---- multi-query path (matrix cores) ---------------------------------------
