@@ -654,6 +654,8 @@ def main() -> int:
                  lambda: wl_attention_planar(bh, synth, dev, stream, 1, 32767, 4)),
                 ("attention decode ctx=4096 planar4",
                  lambda: wl_attention_planar(bh, synth, dev, stream, 1, 4095, 4)),
+                ("attention batch 64 queries ctx=4096 planar4",
+                 lambda: wl_attention_planar(bh, synth, dev, stream, 64, 4032, 4)),
             ]
             products = [  # (name, rows, ne0, tokens): decode matvecs and batched products
                 ("pq2_matvec LM head [248320x5120] N=1", 248320, 5120, 1),

@@ -643,16 +643,22 @@ void or_planar_dequantize(const uint8_t *packed, float norm, size_t hd, unsigned
 
 /* PlanarQuant::dot_rotated_scratch, src/kvquant.rs:444-460: f32 sum in
  * index order of q_rot[i] * c[idx_i] over i < hd, times the norm */
-float or_planar_dot_rotated(const float *q_rot, const uint8_t *packed, float norm, size_t hd,
-                            unsigned bits) {
+/* the dot against a given codebook (the attention loop builds it once) */
+static float planar_dot_cb(const float *q_rot, const uint8_t *packed, float norm, size_t hd,
+                           unsigned bits, const float *cb) {
   size_t hp = (hd + 1) / 2 * 2;
-  float cb[256];
   uint8_t idx[256];
-  or_planar_codebook(hd, bits, cb);
   or_planar_unpack(packed, hp, bits, idx);
   float acc = 0.0f;
   for (size_t i = 0; i < hd; ++i) acc += q_rot[i] * cb[idx[i]];
   return acc * norm;
+}
+
+float or_planar_dot_rotated(const float *q_rot, const uint8_t *packed, float norm, size_t hd,
+                            unsigned bits) {
+  float cb[256];
+  or_planar_codebook(hd, bits, cb);
+  return planar_dot_cb(q_rot, packed, norm, hd, bits, cb);
 }
 
 /* AttnCache::append_k_quantized / append_v_quantized / append_v,
@@ -706,7 +712,7 @@ int or_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *
       or_planar_rotate(q + (i * n_head + hq) * hd, hd, gc, gs, qrot);
       for (size_t j = 0; j < n_pos; ++j) {
         size_t r = j * n_kv + kv;
-        scores[j] = or_planar_dot_rotated(qrot, kq + r * plen, kn[r], hd, bits) * scale;
+        scores[j] = planar_dot_cb(qrot, kq + r * plen, kn[r], hd, bits, cb) * scale;
       }
       or_softmax_rows(scores, n_pos, n_pos, 1.0f, probs);
       float *o = out + (i * n_head + hq) * hd;

@@ -511,20 +511,65 @@ struct PlanarArgs {
   float scale;
 };
 
+// One tile's global data, held in registers: the lane's K words and norms
+// of its four score positions, and its V index bits (one or two dwords per
+// position of the wave) and the norm of position `lane` -- or, V in f32, the
+// wave's f32 V rows.  Quantized caches load the next tile's set while the
+// current one is computed.
+template <int BITS, bool VQ>
+struct PlanarTile {
+  static constexpr int kPasses = kPlTile / 16;
+  static constexpr bool kDw = BITS % 2 == 0;  // whole dwords (even BITS) or halfwords
+  static constexpr int kWords = kDw ? BITS / 2 : BITS;
+  static constexpr int kVj = kPlTile / 4;
+  // 4 BITS index bits at bit 4 lane BITS straddle a dword boundary for
+  // some lanes unless BITS divides 8
+  static constexpr bool kTwo = 8 % BITS != 0;
+  uint32_t kw[kPasses][kWords];
+  float kn[kPasses];
+  uint32_t vlo[VQ ? kVj : 1], vhi[VQ && kTwo ? kVj : 1];
+  float vn;
+  float4 vr[VQ ? 1 : kVj];
+
+  __device__ __forceinline__ void load(const PlanarArgs &a, size_t t0, int nt, int g, int grp,
+                                       int sub, int w, int lane, int vdw, bool two) {
+    constexpr int kPlen = 32 * BITS;
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int p = pass * 16 + grp;
+      const size_t row = (t0 + (p < nt ? p : nt - 1)) * a.n_kv + g;
+      const uint8_t *src = a.kq + row * kPlen + 2 * BITS * sub;
+#pragma unroll
+      for (int h = 0; h < kWords; ++h)
+        kw[pass][h] = kDw ? reinterpret_cast<const uint32_t *>(src)[h]
+                          : static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(src)[h]);
+      kn[pass] = a.kn[row];
+    }
+#pragma unroll
+    for (int jj = 0; jj < kVj; ++jj) {
+      const int j = w + 4 * jj;
+      const size_t row = (t0 + (j < nt ? j : nt - 1)) * a.n_kv + g;
+      if constexpr (VQ) {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.vq + row * kPlen) + vdw;
+        vlo[jj] = src[0];
+        if constexpr (kTwo) vhi[jj] = two ? src[1] : 0u;
+      } else {
+        vr[jj] = reinterpret_cast<const float4 *>(a.vf + row * kPlanarHd)[lane];
+      }
+    }
+    if constexpr (VQ) vn = a.vn[(t0 + (lane < nt ? lane : nt - 1)) * a.n_kv + g];
+  }
+};
+
 template <int REP, int BITS, bool VQ>
 __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, PlanarTables tb) {
+  using Tile = PlanarTile<BITS, VQ>;
   constexpr int kSlots = (REP + 3) / 4;
-  constexpr int kPlen = 32 * BITS;         // packed row bytes
   constexpr uint32_t kMask = (1u << BITS) - 1u;
-  constexpr int kPasses = kPlTile / 16;
-  // a lane's 2 BITS bytes of a packed K row: BITS / 2 dwords (even BITS) or
-  // BITS halfwords, at byte 2 BITS sub
-  constexpr bool kDw = BITS % 2 == 0;
-  constexpr int kWords = kDw ? BITS / 2 : BITS;
-  constexpr int kWordBits = kDw ? 32 : 16;
+  constexpr int kPasses = Tile::kPasses;
+  constexpr int kVj = Tile::kVj;
   __shared__ float s_c[256];
   __shared__ float s_q[REP][kPlanarHd];
-  __shared__ float s_kn[kPlTile], s_vn[kPlTile];
   __shared__ float s_e[kPlTile][REP];
   __shared__ float s_corr[REP];
   __shared__ float s_acc[4][REP][kPlanarHd];
@@ -543,6 +588,14 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
       a.pacc[(part0 + static_cast<size_t>(o / kHd) * a.n_chunks) * kHd + o % kHd] = 0.0f;
     return;
   }
+  const int grp = tid / kQkLanes, sub = tid % kQkLanes;
+  const int vbit = 4 * lane * BITS, vdw = vbit >> 5, vsh = vbit & 31;
+  const bool two = vsh + 4 * BITS > 32;
+  auto tile_len = [&](size_t t0) {
+    return static_cast<int>(end - t0 < static_cast<size_t>(kPlTile) ? end - t0 : kPlTile);
+  };
+  Tile nxt;
+  nxt.load(a, beg, tile_len(beg), g, grp, sub, w, lane, vdw, two);
   s_c[tid] = tb.cent[tid];
   // q rows of the kv head's REP heads, rotated: pair p of head r
   for (int o = tid; o < REP * kPlanarHd / 2; o += kBlock) {
@@ -554,7 +607,6 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
     s_q[r][2 * pp + 1] = sn * qa.x + cc * qa.y;
   }
   __syncthreads();
-  const int grp = tid / kQkLanes, sub = tid % kQkLanes;
   // the lane's 16 rotated coordinates of every head stay in registers for
   // the whole chunk (re-reading them from LDS per position is what bounds a
   // straightforward version: 16 lanes at a 64-byte stride share few banks)
@@ -580,56 +632,23 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
   for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int x = 0; x < 4; ++x) acc[r][x] = 0.0f;
-  const int vbit = 4 * lane * BITS, vdw = vbit >> 5, vsh = vbit & 31;
-  const bool two = vsh + 4 * BITS > 32;
 
   for (size_t t0 = beg; t0 < end; t0 += kPlTile) {
-    const int nt = static_cast<int>(end - t0 < static_cast<size_t>(kPlTile) ? end - t0 : kPlTile);
-    uint32_t kw[kPasses][kWords];
-#pragma unroll
-    for (int pass = 0; pass < kPasses; ++pass) {
-      const int p = pass * 16 + grp;
-      const size_t row = (t0 + (p < nt ? p : nt - 1)) * a.n_kv + g;
-      const uint8_t *src = a.kq + row * kPlen + 2 * BITS * sub;
-#pragma unroll
-      for (int h = 0; h < kWords; ++h)
-        kw[pass][h] = kDw ? reinterpret_cast<const uint32_t *>(src)[h]
-                          : static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(src)[h]);
-    }
-    if (tid < nt) {
-      const size_t row = (t0 + tid) * a.n_kv + g;
-      s_kn[tid] = a.kn[row];
-      if (VQ) s_vn[tid] = a.vn[row];
-    }
-    // the wave's V data of the tile, issued now so its latency overlaps the
-    // scores: index bits [4 lane BITS, +4 BITS) of each row (one or two
-    // dwords), or the f32 rows
-    constexpr int kVj = kPlTile / 4;
-    uint32_t vlo[VQ ? kVj : 1], vhi[VQ ? kVj : 1];
-    float4 vr[VQ ? 1 : kVj];
-#pragma unroll
-    for (int jj = 0; jj < kVj; ++jj) {
-      const int j = w + 4 * jj;
-      const size_t row = (t0 + (j < nt ? j : nt - 1)) * a.n_kv + g;
-      if constexpr (VQ) {
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.vq + row * kPlen) + vdw;
-        vlo[jj] = src[0];
-        vhi[jj] = two ? src[1] : 0u;
-      } else {
-        vr[jj] = reinterpret_cast<const float4 *>(a.vf + row * kPlanarHd)[lane];
-      }
-    }
-    __syncthreads();  // s_kn, s_vn; the previous tile's s_e consumed
+    const int nt = tile_len(t0);
+    const Tile cur = nxt;
+    if (VQ && t0 + kPlTile < end)
+      nxt.load(a, t0 + kPlTile, tile_len(t0 + kPlTile), g, grp, sub, w, lane, vdw, two);
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
       const int p = pass * 16 + grp;
       unsigned __int128 win = 0;
 #pragma unroll
-      for (int h = 0; h < kWords; ++h) win |= static_cast<unsigned __int128>(kw[pass][h]) << (kWordBits * h);
+      for (int h = 0; h < Tile::kWords; ++h)
+        win |= static_cast<unsigned __int128>(cur.kw[pass][h]) << ((Tile::kDw ? 32 : 16) * h);
       float cv[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) cv[e] = s_c[static_cast<uint32_t>(win >> (e * BITS)) & kMask];
-      const float kscale = s_kn[p < nt ? p : nt - 1] * a.scale;
+      const float kscale = cur.kn[pass] * a.scale;
 #pragma unroll
       for (int r = 0; r < REP; ++r) {
         float s0 = qreg[r][0] * cv[0], s1 = qreg[r][8] * cv[8];
@@ -643,7 +662,7 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
         if (sub == 0) s_e[p][r] = p < nt ? d * kscale : -INFINITY;
       }
     }
-    __syncthreads();
+    __syncthreads();  // scores in s_e
 #pragma unroll
     for (int u = 0; u < kSlots; ++u) {
       const int r = w + 4 * u;
@@ -653,13 +672,14 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
         const bool none = m_new == -INFINITY;
         const float corr = none ? 1.0f : expf(run_m[u] - m_new);
         const float e = none ? 0.0f : expf(sc - m_new);
-        s_e[lane][r] = e;
+        // the P.V weight: p_j, or (p_j |v_j|) for a quantized V (src/forward.rs:344)
+        s_e[lane][r] = VQ ? e * cur.vn : e;
         run_l[u] = run_l[u] * corr + wave_sum(e);
         run_m[u] = m_new;
         if (lane == 0) s_corr[r] = corr;
       }
     }
-    __syncthreads();
+    __syncthreads();  // weights and corrections
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
       const float cr = s_corr[r];
@@ -672,24 +692,30 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
       const int j = w + 4 * jj;
       if (j < nt) {
         float4 v;
-        float vs = 1.0f;
         if constexpr (VQ) {
-          const uint64_t bitsv = ((static_cast<uint64_t>(vhi[jj]) << 32) | vlo[jj]) >> vsh;
+          uint64_t bitsv = cur.vlo[jj];
+          if constexpr (Tile::kTwo) bitsv |= static_cast<uint64_t>(cur.vhi[jj]) << 32;
+          bitsv >>= vsh;
           v = make_float4(s_c[bitsv & kMask], s_c[(bitsv >> BITS) & kMask],
                           s_c[(bitsv >> (2 * BITS)) & kMask], s_c[(bitsv >> (3 * BITS)) & kMask]);
-          vs = s_vn[j];
         } else {
-          v = vr[jj];
+          v = cur.vr[jj];
         }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-          const float e = VQ ? s_e[j][r] * vs : s_e[j][r];  // (p_j |v_j|) (src/forward.rs:344)
+          const float e = s_e[j][r];
           acc[r][0] = fmaf(e, v.x, acc[r][0]);
           acc[r][1] = fmaf(e, v.y, acc[r][1]);
           acc[r][2] = fmaf(e, v.z, acc[r][2]);
           acc[r][3] = fmaf(e, v.w, acc[r][3]);
         }
       }
+    }
+    if (!VQ && t0 + kPlTile < end) {
+      __syncthreads();  // s_e consumed before the next tile's scores
+      nxt.load(a, t0 + kPlTile, tile_len(t0 + kPlTile), g, grp, sub, w, lane, vdw, two);
+    } else {
+      __syncthreads();  // s_e consumed before the next tile's scores
     }
   }
 #pragma unroll
@@ -773,6 +799,9 @@ struct MqArgs {
   size_t pos0, kv_stride, chunk;
   int n_head, n_q, rep, n_chunks, n_kv;
   float scale;
+  // planar-quantized caches: kc holds the packed K rows, vc the packed V rows
+  // (or V's f32 rows), kn / vn the norms; unused otherwise
+  const float *kn, *vn;
 };
 
 // max over the four lanes l % 16 + 16 g (one row): permlane swaps
@@ -819,8 +848,17 @@ __device__ __forceinline__ void split_hl(float x, _Float16 &h, _Float16 &l) {
 // fragment is one 16-byte LDS read.
 __device__ __forceinline__ int vcol(int p) { return p < 16 ? 8 * (p >> 2) + (p & 3) : 8 * ((p - 16) >> 2) + 4 + (p & 3); }
 
-template <bool F16>
-__global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
+// PB > 0: a planar-quantized cache of PB-bit indices (src/kvquant.rs).  The
+// tile's K and V values are the centroids of the packed indices, looked up
+// while staging (V's times its row norm, or V's f32 rows when VQ is false),
+// q is rotated as it is split, each score takes K's row norm with the
+// position's scale (src/forward.rs:307), and the sums stay in rotated space
+// for attn_merge_rows_rot_kernel to turn back.  The rest is the f32 path.
+template <bool F16, int PB, bool VQ>
+__device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, const float *gc,
+                                        const float *gs) {
+  constexpr bool PL = PB > 0;
+  static_assert(!(PL && F16), "planar caches take the f32 staging");
   __shared__ __attribute__((aligned(16))) _Float16 sKh[kMqTile * kKStride];
   __shared__ __attribute__((aligned(16))) _Float16 sKl[F16 ? 8 : kMqTile * kKStride];
   __shared__ __attribute__((aligned(16))) _Float16 sVh[kHd * kVStride];
@@ -828,6 +866,7 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 sQl[kMqRows * kKStride];  // q lo fragments
   __shared__ float sKs[kMqTile];  // 2^-b of each staged K row
   __shared__ unsigned sVmax[2];   // bits of a tile's largest |v| (non-negative floats order as ints), by tile parity
+  __shared__ float sC[PL ? 256 : 1];  // the centroids
   // XCD-aware numbering: workgroups go to the 8 XCDs round robin by id, so
   // the row tiles of one (chunk, kv head) get ids 8 apart -- the same XCD,
   // dispatched together -- and share the K/V tiles in that XCD's L2.
@@ -888,6 +927,16 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
       v[2 * s] = valid ? qr[8 * s] : f32x4{0.f, 0.f, 0.f, 0.f};
       v[2 * s + 1] = valid ? qr[8 * s + 1] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    if constexpr (PL) {
+      // rotated q: pairs (2p, 2p + 1) of the lane's dims (src/kvquant.rs:356-366)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int p0 = (32 * (k >> 1) + 8 * grp + 4 * (k & 1)) >> 1;
+        const float c0 = gc[p0], s0 = gs[p0], c1 = gc[p0 + 1], s1 = gs[p0 + 1];
+        const f32x4 x = v[k];
+        v[k] = f32x4{c0 * x.x - s0 * x.y, s0 * x.x + c0 * x.y, c1 * x.z - s1 * x.w, s1 * x.z + c1 * x.w};
+      }
+    }
     float m = 0.0f;
 #pragma unroll
     for (int k = 0; k < 16; ++k)
@@ -924,6 +973,9 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
     sVmax[0] = 0u;
     sVmax[1] = 0u;
   }
+  if constexpr (PL) {
+    if (tid < 256) sC[tid] = cent[tid];
+  }
   __syncthreads();
   int parity = 0;
 
@@ -941,10 +993,51 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
   using VElt = typename std::conditional<F16, uint16_t, float>::type;
   KReg kr;
   VElt vr[4][4];
+  // planar: the lane's 2 PB bytes of K row sp (16 indices) as PB / 2 dwords
+  // or PB halfwords, and of its V positions the index bits of dims vd + 64 i
+  // (one or two dwords), with the rows' norms
+  constexpr int kPlen = 32 * (PL ? PB : 1);
+  constexpr bool kKDw = PB % 2 == 0;
+  constexpr int kKWords = !PL ? 1 : (kKDw ? PB / 2 : PB);
+  constexpr bool kVTwo = PL && 8 % PB != 0;
+  uint32_t kw[kKWords];
+  float knr = 0.0f;
+  uint32_t vlo[PL && VQ ? 4 : 1][PL && VQ ? 4 : 1], vhi[kVTwo && VQ ? 4 : 1][kVTwo && VQ ? 4 : 1];
+  float vnr[PL && VQ ? 4 : 1];
   auto fetch = [&](size_t t0) {
     const int nt = static_cast<int>(end - t0 < kMqTile ? end - t0 : kMqTile);
     const size_t krow = (t0 + (sp < nt ? sp : nt - 1)) * a.kv_stride + head_off + 16 * kpart;
     const VElt *vcp = static_cast<const VElt *>(a.vc);
+    if constexpr (PL) {
+      const size_t prow = (t0 + (sp < nt ? sp : nt - 1)) * a.n_kv + g;
+      const uint8_t *src = static_cast<const uint8_t *>(a.kc) + prow * kPlen + 2 * PB * kpart;
+#pragma unroll
+      for (int h = 0; h < kKWords; ++h)
+        kw[h] = kKDw ? reinterpret_cast<const uint32_t *>(src)[h]
+                     : static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(src)[h]);
+      knr = a.kn[prow];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int pj = 4 * vpg + jj;
+        const size_t vpos = t0 + (pj < nt ? pj : nt - 1);
+        if constexpr (VQ) {
+          const size_t vrow = vpos * a.n_kv + g;
+          const uint32_t *vsrc = reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(a.vc) + vrow * kPlen);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int bit = (vd + 64 * i) * PB;
+            vlo[jj][i] = vsrc[bit >> 5];
+            if constexpr (kVTwo) vhi[jj][i] = (bit & 31) + PB > 32 ? vsrc[(bit >> 5) + 1] : 0u;
+          }
+          vnr[jj] = a.vn[vrow];
+        } else {
+          const size_t e = vpos * a.kv_stride + head_off + vd;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vr[jj][i] = vcp[e + 64 * i];
+        }
+      }
+      return;
+    }
     if constexpr (F16) {
       const uint16_t *kcp = static_cast<const uint16_t *>(a.kc);
       kr[0] = *reinterpret_cast<const uint4 *>(kcp + krow);
@@ -981,6 +1074,30 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
       }
       __syncthreads();
     } else {
+      if constexpr (PL) {
+        // centroids of the staged indices (K: 16 of row sp; V: 4 dims of 4
+        // positions, times the V rows' norms)
+        constexpr uint32_t kMask = (1u << PB) - 1u;
+        unsigned __int128 win = 0;
+#pragma unroll
+        for (int h = 0; h < kKWords; ++h) win |= static_cast<unsigned __int128>(kw[h]) << ((kKDw ? 32 : 16) * h);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          kr[k] = f32x4{sC[static_cast<uint32_t>(win >> ((4 * k) * PB)) & kMask],
+                        sC[static_cast<uint32_t>(win >> ((4 * k + 1) * PB)) & kMask],
+                        sC[static_cast<uint32_t>(win >> ((4 * k + 2) * PB)) & kMask],
+                        sC[static_cast<uint32_t>(win >> ((4 * k + 3) * PB)) & kMask]};
+        if constexpr (VQ) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              uint64_t b = vlo[jj][i];
+              if constexpr (kVTwo) b |= static_cast<uint64_t>(vhi[jj][i]) << 32;
+              vr[jj][i] = sC[(b >> (((vd + 64 * i) * PB) & 31)) & kMask] * vnr[jj];
+            }
+        }
+      }
       float km = 0.0f, vm = 0.0f;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -1009,7 +1126,7 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
         *reinterpret_cast<half8 *>(khp + 8 * k2) = hv;
         *reinterpret_cast<half8 *>(klp + 8 * k2) = lv;
       }
-      if (kpart == 0) sKs[sp] = ldexpf(1.0f, -kb);
+      if (kpart == 0) sKs[sp] = PL ? ldexpf(knr, -kb) : ldexpf(1.0f, -kb);
       __syncthreads();  // sVmax[parity] complete
       const int vst = v_shift(__uint_as_float(sVmax[parity]));
       const int vs = vst > vs_cur ? vst : vs_cur;
@@ -1128,6 +1245,16 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
   }
 }
 
+template <bool F16>
+__global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
+  mq_body<F16, 0, false>(a, nullptr, nullptr, nullptr);
+}
+
+template <int PB, bool VQ>
+__global__ __launch_bounds__(kMqThreads) void attn_mq_planar_kernel(MqArgs a, PlanarTables tb) {
+  mq_body<false, PB, VQ>(a, tb.cent, tb.gc, tb.gs);
+}
+
 // Chunk merge of the multi-query path (few chunks, many rows): one block of
 // four waves per (query, head) row, wave w owning dims 64 w .. 64 w + 63 (one
 // per lane).  Every wave weighs the chunks itself -- e^(m_c - M) from the
@@ -1135,9 +1262,11 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
 // the chunks' accumulators, all of a lane's loads in flight together, and
 // divides by the weighted sum.  Chunks with no visible position (max -inf)
 // are left out.
-__global__ __launch_bounds__(256) void attn_merge_rows_kernel(const float *pm, const float *pl,
-                                                              const float *pacc, int n_chunks,
-                                                              float *out) {
+// ROT: the inverse Givens rotation of the merged row, as in combine1_body.
+template <bool ROT>
+__device__ __forceinline__ void merge_rows_body(const float *pm, const float *pl, const float *pacc,
+                                                int n_chunks, float *out, const float *gc,
+                                                const float *gs) {
   __shared__ float s_w[4][64];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const size_t row = blockIdx.x;
@@ -1166,7 +1295,27 @@ __global__ __launch_bounds__(256) void attn_merge_rows_kernel(const float *pm, c
     __builtin_amdgcn_wave_barrier();  // weights consumed before the next tile's
   }
   den = wave_sum(den);
-  out[row * kHd + 64 * w + lane] = num / den;
+  const float val = num / den;
+  const int d = 64 * w + lane;
+  if constexpr (ROT) {
+    const float other = __shfl_xor(val, 1, 64);
+    const float c = gc[d >> 1], sn = gs[d >> 1];
+    out[row * kHd + d] = (d & 1) == 0 ? c * val + sn * other : -sn * other + c * val;
+  } else {
+    out[row * kHd + d] = val;
+  }
+}
+
+__global__ __launch_bounds__(256) void attn_merge_rows_kernel(const float *pm, const float *pl,
+                                                              const float *pacc, int n_chunks,
+                                                              float *out) {
+  merge_rows_body<false>(pm, pl, pacc, n_chunks, out, nullptr, nullptr);
+}
+
+__global__ __launch_bounds__(256) void attn_merge_rows_rot_kernel(const float *pm, const float *pl,
+                                                                  const float *pacc, int n_chunks,
+                                                                  float *out, PlanarTables tb) {
+  merge_rows_body<true>(pm, pl, pacc, n_chunks, out, tb.gc, tb.gs);
 }
 
 // ---- generic path ----------------------------------------------------------
@@ -1282,6 +1431,21 @@ int decode_dispatch(int rep, const DecodeArgs &a, int n_kv, int n_q, hipStream_t
     case 8: return launch_decode<8, T>(a, n_kv, n_q, st);
     default: return fail(BH_ERR_ARG, "attention: no decode kernel for this grouping");
   }
+}
+
+template <bool VQ>
+int launch_mq_planar(int bits, const MqArgs &m, dim3 grid, const PlanarTables &tb, hipStream_t st) {
+  switch (bits) {
+    case 1: BH_LAUNCH((attn_mq_planar_kernel<1, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+    case 2: BH_LAUNCH((attn_mq_planar_kernel<2, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+    case 3: BH_LAUNCH((attn_mq_planar_kernel<3, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+    case 4: BH_LAUNCH((attn_mq_planar_kernel<4, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+    case 5: BH_LAUNCH((attn_mq_planar_kernel<5, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+    case 6: BH_LAUNCH((attn_mq_planar_kernel<6, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+    case 7: BH_LAUNCH((attn_mq_planar_kernel<7, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+    default: BH_LAUNCH((attn_mq_planar_kernel<8, VQ>), grid, kMqThreads, 0, st, m, tb); break;
+  }
+  return ok();
 }
 
 bool decode_rep(size_t rep) {
@@ -1481,6 +1645,42 @@ extern "C" int bh_attention_planar(const float *q, size_t n_q, size_t pos0, cons
   PlanarTables tb;
   if (!planar_tables(hd, bits, &tb)) return fail(BH_ERR_ARG, "attention_planar: no tables");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const float scale = 1.0f / sqrtf(static_cast<float>(hd));  // src/forward.rs:282
+  if (n_q * rep >= static_cast<size_t>(kMqMinRows)) {
+    // many queries: the matrix-core path with planar staging, chunked as
+    // bh_attention's
+    const size_t R = n_q * rep;
+    const size_t tiles_r = (R + kMqRows - 1) / kMqRows;
+    if (tiles_r > 65535) return fail(BH_ERR_SHAPE, "attention_planar: too many queries");
+    const size_t cap = mq_capacity(false);
+    const size_t want = cap / (tiles_r * n_kv) > 0 ? cap / (tiles_r * n_kv) : 1;
+    const size_t ptiles = (n_max + kMqTile - 1) / kMqTile;
+    const size_t per = (ptiles + want - 1) / want;
+    const size_t chunk = per * kMqTile;
+    const size_t n_chunks = (n_max + chunk - 1) / chunk;
+    if (n_chunks > 65535) return fail(BH_ERR_SHAPE, "attention_planar: too many positions");
+    size_t rows = 0, sbytes = 0;
+    if (!mul_size(n_q, n_head, n_chunks, &rows) || !mul_size(rows, kHd + 2, 4, &sbytes))
+      return fail(BH_ERR_SHAPE, "attention_planar: scratch size overflows");
+    float *scratch = static_cast<float *>(device_scratch(sbytes, kScratchAttention, st));
+    if (scratch == nullptr) return BH_ERR_HIP;
+    MqArgs m{q, kq, vq != nullptr ? static_cast<const void *>(vq) : static_cast<const void *>(v_f32),
+             scratch, scratch + rows, scratch + 2 * rows, pos0, n_kv * kHd, chunk,
+             static_cast<int>(n_head), static_cast<int>(n_q), static_cast<int>(rep),
+             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale, kn, vn};
+    const size_t nb = n_chunks * n_kv * tiles_r;
+    if (nb > 0x7fffffffu) return fail(BH_ERR_SHAPE, "attention_planar: too many blocks");
+    const int e = vq != nullptr ? launch_mq_planar<true>(static_cast<int>(bits), m, dim3(static_cast<unsigned>(nb)), tb, st)
+                                : launch_mq_planar<false>(static_cast<int>(bits), m, dim3(static_cast<unsigned>(nb)), tb, st);
+    if (e) return e;
+    if (vq != nullptr)
+      BH_LAUNCH(attn_merge_rows_rot_kernel, static_cast<unsigned>(n_q * n_head), 256, 0, st, m.pm, m.pl,
+                m.pacc, static_cast<int>(n_chunks), out, tb);
+    else
+      BH_LAUNCH(attn_merge_rows_kernel, static_cast<unsigned>(n_q * n_head), 256, 0, st, m.pm, m.pl,
+                m.pacc, static_cast<int>(n_chunks), out);
+    return ok();
+  }
   // chunks of whole tiles: about 512 blocks for one query, 2048 for several,
   // and at most 128 chunks (the one-round-trip merge)
   const size_t blocks = n_q == 1 ? 512 : 2048;
@@ -1497,7 +1697,7 @@ extern "C" int bh_attention_planar(const float *q, size_t n_q, size_t pos0, cons
   if (scratch == nullptr) return BH_ERR_HIP;
   PlanarArgs a{q,       kq,   kn,    vq, vn, v_f32, scratch, scratch + rows, scratch + 2 * rows,
                pos0,    chunk, static_cast<int>(n_head), static_cast<int>(n_chunks),
-               static_cast<int>(n_kv), static_cast<int>(bits), 1.0f / sqrtf(static_cast<float>(hd))};
+               static_cast<int>(n_kv), static_cast<int>(bits), scale};
   const dim3 grid(static_cast<unsigned>(n_chunks), static_cast<unsigned>(n_kv), static_cast<unsigned>(n_q));
   int e = BH_OK;
   switch (rep) {

@@ -88,6 +88,13 @@ def test_kv_store_planar_f32_v_and_offset(bh, oracle, synth, dev):
     (1, True, 2, 63, 8, 8),        # one q head per kv head
     (5, True, 1, 300, 16, 2),      # groups of 8
     (6, False, 4, 50, 12, 4),
+    # n_q * rep >= 48: the matrix-core path
+    (4, True, 8, 500, 24, 4),      # 48 rows per kv head
+    (3, True, 64, 4032, 24, 4),    # 64 queries at ctx 4096
+    (7, True, 20, 33, 24, 4),      # index bits straddling dwords
+    (2, False, 16, 100, 16, 2),    # V in f32, groups of 8
+    (1, True, 50, 0, 8, 8),        # one q head per kv head, from position 0
+    (8, True, 130, 70, 12, 4),     # more than one 128-row tile
 ])
 def test_attention_planar(bh, oracle, synth, dev, bits, quantize_v, n_q, pos0, n_head, n_kv):
     n = pos0 + n_q
