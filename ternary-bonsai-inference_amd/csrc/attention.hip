@@ -479,6 +479,20 @@ __global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_rot_kernel(
   combine1_body<kCombWaves, kCombPer, true>(pm, pl, pacc, n_chunks, out, tb.gc, tb.gs);
 }
 
+// max over the four lanes l % 16 + 16 g (one row): permlane swaps
+__device__ __forceinline__ float rows4_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---- planar-quantized caches (src/forward.rs:296-349, src/kvquant.rs) -------
 //
 // K (and V, unless the cache keeps V in f32: BONSAI_KV=planarNk) hold per
@@ -511,11 +525,12 @@ struct PlanarArgs {
   float scale;
 };
 
-// One tile's global data, held in registers: the lane's K words and norms
-// of its four score positions, and its V index bits (one or two dwords per
-// position of the wave) and the norm of position `lane` -- or, V in f32, the
-// wave's f32 V rows.  Quantized caches load the next tile's set while the
-// current one is computed.
+// One tile's global data of a lane, held in registers: the K words and
+// norms of the four positions its 16-lane group scores (one per pass), the
+// V norms of the same positions, and the V index bits (one or two dwords)
+// of the wave's 16 positions for the lane's 4 dims -- or, V in f32, the f32
+// dims.  The wave's positions of a tile are pass * 16 + 4 w + g (g the
+// lane's group, pass 0..3): local index jl = 4 pass + g.
 template <int BITS, bool VQ>
 struct PlanarTile {
   static constexpr int kPasses = kPlTile / 16;
@@ -527,51 +542,101 @@ struct PlanarTile {
   static constexpr bool kTwo = 8 % BITS != 0;
   uint32_t kw[kPasses][kWords];
   float kn[kPasses];
+  float vn[VQ ? kPasses : 1];
   uint32_t vlo[VQ ? kVj : 1], vhi[VQ && kTwo ? kVj : 1];
-  float vn;
   float4 vr[VQ ? 1 : kVj];
 
-  __device__ __forceinline__ void load(const PlanarArgs &a, size_t t0, int nt, int g, int grp,
-                                       int sub, int w, int lane, int vdw, bool two) {
+  // addresses: the tile's first row once (uniform), then 32-bit offsets of
+  // whole positions (64-bit products per row cost ~250 VALU per tile)
+  // K words and norms (and V norms) of the group's positions
+  __device__ __forceinline__ void load_k(const PlanarArgs &a, size_t t0, int nt, int g, int w,
+                                         int grp4, int sub) {
     constexpr int kPlen = 32 * BITS;
+    const uint32_t nkv = static_cast<uint32_t>(a.n_kv);
+    const uint32_t pstride = nkv * kPlen;  // bytes from one position to the next
+    const size_t r0 = t0 * a.n_kv + g;
+    const uint8_t *kb = a.kq + r0 * kPlen + 2 * BITS * sub;
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
-      const int p = pass * 16 + grp;
-      const size_t row = (t0 + (p < nt ? p : nt - 1)) * a.n_kv + g;
-      const uint8_t *src = a.kq + row * kPlen + 2 * BITS * sub;
+      const uint32_t p = static_cast<uint32_t>(min(pass * 16 + 4 * w + grp4, nt - 1));
+      const uint8_t *src = kb + p * pstride;
 #pragma unroll
       for (int h = 0; h < kWords; ++h)
         kw[pass][h] = kDw ? reinterpret_cast<const uint32_t *>(src)[h]
                           : static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(src)[h]);
-      kn[pass] = a.kn[row];
+      kn[pass] = a.kn[r0 + p * nkv];
+      if constexpr (VQ) vn[pass] = a.vn[r0 + p * nkv];
     }
+  }
+  // V index bits (or f32 dims) of the wave's 16 positions
+  __device__ __forceinline__ void load_v(const PlanarArgs &a, size_t t0, int nt, int g, int w,
+                                         int lane, int vdw, bool two) {
+    constexpr int kPlen = 32 * BITS;
+    const uint32_t nkv = static_cast<uint32_t>(a.n_kv);
+    const uint32_t pstride = nkv * kPlen;
+    const size_t r0 = t0 * a.n_kv + g;
+    if constexpr (VQ) {
+      const uint8_t *vb = a.vq + r0 * kPlen + 4 * vdw;
 #pragma unroll
-    for (int jj = 0; jj < kVj; ++jj) {
-      const int j = w + 4 * jj;
-      const size_t row = (t0 + (j < nt ? j : nt - 1)) * a.n_kv + g;
-      if constexpr (VQ) {
-        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.vq + row * kPlen) + vdw;
-        vlo[jj] = src[0];
-        if constexpr (kTwo) vhi[jj] = two ? src[1] : 0u;
-      } else {
-        vr[jj] = reinterpret_cast<const float4 *>(a.vf + row * kPlanarHd)[lane];
+      for (int jl = 0; jl < kVj; ++jl) {
+        const uint32_t j = static_cast<uint32_t>(min((jl >> 2) * 16 + 4 * w + (jl & 3), nt - 1));
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(vb + j * pstride);
+        vlo[jl] = src[0];
+        if constexpr (kTwo) vhi[jl] = two ? src[1] : 0u;
+      }
+    } else {
+      const float *vfb = a.vf + r0 * kPlanarHd + 4 * lane;
+      const uint32_t vstride = nkv * kPlanarHd;  // floats
+#pragma unroll
+      for (int jl = 0; jl < kVj; ++jl) {
+        const uint32_t j = static_cast<uint32_t>(min((jl >> 2) * 16 + 4 * w + (jl & 3), nt - 1));
+        vr[jl] = *reinterpret_cast<const float4 *>(vfb + j * vstride);
       }
     }
-    if constexpr (VQ) vn = a.vn[(t0 + (lane < nt ? lane : nt - 1)) * a.n_kv + g];
   }
 };
 
+// x[i] for a per-lane i as a chain of selects.  Each value goes through an
+// empty asm statement first: otherwise the compiler turns the chain back
+// into an indexed load and puts the array in scratch memory.
+template <int N>
+__device__ __forceinline__ float pick(const float (&x)[N], int i) {
+  float v = x[0];
+#pragma unroll
+  for (int r = 1; r < N; ++r) {
+    float xr = x[r];
+    asm volatile("" : "+v"(xr));
+    v = i == r ? xr : v;
+  }
+  return v;
+}
+
+// Each wave runs its own online softmax over the positions it scores (no
+// block barrier inside the chunk loop): after a pass's DPP row sums every
+// lane of a 16-lane group holds all REP scores of the group's position, so
+// the wave's per-head tile max is two permlane swaps away; lane sub < REP
+// forms head sub's weight of its position, writes it (times |v_j| for a
+// quantized V) to the wave's own LDS slice and keeps head sub's running sum;
+// P.V then reads the weights back as broadcasts.  The four waves' (max,
+// sum, accumulator) states merge once per chunk.
 template <int REP, int BITS, bool VQ>
 __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, PlanarTables tb) {
   using Tile = PlanarTile<BITS, VQ>;
-  constexpr int kSlots = (REP + 3) / 4;
   constexpr uint32_t kMask = (1u << BITS) - 1u;
   constexpr int kPasses = Tile::kPasses;
   constexpr int kVj = Tile::kVj;
+  static_assert(REP <= 16, "one head per lane of a 16-lane group");
+  static_assert(kPasses == 4, "the tile max below reads four passes");
+  // 2- and 4-bit indices are looked up a byte at a time: entry b of s_cb
+  // holds the centroids of the kE indices packed in byte b, in bit order
+  constexpr bool kByteTab = BITS == 2 || BITS == 4;
+  constexpr int kE = kByteTab ? 8 / BITS : 1;
+  using CVec = typename std::conditional<kE == 4, float4, float2>::type;
+  __shared__ __attribute__((aligned(16))) CVec s_cb[kByteTab ? 256 : 1];
   __shared__ float s_c[256];
   __shared__ float s_q[REP][kPlanarHd];
-  __shared__ float s_e[kPlTile][REP];
-  __shared__ float s_corr[REP];
+  __shared__ float s_e[4][kVj][REP];  // per wave: weights of its 16 positions
+  __shared__ float s_wm[4][REP], s_wl[4][REP], s_ww[4][REP];
   __shared__ float s_acc[4][REP][kPlanarHd];
   const int c = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
   const int tid = threadIdx.x, w = tid / 64, lane = tid % 64;
@@ -588,15 +653,25 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
       a.pacc[(part0 + static_cast<size_t>(o / kHd) * a.n_chunks) * kHd + o % kHd] = 0.0f;
     return;
   }
-  const int grp = tid / kQkLanes, sub = tid % kQkLanes;
+  const int grp4 = lane / kQkLanes, sub = lane % kQkLanes;  // group within the wave, lane in it
   const int vbit = 4 * lane * BITS, vdw = vbit >> 5, vsh = vbit & 31;
   const bool two = vsh + 4 * BITS > 32;
   auto tile_len = [&](size_t t0) {
     return static_cast<int>(end - t0 < static_cast<size_t>(kPlTile) ? end - t0 : kPlTile);
   };
   Tile nxt;
-  nxt.load(a, beg, tile_len(beg), g, grp, sub, w, lane, vdw, two);
+  nxt.load_k(a, beg, tile_len(beg), g, w, grp4, sub);
+  nxt.load_v(a, beg, tile_len(beg), g, w, lane, vdw, two);
   s_c[tid] = tb.cent[tid];
+  if constexpr (kByteTab) {
+    float ce[kE];
+#pragma unroll
+    for (int e = 0; e < kE; ++e) ce[e] = tb.cent[(tid >> (e * BITS)) & kMask];
+    if constexpr (kE == 4)
+      s_cb[tid] = CVec{ce[0], ce[1], ce[2], ce[3]};
+    else
+      s_cb[tid] = CVec{ce[0], ce[kE - 1]};
+  }
   // q rows of the kv head's REP heads, rotated: pair p of head r
   for (int o = tid; o < REP * kPlanarHd / 2; o += kBlock) {
     const int r = o / (kPlanarHd / 2), pp = o % (kPlanarHd / 2);
@@ -621,12 +696,9 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
       qreg[r][e + 2] = v4.z;
       qreg[r][e + 3] = v4.w;
     }
-  float run_m[kSlots], run_l[kSlots];
-#pragma unroll
-  for (int u = 0; u < kSlots; ++u) {
-    run_m[u] = -INFINITY;
-    run_l[u] = 0.0f;
-  }
+  // head sub's running max and sum over the wave's positions (lanes sub <
+  // REP; the same in the four groups)
+  float run_m = -INFINITY, run_l = 0.0f;
   float acc[REP][4];
 #pragma unroll
   for (int r = 0; r < REP; ++r)
@@ -636,19 +708,34 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
   for (size_t t0 = beg; t0 < end; t0 += kPlTile) {
     const int nt = tile_len(t0);
     const Tile cur = nxt;
-    if (VQ && t0 + kPlTile < end)
-      nxt.load(a, t0 + kPlTile, tile_len(t0 + kPlTile), g, grp, sub, w, lane, vdw, two);
+    const bool more = t0 + kPlTile < end;
+    // the next tile's V words now, its K words once this tile's are used
+    if (more) nxt.load_v(a, t0 + kPlTile, tile_len(t0 + kPlTile), g, w, lane, vdw, two);
+    float sc[kPasses];  // head sub's score of the group's position, per pass
 #pragma unroll
     for (int pass = 0; pass < kPasses; ++pass) {
-      const int p = pass * 16 + grp;
+      const bool in = pass * 16 + 4 * w + grp4 < nt;
       unsigned __int128 win = 0;
 #pragma unroll
       for (int h = 0; h < Tile::kWords; ++h)
         win |= static_cast<unsigned __int128>(cur.kw[pass][h]) << ((Tile::kDw ? 32 : 16) * h);
       float cv[16];
+      if constexpr (kByteTab) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) cv[e] = s_c[static_cast<uint32_t>(win >> (e * BITS)) & kMask];
+        for (int b = 0; b < 16 / kE; ++b) {
+          const CVec cb = s_cb[static_cast<uint32_t>(win >> (8 * b)) & 0xFFu];
+          if constexpr (kE == 4) {
+            cv[4 * b] = cb.x; cv[4 * b + 1] = cb.y; cv[4 * b + 2] = cb.z; cv[4 * b + 3] = cb.w;
+          } else {
+            cv[2 * b] = cb.x; cv[2 * b + 1] = cb.y;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) cv[e] = s_c[static_cast<uint32_t>(win >> (e * BITS)) & kMask];
+      }
       const float kscale = cur.kn[pass] * a.scale;
+      float d[REP];
 #pragma unroll
       for (int r = 0; r < REP; ++r) {
         float s0 = qreg[r][0] * cv[0], s1 = qreg[r][8] * cv[8];
@@ -657,53 +744,71 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
           s0 = fmaf(qreg[r][e], cv[e], s0);
           s1 = fmaf(qreg[r][8 + e], cv[8 + e], s1);
         }
-        const float d = row16_sum(s0 + s1);
-        // src/forward.rs:307: dot_rotated (times the norm) * scale
-        if (sub == 0) s_e[p][r] = p < nt ? d * kscale : -INFINITY;
+        d[r] = s0 + s1;
       }
+      // the REP row sums step by step, so their DPP moves fill each other's
+      // wait slots (every lane of the row ends with the sum)
+#pragma unroll
+      for (int r = 0; r < REP; ++r) d[r] += dpp_row<0xB1>(d[r]);
+#pragma unroll
+      for (int r = 0; r < REP; ++r) d[r] += dpp_row<0x4E>(d[r]);
+#pragma unroll
+      for (int r = 0; r < REP; ++r) d[r] += dpp_row<0x141>(d[r]);
+#pragma unroll
+      for (int r = 0; r < REP; ++r) d[r] += dpp_row<0x140>(d[r]);
+      // src/forward.rs:307: dot_rotated (times the norm) * scale
+      sc[pass] = in ? pick(d, sub) * kscale : -INFINITY;
     }
-    __syncthreads();  // scores in s_e
+    if (more) nxt.load_k(a, t0 + kPlTile, tile_len(t0 + kPlTile), g, w, grp4, sub);
+    // head sub's max over the wave's 16 positions (the four groups)
+    const float hm = fmaxf(run_m, rows4_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]))));
+    const float corr_mine = hm == -INFINITY ? 1.0f : expf(run_m - hm);
+    run_m = hm;
+    float ps = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kSlots; ++u) {
-      const int r = w + 4 * u;
-      if (r < REP) {
-        const float sc = s_e[lane][r];
-        const float m_new = fmaxf(run_m[u], wave_max(sc));
-        const bool none = m_new == -INFINITY;
-        const float corr = none ? 1.0f : expf(run_m[u] - m_new);
-        const float e = none ? 0.0f : expf(sc - m_new);
-        // the P.V weight: p_j, or (p_j |v_j|) for a quantized V (src/forward.rs:344)
-        s_e[lane][r] = VQ ? e * cur.vn : e;
-        run_l[u] = run_l[u] * corr + wave_sum(e);
-        run_m[u] = m_new;
-        if (lane == 0) s_corr[r] = corr;
-      }
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const float e = hm == -INFINITY ? 0.0f : expf(sc[pass] - hm);
+      ps += e;
+      // the P.V weight: p_j, or (p_j |v_j|) for a quantized V (src/forward.rs:344)
+      if (sub < REP) s_e[w][4 * pass + grp4][sub] = VQ ? e * cur.vn[pass] : e;
     }
-    __syncthreads();  // weights and corrections
+    run_l = run_l * corr_mine + rows4_sum(ps);
+    float corr[REP];  // head r's correction, from lane r
 #pragma unroll
-    for (int r = 0; r < REP; ++r) {
-      const float cr = s_corr[r];
+    for (int r = 0; r < REP; ++r)
+      corr[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr_mine), r));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int x = 0; x < 4; ++x) acc[r][x] *= cr;
-    }
-    // P.V: lane owns dims 4 lane .. +3, wave w takes positions w, w + 4, ...
+    for (int r = 0; r < REP; ++r)
 #pragma unroll
-    for (int jj = 0; jj < kVj; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < nt) {
+      for (int x = 0; x < 4; ++x) acc[r][x] *= corr[r];
+    // P.V: lane owns dims 4 lane .. +3 of the wave's 16 positions
+#pragma unroll
+    for (int jl = 0; jl < kVj; ++jl) {
+      if ((jl >> 2) * 16 + 4 * w + (jl & 3) < nt) {
         float4 v;
         if constexpr (VQ) {
-          uint64_t bitsv = cur.vlo[jj];
-          if constexpr (Tile::kTwo) bitsv |= static_cast<uint64_t>(cur.vhi[jj]) << 32;
-          bitsv >>= vsh;
-          v = make_float4(s_c[bitsv & kMask], s_c[(bitsv >> BITS) & kMask],
-                          s_c[(bitsv >> (2 * BITS)) & kMask], s_c[(bitsv >> (3 * BITS)) & kMask]);
+          if constexpr (kE == 4) {  // 2 bits: the lane's 4 indices are one byte
+            v = s_cb[(cur.vlo[jl] >> vsh) & 0xFFu];
+          } else if constexpr (kE == 2) {  // 4 bits: two bytes
+            const uint32_t bb = cur.vlo[jl] >> vsh;
+            const CVec lo = s_cb[bb & 0xFFu], hi = s_cb[(bb >> 8) & 0xFFu];
+            v = make_float4(lo.x, lo.y, hi.x, hi.y);
+          } else {
+            uint64_t bitsv = cur.vlo[jl];
+            if constexpr (Tile::kTwo) bitsv |= static_cast<uint64_t>(cur.vhi[jl]) << 32;
+            bitsv >>= vsh;
+            v = make_float4(s_c[bitsv & kMask], s_c[(bitsv >> BITS) & kMask],
+                            s_c[(bitsv >> (2 * BITS)) & kMask], s_c[(bitsv >> (3 * BITS)) & kMask]);
+          }
         } else {
-          v = cur.vr[jj];
+          v = cur.vr[jl];
         }
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-          const float e = s_e[j][r];
+          const float e = s_e[w][jl][r];
           acc[r][0] = fmaf(e, v.x, acc[r][0]);
           acc[r][1] = fmaf(e, v.y, acc[r][1]);
           acc[r][2] = fmaf(e, v.z, acc[r][2]);
@@ -711,30 +816,40 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
         }
       }
     }
-    if (!VQ && t0 + kPlTile < end) {
-      __syncthreads();  // s_e consumed before the next tile's scores
-      nxt.load(a, t0 + kPlTile, tile_len(t0 + kPlTile), g, grp, sub, w, lane, vdw, two);
-    } else {
-      __syncthreads();  // s_e consumed before the next tile's scores
-    }
+    // the weights are consumed before the next tile writes them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+  // merge the four waves: weights e^(m_w - M) per head
 #pragma unroll
   for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int x = 0; x < 4; ++x) s_acc[w][r][4 * lane + x] = acc[r][x];
+  if (lane < REP) {
+    s_wm[w][lane] = run_m;
+    s_wl[w][lane] = run_l;
+  }
+  __syncthreads();
+  if (tid < REP) {
+    const int r = tid;
+    const float big = fmaxf(fmaxf(s_wm[0][r], s_wm[1][r]), fmaxf(s_wm[2][r], s_wm[3][r]));
+    float l = 0.0f;
 #pragma unroll
-  for (int u = 0; u < kSlots; ++u) {
-    const int r = w + 4 * u;
-    if (r < REP && lane == 0) {
-      a.pm[part0 + static_cast<size_t>(r) * a.n_chunks] = run_m[u];
-      a.pl[part0 + static_cast<size_t>(r) * a.n_chunks] = run_l[u];
+    for (int ww = 0; ww < 4; ++ww) {
+      const float wt = s_wm[ww][r] == -INFINITY ? 0.0f : expf(s_wm[ww][r] - big);
+      s_ww[ww][r] = wt;
+      l += s_wl[ww][r] * wt;
     }
+    a.pm[part0 + static_cast<size_t>(r) * a.n_chunks] = big;
+    a.pl[part0 + static_cast<size_t>(r) * a.n_chunks] = l;
   }
   __syncthreads();
   for (int o = tid; o < REP * kHd; o += kBlock) {
-    const int r = o / kHd, d = o % kHd;
-    const float sum = (s_acc[0][r][d] + s_acc[1][r][d]) + (s_acc[2][r][d] + s_acc[3][r][d]);
-    a.pacc[(part0 + static_cast<size_t>(r) * a.n_chunks) * kHd + d] = sum;
+    const int r = o / kHd, dd = o % kHd;
+    const float sum = (s_acc[0][r][dd] * s_ww[0][r] + s_acc[1][r][dd] * s_ww[1][r]) +
+                      (s_acc[2][r][dd] * s_ww[2][r] + s_acc[3][r][dd] * s_ww[3][r]);
+    a.pacc[(part0 + static_cast<size_t>(r) * a.n_chunks) * kHd + dd] = sum;
   }
 }
 
@@ -803,20 +918,6 @@ struct MqArgs {
   // (or V's f32 rows), kn / vn the norms; unused otherwise
   const float *kn, *vn;
 };
-
-// max over the four lanes l % 16 + 16 g (one row): permlane swaps
-__device__ __forceinline__ float rows4_max(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float rows4_sum(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // 2^e as a float for e <= 127; 0 below the normal range
 __device__ __forceinline__ float pow2f(int e) {
