@@ -147,6 +147,20 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// max over the four lanes l % 16 + 16 g (one row): permlane swaps
+__device__ __forceinline__ float rows4_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 struct FMaxOp {
   __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
 };
@@ -157,9 +171,10 @@ template <int REP, class T, int TILE>
 __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
   static_assert(TILE == 32 || TILE == 64, "tiles of 32 or 64 positions");
   constexpr int kPasses = TILE / 16;
-  constexpr int kSlots = (REP + 3) / 4;  // heads owned per wave for the softmax state
-  __shared__ float s_e[TILE][REP];       // scores, then exponentials
-  __shared__ float s_corr[REP];
+  constexpr int kWj = kPasses * 4;  // positions of a wave per tile
+  static_assert(REP <= 16, "one head per lane of a 16-lane group");
+  __shared__ float s_e[4][kWj][REP];  // per wave: P.V weights of its positions
+  __shared__ float s_wm[4][REP], s_wl[4][REP], s_ww[4][REP];
   __shared__ float s_acc[4][REP][kHd];
   __shared__ f32x4 s_q[REP * kHd / 4];
   const T *kc = static_cast<const T *>(a.kc);
@@ -181,6 +196,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
     return;
   }
   const int grp = tid / kQkLanes, sub = tid % kQkLanes;
+  const int grp4 = lane / kQkLanes;  // the lane's group within its wave
   // the group's q rows go to LDS (REP x 256 floats, the kv head's q heads
   // are consecutive), so registers go to the K and V tiles.  They are loaded
   // here and stored to LDS only after the first tile's K (and V) loads are
@@ -197,12 +213,13 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
       qreg[u] = qg[o < kQ4 ? o : kQ4 - 1];
     }
   }
-  float run_m[kSlots], run_l[kSlots];
-#pragma unroll
-  for (int u = 0; u < kSlots; ++u) {
-    run_m[u] = -INFINITY;
-    run_l[u] = 0.0f;
-  }
+  // Each wave runs its own online softmax over the positions it scores
+  // (pass * 16 + 4 w + g, g its lane group): after a pass's DPP row sums
+  // every lane of a group holds the group's REP scores, lane sub keeps head
+  // sub's, the wave's per-head max is two permlane swaps away, and head
+  // sub's running max and sum live in lane sub.  No block barrier inside the
+  // chunk loop but the q stage's; the four waves merge once per chunk.
+  float run_m = -INFINITY, run_l = 0.0f;
   float acc[REP][4];
 #pragma unroll
   for (int r = 0; r < REP; ++r)
@@ -227,7 +244,10 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
         if (o < kQ4) s_q[o] = qreg[u];
       }
     }
-    __syncthreads();  // s_q written (first tile), while the K rows are in flight
+    if (t0 == beg) __syncthreads();  // s_q written, while the K rows are in flight
+    float sc[kPasses];  // head sub's score of the group's position, per pass
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) sc[pass] = -INFINITY;
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
       f32x4 qv[kQkPer / 4];  // head r's 16 dims of this lane, read once per tile
@@ -253,7 +273,7 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
           part[h] = fmaf(q1.w, k1.w, s);
         }
         const float d = row16_sum(part[0] + part[1]);
-        if (sub == 0) s_e[pass * 16 + grp][r] = p < end ? d * a.scale : -INFINITY;
+        if (sub == r) sc[pass] = p < end ? d * a.scale : -INFINITY;
       }
     }
     // the wave's V rows of the tile: issued now (the K registers are free) so
@@ -261,45 +281,44 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
     // the K rows instead, one round trip per tile, they measured slower:
     // ctx 4096 14.0 -> 15.7 us, ctx 32768 55 -> 60 us)
     const int nt = static_cast<int>(end - t0 < static_cast<size_t>(TILE) ? end - t0 : TILE);
-    f32x4 vr[TILE / 4];
+    f32x4 vr[kWj];  // the wave's positions (jl >> 2) * 16 + 4 w + (jl & 3)
 #pragma unroll
-    for (int jj = 0; jj < TILE / 4; ++jj) {
-      const int j = w + 4 * jj;
-      vr[jj] = Kv<T>::load4(vc, (t0 + (j < nt ? j : nt - 1)) * a.kv_stride + head_off + 4 * lane);
+    for (int jl = 0; jl < kWj; ++jl) {
+      const int j = min((jl >> 2) * 16 + 4 * w + (jl & 3), nt - 1);
+      vr[jl] = Kv<T>::load4(vc, (t0 + j) * a.kv_stride + head_off + 4 * lane);
     }
-    __syncthreads();
-    // softmax state: wave w owns heads w, w + 4
+    // head sub's max over the wave's positions (the four groups)
+    float tm = sc[0];
 #pragma unroll
-    for (int u = 0; u < kSlots; ++u) {
-      const int r = w + 4 * u;
-      if (r < REP) {
-        const float s = lane < TILE ? s_e[lane][r] : -INFINITY;
-        const float m_new = fmaxf(run_m[u], wave_max(s));
-        const bool none = m_new == -INFINITY;
-        const float corr = none ? 1.0f : expf(run_m[u] - m_new);
-        const float e = none ? 0.0f : expf(s - m_new);
-        if (lane < TILE) s_e[lane][r] = e;
-        run_l[u] = run_l[u] * corr + wave_sum(e);
-        run_m[u] = m_new;
-        if (lane == 0) s_corr[r] = corr;
-      }
+    for (int pass = 1; pass < kPasses; ++pass) tm = fmaxf(tm, sc[pass]);
+    const float hm = fmaxf(run_m, rows4_max(tm));
+    const float corr_mine = hm == -INFINITY ? 1.0f : expf(run_m - hm);
+    run_m = hm;
+    float ps = 0.0f;
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const float e = hm == -INFINITY ? 0.0f : expf(sc[pass] - hm);
+      ps += e;
+      if (sub < REP) s_e[w][4 * pass + grp4][sub] = e;
     }
-    __syncthreads();
-    // P.V: lane owns dims 4*lane .. +3, wave w takes positions w, w+4, ...
+    run_l = run_l * corr_mine + rows4_sum(ps);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // P.V: lane owns dims 4*lane .. +3 of the wave's positions
 #pragma unroll
     for (int r = 0; r < REP; ++r) {
-      const float cr = s_corr[r];
+      const float cr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr_mine), r));
 #pragma unroll
       for (int x = 0; x < 4; ++x) acc[r][x] *= cr;
     }
 #pragma unroll
-    for (int jj = 0; jj < TILE / 4; ++jj) {
-      const int j = w + 4 * jj;
-      if (j < nt) {
-        const f32x4 v = vr[jj];
+    for (int jl = 0; jl < kWj; ++jl) {
+      if ((jl >> 2) * 16 + 4 * w + (jl & 3) < nt) {
+        const f32x4 v = vr[jl];
 #pragma unroll
         for (int r = 0; r < REP; ++r) {
-          const float e = s_e[j][r];
+          const float e = s_e[w][jl][r];
           acc[r][0] = fmaf(e, v.x, acc[r][0]);
           acc[r][1] = fmaf(e, v.y, acc[r][1]);
           acc[r][2] = fmaf(e, v.z, acc[r][2]);
@@ -307,24 +326,39 @@ __global__ __launch_bounds__(kBlock) void attn_decode_kernel(DecodeArgs a) {
         }
       }
     }
-    __syncthreads();  // s_e and s_corr are rewritten by the next tile
+    // the weights are consumed before the next tile writes them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+  // merge the four waves: weights e^(m_w - M) per head
 #pragma unroll
   for (int r = 0; r < REP; ++r)
 #pragma unroll
     for (int x = 0; x < 4; ++x) s_acc[w][r][4 * lane + x] = acc[r][x];
+  if (lane < REP) {
+    s_wm[w][lane] = run_m;
+    s_wl[w][lane] = run_l;
+  }
+  __syncthreads();
+  if (tid < REP) {
+    const int r = tid;
+    const float big = fmaxf(fmaxf(s_wm[0][r], s_wm[1][r]), fmaxf(s_wm[2][r], s_wm[3][r]));
+    float l = 0.0f;
 #pragma unroll
-  for (int u = 0; u < kSlots; ++u) {
-    const int r = w + 4 * u;
-    if (r < REP && lane == 0) {
-      a.pm[part0 + static_cast<size_t>(r) * a.n_chunks] = run_m[u];
-      a.pl[part0 + static_cast<size_t>(r) * a.n_chunks] = run_l[u];
+    for (int ww = 0; ww < 4; ++ww) {
+      const float wt = s_wm[ww][r] == -INFINITY ? 0.0f : expf(s_wm[ww][r] - big);
+      s_ww[ww][r] = wt;
+      l += s_wl[ww][r] * wt;
     }
+    a.pm[part0 + static_cast<size_t>(r) * a.n_chunks] = big;
+    a.pl[part0 + static_cast<size_t>(r) * a.n_chunks] = l;
   }
   __syncthreads();
   for (int o = tid; o < REP * kHd; o += kBlock) {
     const int r = o / kHd, d = o % kHd;
-    const float sum = (s_acc[0][r][d] + s_acc[1][r][d]) + (s_acc[2][r][d] + s_acc[3][r][d]);
+    const float sum = (s_acc[0][r][d] * s_ww[0][r] + s_acc[1][r][d] * s_ww[1][r]) +
+                      (s_acc[2][r][d] * s_ww[2][r] + s_acc[3][r][d] * s_ww[3][r]);
     a.pacc[(part0 + static_cast<size_t>(r) * a.n_chunks) * kHd + d] = sum;
   }
 }
@@ -477,20 +511,6 @@ template <int kCombWaves, int kCombPer>
 __global__ __launch_bounds__(64 * kCombWaves) void attn_combine1_rot_kernel(
     const float *pm, const float *pl, const float *pacc, int n_chunks, float *out, PlanarTables tb) {
   combine1_body<kCombWaves, kCombPer, true>(pm, pl, pacc, n_chunks, out, tb.gc, tb.gs);
-}
-
-// max over the four lanes l % 16 + 16 g (one row): permlane swaps
-__device__ __forceinline__ float rows4_max(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float rows4_sum(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // ---- planar-quantized caches (src/forward.rs:296-349, src/kvquant.rs) -------
