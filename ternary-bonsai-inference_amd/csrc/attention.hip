@@ -920,6 +920,7 @@ int launch_planar(const PlanarArgs &a, dim3 grid, const PlanarTables &tb, hipStr
 // relative (sums in another order).
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 constexpr int kMqThreads = 512; // 8 waves
 constexpr int kMqRows = 128;    // q rows per block: 8 waves x 16
 constexpr int kMqTile = 32;     // positions per tile
@@ -1376,6 +1377,216 @@ __global__ __launch_bounds__(kMqThreads) void attn_mq_planar_kernel(MqArgs a, Pl
   mq_body<false, PB, VQ>(a, tb.cent, tb.gc, tb.gs);
 }
 
+// Decode over an f16 cache on the matrix cores.  Block (chunk, kv head,
+// query) of 4 waves; each wave streams its own 16-position steps (positions
+// p0 .. p0 + 15, p0 = chunk start + 16 w + 64 k) with its own online softmax
+// and no block barrier.  S^T = K Q^T on v_mfma_f32_16x16x32_f16: the A
+// operand is the K rows themselves (lane l: position p0 + l % 16, 8
+// consecutive f16 dims, one 16-byte load -- no conversion, no staging), B
+// the kv head's REP q rows (zero rows up to 16) split into f16 hi + lo after
+// scaling by 2^a (the multi-query kernel's split).  The lane that ends with
+// a row's scores of four positions holds exactly that row's P fragment of
+// O^T += V^T P^T on v_mfma_f32_16x16x16_f16 (P times 2^14, split hi + lo);
+// V^T comes from the wave's 16 V rows staged in its own LDS slice (16-byte
+// stores, rows padded by 32 bytes so the four lane groups read distinct
+// banks).  The four waves merge once per chunk, as in the VALU kernel.
+template <int REP>
+__global__ __launch_bounds__(kBlock) void attn_decode_f16_mfma_kernel(DecodeArgs a) {
+  static_assert(REP <= 16, "q rows of one MFMA tile");
+  constexpr int kVStr = kHd + 16;  // halves per staged V row
+  __shared__ __attribute__((aligned(16))) _Float16 s_v[4][16 * kVStr];
+  __shared__ float s_wm[4][REP], s_wl[4][REP], s_ww[4][REP];
+  // the waves' accumulators for the merge reuse the V slices
+  static_assert(sizeof(float) * 4 * REP * kHd <= sizeof(_Float16) * 4 * 16 * kVStr, "merge area");
+  auto s_o = reinterpret_cast<float (*)[REP][kHd]>(&s_v[0][0]);
+  __shared__ __attribute__((aligned(16))) _Float16 s_qh[16 * kKStride];  // q hi and lo fragments
+  __shared__ __attribute__((aligned(16))) _Float16 s_ql[16 * kKStride];  // (every wave's)
+  const uint16_t *kc = static_cast<const uint16_t *>(a.kc);
+  const uint16_t *vc = static_cast<const uint16_t *>(a.vc);
+  const int c = blockIdx.x, g = blockIdx.y, i = blockIdx.z;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, grp = l >> 4;
+  const size_t n_pos = a.pos0 + i + 1;
+  const size_t beg = static_cast<size_t>(c) * a.chunk;
+  const size_t end = beg + a.chunk < n_pos ? beg + a.chunk : n_pos;
+  const size_t part0 = (static_cast<size_t>(i) * a.n_head + static_cast<size_t>(g) * REP) *
+                       a.n_chunks + c;
+  if (beg >= end) {  // this query has no positions in the chunk
+    if (tid < REP) {
+      a.pm[part0 + static_cast<size_t>(tid) * a.n_chunks] = -INFINITY;
+      a.pl[part0 + static_cast<size_t>(tid) * a.n_chunks] = 0.0f;
+    }
+    for (int o = tid; o < REP * kHd; o += kBlock)
+      a.pacc[(part0 + static_cast<size_t>(o / kHd) * a.n_chunks) * kHd + o % kHd] = 0.0f;
+    return;
+  }
+  const size_t head_off = static_cast<size_t>(g) * kHd;
+  // q fragments: row r16 (< REP), dims 32 s + 8 grp .. +7, scaled and
+  // split, into LDS (every wave needs the same; wave 0 writes them)
+  _Float16 *qhrow = s_qh + r16 * kKStride + 8 * grp;
+  _Float16 *qlrow = s_ql + r16 * kKStride + 8 * grp;
+  int qa = 0;
+  {
+    const bool rv = r16 < REP;
+    const f32x4 *qr = reinterpret_cast<const f32x4 *>(
+        a.q + (static_cast<size_t>(i) * a.n_head + g * REP + (rv ? r16 : 0)) * kHd + 8 * grp);
+    f32x4 v[16];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      v[2 * s] = rv ? qr[8 * s] : f32x4{0.f, 0.f, 0.f, 0.f};
+      v[2 * s + 1] = rv ? qr[8 * s + 1] : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      m = fmaxf(m, fmaxf(fmaxf(fabsf(v[k].x), fabsf(v[k].y)), fmaxf(fabsf(v[k].z), fabsf(v[k].w))));
+    qa = split_shift(rows4_max(m));
+    const float f = ldexpf(1.0f, qa);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 x = v[2 * s + h];
+        _Float16 hi, lo;
+        half4v hi4, lo4;
+        split_hl(x.x * f, hi, lo); hi4[0] = hi; lo4[0] = lo;
+        split_hl(x.y * f, hi, lo); hi4[1] = hi; lo4[1] = lo;
+        split_hl(x.z * f, hi, lo); hi4[2] = hi; lo4[2] = lo;
+        split_hl(x.w * f, hi, lo); hi4[3] = hi; lo4[3] = lo;
+        if (w == 0) {
+          *reinterpret_cast<half4v *>(qhrow + 32 * s + 4 * h) = hi4;
+          *reinterpret_cast<half4v *>(qlrow + 32 * s + 4 * h) = lo4;
+        }
+      }
+  }
+  __syncthreads();  // s_qh, s_ql
+  const float qunscale = ldexpf(a.scale, -qa);  // scores: S' * 2^-a * (1/sqrtf(hd))
+  f32x4 o[16];
+#pragma unroll
+  for (int dt = 0; dt < 16; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float run_m = -INFINITY, run_l = 0.0f;  // row r16's (the same in the four groups)
+  _Float16 *sv = s_v[w];
+  u32x4v kf[8];  // ext vectors: a HIP vector-struct array here is kept in scratch
+  auto load_k = [&](size_t p0) {
+    const size_t pos = p0 + r16 < end ? p0 + r16 : end - 1;
+    const uint16_t *src = kc + pos * a.kv_stride + head_off + 8 * grp;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) kf[s] = *reinterpret_cast<const u32x4v *>(src + 32 * s);
+  };
+  // the 16 V rows: 16-byte unit e = 64 k + l of the wave's 512 is unit
+  // e % 32 of row e / 32
+  u32x4v vr[8];
+  auto load_v = [&](size_t p0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = 64 * k + l, pj = e >> 5, u = e & 31;
+      const size_t pos = p0 + pj < end ? p0 + pj : end - 1;
+      vr[k] = *reinterpret_cast<const u32x4v *>(vc + pos * a.kv_stride + head_off + 8 * u);
+    }
+  };
+  size_t p0 = beg + 16 * w;
+  if (p0 < end) {
+    load_k(p0);
+    load_v(p0);
+  }
+  for (; p0 < end; p0 += 64) {
+    f32x4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const half8 ka = __builtin_bit_cast(half8, kf[s]);
+      st = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          ka, *reinterpret_cast<const half8 *>(qhrow + 32 * s), st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          ka, *reinterpret_cast<const half8 *>(qlrow + 32 * s), st, 0, 0, 0);
+    }
+    if (p0 + 64 < end) load_k(p0 + 64);  // the next step's K rows, in flight during this one
+    // row r16's scores of positions p0 + 4 grp + j
+    float sc[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sc[j] = p0 + 4 * grp + j < end ? st[j] * qunscale : -INFINITY;
+      tmax = fmaxf(tmax, sc[j]);
+    }
+    const float m_new = fmaxf(run_m, rows4_max(tmax));
+    const bool none = m_new == -INFINITY;
+    const float corr = none ? 1.0f : expf(run_m - m_new);
+    float ps = 0.0f;
+    half4v ph, pl;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = none ? 0.0f : expf(sc[j] - m_new);
+      ps += p;
+      _Float16 hi, lo;
+      split_hl(p * 16384.0f, hi, lo);
+      ph[j] = hi;
+      pl[j] = lo;
+    }
+    run_l = run_l * corr + rows4_sum(ps);
+    run_m = m_new;
+    if (__builtin_amdgcn_ballot_w64(corr != 1.0f) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) o[dt] = o[dt] * corr;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int e = 64 * k + l, pj = e >> 5, u = e & 31;
+      *reinterpret_cast<u32x4v *>(sv + pj * kVStr + 8 * u) = vr[k];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (p0 + 64 < end) load_v(p0 + 64);  // the next step's V rows, in flight during P.V and its scores
+    // O^T += V^T P^T: A = V^T rows 16 dt + r16, positions 4 grp .. +3
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      half4v va;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) va[j] = sv[(4 * grp + j) * kVStr + 16 * dt + r16];
+      f32x4 acc = o[dt];
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc, 0, 0, 0);
+      o[dt] = acc;
+    }
+    // the staged rows are consumed before the next step writes them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  // merge the four waves: weights e^(m_w - M) per head
+  __syncthreads();  // every wave is done with its V slice
+  if (r16 < REP) {
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_o[w][r16][16 * dt + 4 * grp + j] = o[dt][j] * (1.0f / 16384.0f);
+    if (grp == 0) {
+      s_wm[w][r16] = run_m;
+      s_wl[w][r16] = run_l;
+    }
+  }
+  __syncthreads();
+  if (tid < REP) {
+    const int r = tid;
+    const float big = fmaxf(fmaxf(s_wm[0][r], s_wm[1][r]), fmaxf(s_wm[2][r], s_wm[3][r]));
+    float lsum = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float wt = s_wm[ww][r] == -INFINITY ? 0.0f : expf(s_wm[ww][r] - big);
+      s_ww[ww][r] = wt;
+      lsum += s_wl[ww][r] * wt;
+    }
+    a.pm[part0 + static_cast<size_t>(r) * a.n_chunks] = big;
+    a.pl[part0 + static_cast<size_t>(r) * a.n_chunks] = lsum;
+  }
+  __syncthreads();
+  for (int x = tid; x < REP * kHd; x += kBlock) {
+    const int r = x / kHd, dd = x % kHd;
+    const float sum = (s_o[0][r][dd] * s_ww[0][r] + s_o[1][r][dd] * s_ww[1][r]) +
+                      (s_o[2][r][dd] * s_ww[2][r] + s_o[3][r][dd] * s_ww[3][r]);
+    a.pacc[(part0 + static_cast<size_t>(r) * a.n_chunks) * kHd + dd] = sum;
+  }
+}
+
 // Chunk merge of the multi-query path (few chunks, many rows): one block of
 // four waves per (query, head) row, wave w owning dims 64 w .. 64 w + 63 (one
 // per lane).  Every wave weighs the chunks itself -- e^(m_c - M) from the
@@ -1513,6 +1724,10 @@ __global__ __launch_bounds__(kBlock) void attn_pv_kernel(GenericArgs a) {
 
 template <int REP, class T>
 int launch_decode(const DecodeArgs &a, int n_kv, int n_q, hipStream_t st) {
+  if constexpr (std::is_same<T, uint16_t>::value) {  // f16: the matrix-core form
+    BH_LAUNCH((attn_decode_f16_mfma_kernel<REP>), dim3(a.n_chunks, n_kv, n_q), kBlock, 0, st, a);
+    return ok();
+  }
   if (a.tile == 32)
     BH_LAUNCH((attn_decode_kernel<REP, T, 32>), dim3(a.n_chunks, n_kv, n_q), kBlock, 0, st, a);
   else
