@@ -136,19 +136,23 @@ def test_graph_softmax_survives_scratch_growth(bh, oracle, synth, dev):
             torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("n_q,pos0", [(1, 4095), (3, 63)])
-def test_graph_attention_decode(bh, synth, dev, n_q, pos0):
-    """The decode attention merges its chunks inside the launch (device-scope
-    arrival counters that the last arriver resets): every replay, with eager
-    calls in between, reproduces the eager result bit for bit (the merge
-    order does not depend on which block arrives last)."""
+@pytest.mark.parametrize("n_q,pos0,f16", [(1, 4095, False), (3, 63, False), (1, 4095, True),
+                                          (2, 700, True)])
+def test_graph_attention_decode(bh, synth, dev, n_q, pos0, f16):
+    """The decode attention (chunk partials in library scratch, then the
+    chunk merge; for an f16 cache the matrix-core kernel): every replay,
+    with eager calls in between, reproduces the eager result bit for bit."""
     import torch
     n_head, n_kv, hd = 24, 4, 256
     r = synth.Rng(77 + n_q)
     n = pos0 + n_q
     q = _t(r.normal(n_q * n_head * hd).reshape(n_q, n_head, hd).astype(np.float32), dev)
-    kc = _t(r.normal(n * n_kv * hd).reshape(n, n_kv * hd).astype(np.float32), dev)
-    vc = _t(r.normal(n * n_kv * hd).reshape(n, n_kv * hd).astype(np.float32), dev)
+    kn = r.normal(n * n_kv * hd).reshape(n, n_kv * hd).astype(np.float32)
+    vn = r.normal(n * n_kv * hd).reshape(n, n_kv * hd).astype(np.float32)
+    if f16:
+        kn = kn.astype(np.float16).view(np.uint16)
+        vn = vn.astype(np.float16).view(np.uint16)
+    kc, vc = _t(kn, dev), _t(vn, dev)
 
     def make_out():
         return [torch.empty_like(q)]
