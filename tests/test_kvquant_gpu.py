@@ -83,6 +83,8 @@ def test_kv_store_planar_f32_v_and_offset(bh, oracle, synth, dev):
     (4, True, 1, 32, 24, 4),       # a tile and one position
     (4, True, 1, 4095, 24, 4),     # the model's decode at ctx 4096
     (3, True, 1, 9000, 24, 4),     # several tiles per chunk, ragged last chunk
+    (2, True, 1, 2000, 24, 4),     # 2-bit K and V
+    (8, True, 1, 5000, 16, 2),     # 8-bit, groups of 8
     (2, False, 1, 700, 24, 4),     # V in f32 (planarNk)
     (8, True, 3, 100, 24, 4),      # several queries
     (1, True, 2, 63, 8, 8),        # one q head per kv head
