@@ -1864,7 +1864,7 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
     if (scratch == nullptr) return BH_ERR_HIP;
     MqArgs m{q, k_cache, v_cache, scratch, scratch + rows, scratch + 2 * rows, pos0, kv_stride,
              chunk, static_cast<int>(n_head), static_cast<int>(n_q), static_cast<int>(rep),
-             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale};
+             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale, nullptr, nullptr};
     // 1-D grid of (chunk, kv head, row tile) in XCD-aware order (the kernel
     // decodes it)
     const size_t nb = n_chunks * n_kv * tiles_r;

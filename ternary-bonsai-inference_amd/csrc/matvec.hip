@@ -798,12 +798,6 @@ __device__ __forceinline__ void q1_digits(float (&f)[16], uint4 frag[4], float2 
   for (int d = 0; d < 4; ++d) frag[d] = make_uint4(dg[d][0], dg[d][1], dg[d][2], dg[d][3]);
   fac = make_float2(__int_as_float(sx), bad ? __builtin_nanf("") : ldexpf(1.0f, -ex));
 }
-__device__ __forceinline__ void q1_prep_item(const float *xb, int s, bool live, uint4 frag[4],
-                                             float2 &fac) {
-  float f[16];
-  q1_load_item(xb, s, live, f);
-  q1_digits(f, frag, fac);
-}
 
 // Digit fragments of x into LDS by all `lanes` lanes of the workgroup:
 // uint4 (8 Q + s) * 16 + 4 j + d for block 4 Q + j, step s, digit d; block

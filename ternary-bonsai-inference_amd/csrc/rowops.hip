@@ -431,12 +431,6 @@ __device__ __forceinline__ double ms_scaled(const MaxSum &a, double M) {
   return a.m == -INFINITY ? a.s : a.s * exp(static_cast<double>(a.m) - M);
 }
 
-__device__ __forceinline__ MaxSum ms_merge(MaxSum a, MaxSum b) {
-  const float M = b.m > a.m ? b.m : a.m;
-  const double dM = static_cast<double>(M);
-  return MaxSum{M, ms_scaled(a, dM) + ms_scaled(b, dM)};
-}
-
 // Split-row pass 1: block (c, r) reduces chunk c of row r (kSplitVPT float4
 // per lane, loaded up front) to (max, sum of e^(y - max)).  The chunk max
 // comes first, so each element costs one exponential.  Both passes are
