@@ -46,20 +46,6 @@ constexpr int kPq2Block = 34;
 constexpr size_t kMaxSeqSmem = 128 * 1024;  // LDS cap of a fused block (gfx950: 160 KB per CU)
 
 
-// Decodes float4 number f (weights 4f..4f+3 of the row) from the staged row.
-__device__ __forceinline__ float4 decode4(const uint8_t *rowb, int f) {
-  const int b = f >> 5;  // 32 float4 per 128-weight block
-  const int q = f & 31;
-  const uint8_t *blk = rowb + b * kPq2Block;
-  const uint32_t h = static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8);
-  const float scale = __uint_as_float(half_bits_to_f32_bits(h));
-  const bool finite = (h & 0x7c00u) != 0x7c00u;
-  const uint32_t c = blk[2 + q];
-  return make_float4(pq2_weight(c & 3u, scale, finite), pq2_weight((c >> 2) & 3u, scale, finite),
-                     pq2_weight((c >> 4) & 3u, scale, finite),
-                     pq2_weight((c >> 6) & 3u, scale, finite));
-}
-
 // ---------------------------------------------------------------------------
 // Fused gather + RMSNorm with the reference's sequential f32 sum of squares:
 // one launch, one block of kFusedThreads lanes per kFusedRows output rows.
