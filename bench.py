@@ -563,9 +563,6 @@ def main() -> int:
                     help="after the headline, time only the entries whose name matches this regex")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="length of the CPU-baseline sample (0 disables)")
-    ap.add_argument("--ceiling", action="store_true",
-                    help="only run the streaming-ceiling diagnostic (plain copy / read / write "
-                         "at the bench's sizes) and print its table")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -574,14 +571,6 @@ def main() -> int:
               "(every kernel is row-independent: multi-GPU runs would shard rows with no "
               "exchange)", file=sys.stderr)
         return 2
-
-    if args.ceiling:
-        import subprocess
-        exe = PKG_DIR / "lib" / "stream_ceiling"
-        if not exe.exists():
-            print(f"bench.py: {exe} missing: run __graft_entry__.build()", file=sys.stderr)
-            return 2
-        return subprocess.run([str(exe)]).returncode
 
     import torch
     if not torch.cuda.is_available():

@@ -66,23 +66,6 @@ def build_library(jobs: int | None = None) -> Path:
     return LIB
 
 
-DIAG_SRC = PKG / "diag" / "stream_ceiling.hip"
-DIAG_BIN = PKG / "lib" / "stream_ceiling"
-
-
-def build_diag() -> Path:
-    """The streaming-ceiling diagnostic (plain copy / read / write at the
-    bench's sizes; `python bench.py --ceiling` runs it)."""
-    DIAG_BIN.parent.mkdir(exist_ok=True)
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O3", "-std=c++17",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           str(DIAG_SRC), "-o", str(DIAG_BIN)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"stream_ceiling failed to build:\n{res.stderr}")
-    return DIAG_BIN
-
-
 CPP_TEST_SRC = REPO / "tests" / "cpp" / "test_kernels.cpp"
 CPP_TEST_BIN = REPO / "tests" / "cpp" / "test_kernels"
 
@@ -113,6 +96,5 @@ def clean() -> None:
 
 if __name__ == "__main__":
     print(build_library())
-    print(build_diag())
     print(build_cpp_tests())
     print(build_oracle())

@@ -386,6 +386,38 @@ def test_silu_l2_part_unit_heads(oracle):
         oracle.silu_l2_part(conv, 200, 128, 1e-6)
 
 
+# --- src/forward.rs:524 (SiLU over the conv output), :539-540 (l2_norm_rows on
+#     the q/k heads): the fused oracle equals the composition of the pinned
+#     pieces bit for bit, and a float64 restatement within 2e-6.  A dropped
+#     SiLU (heads of the raw conv) passes the unit-norm check above but fails
+#     both of these.
+@pytest.mark.parametrize("n_tok,conv_dim,l2_dim,hd", [(3, 512, 256, 128), (17, 1280, 1024, 128),
+                                                      (5, 96, 64, 32)])
+def test_silu_l2_part_is_silu_then_pinned_l2(oracle, n_tok, conv_dim, l2_dim, hd):
+    rng = np.random.default_rng(11 + conv_dim)
+    conv = (rng.standard_normal((n_tok, conv_dim)) * 2).astype(np.float32)
+    conv[0, :hd] = 0.0                      # a zero head: the eps floor branch
+    eps = 1e-6
+    out = oracle.silu_l2_part(conv, l2_dim, hd, eps)
+    act = oracle.unary(0, conv)
+    want = act.copy()
+    want[:, :l2_dim] = oracle.l2_norm_rows(np.ascontiguousarray(act[:, :l2_dim]), hd,
+                                           eps).reshape(n_tok, l2_dim)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    # float64: silu, then each head divided by max(its f64 norm, eps)
+    xd = conv.astype(np.float64)
+    sd = xd / (1 + np.exp(-xd))
+    heads = sd[:, :l2_dim].reshape(n_tok, l2_dim // hd, hd)
+    norm = np.maximum(np.sqrt((heads ** 2).sum(-1, keepdims=True)), eps)
+    ref = sd.copy()
+    ref[:, :l2_dim] = (heads / norm).reshape(n_tok, l2_dim)
+    assert np.max(np.abs(out - ref)) <= 2e-6
+    assert np.all(out[0, :hd] == 0.0)
+    # a dropped SiLU is caught: raw-conv heads differ well beyond the bound
+    raw = oracle.l2_norm_rows(np.ascontiguousarray(conv[:, :l2_dim]), hd, eps)
+    assert np.max(np.abs(raw.reshape(n_tok, l2_dim) - out[:, :l2_dim])) > 1e-2
+
+
 def test_unary_modes_closed_form(oracle):
     x = np.linspace(-30, 30, 1001).astype(np.float32)
     b = np.linspace(2, -2, 1001).astype(np.float32)
