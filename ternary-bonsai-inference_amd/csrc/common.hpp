@@ -77,6 +77,17 @@ struct SumOp {
   template <class T> __device__ T operator()(T a, T b) const { return a + b; }
 };
 // max that ignores NaN in the candidate, like the reference's `if v > max`.
+// RMSNorm row scale 1 / sqrt(ss / n + eps) (src/kernels.rs:69-70) with the
+// mean as a multiply by the f32 reciprocal of n (exact for powers of two,
+// <= 1 ulp otherwise) and the hardware reciprocal square root (<= 1 ulp):
+// a few ulps from the correctly rounded divide and square root, far inside
+// the 1e-5 bar, and about twenty instructions shorter on the path between a
+// row's loads and its stores (measured: 21.9 -> 20.9 us on config 2's
+// attention pre-block).
+__device__ __forceinline__ float rms_scale(float ss, float inv_n, float eps) {
+  return __builtin_amdgcn_rsqf(ss * inv_n + eps);
+}
+
 struct MaxOp {
   __device__ float operator()(float a, float b) const { return b > a ? b : a; }
 };

@@ -47,6 +47,7 @@ struct RopeParams {
   int s0, s1, s2, sect;
   float theta_scale;
   float eps;
+  float inv_hd;  // 1 / head_dim
 };
 
 // theta of pair j at the given positions, band selection of src/rope.rs:37-49,
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(kMaxBlock) void qk_norm_rope_kernel(RopeParams a, i
         ss += vv[v].w * vv[v].w;
       }
       ss = lane_group_sum<G>(ss);
-      const float scale = 1.0f / sqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
+      const float scale = rms_scale(ss, a.inv_hd, a.eps);
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const float4 w = is_q ? wq[v] : wk[v];
@@ -251,7 +252,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_loop_kernel(RopeParams a) {
     float ss = 0.0f;
     for (int d = threadIdx.x; d < a.head_dim; d += 64) ss += src[d] * src[d];
     ss = group_reduce<64>(ss, SumOp{}, lds);
-    scale = 1.0f / sqrtf(ss / static_cast<float>(a.head_dim) + a.eps);
+    scale = rms_scale(ss, a.inv_hd, a.eps);
   }
   for (int d = threadIdx.x; d < a.head_dim; d += 64)
     rowbuf[d] = NORM ? (src[d] * scale) * w[d] : src[d];
@@ -358,6 +359,7 @@ int check_rope_common(size_t head_dim, size_t n_dims, const int32_t *sections, R
   p.s2 = sections[2];
   p.sect = static_cast<int>(sect);
   p.head_dim = static_cast<int>(head_dim);
+  p.inv_hd = head_dim ? 1.0f / static_cast<float>(head_dim) : 0.0f;
   p.n_dims = static_cast<int>(n_dims);
   // src/rope.rs:23 -- the C library's powf, as Rust's f32::powf calls it
   p.theta_scale = powf(freq_base, -2.0f / static_cast<float>(n_dims));

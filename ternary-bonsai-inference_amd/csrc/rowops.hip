@@ -214,7 +214,7 @@ __global__ __launch_bounds__(1024) void rms_rows_kernel(
     ss += v[i].w * v[i].w;
   }
   ss = row_reduce<G>(ss, SumOp{}, lds);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(row_len) + eps);
+  const float scale = rms_scale(ss, 1.0f / static_cast<float>(row_len), eps);
   const float4 *w4 = reinterpret_cast<const float4 *>(w);
   float4 *o4 = reinterpret_cast<float4 *>(out) + off;
 #pragma unroll
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kBlock) void rms_rows_loop_kernel(
     ss += v * v;
   }
   ss = group_reduce<kBlock>(ss, SumOp{}, lds);
-  const float scale = 1.0f / sqrtf(ss / static_cast<float>(row_len) + eps);
+  const float scale = rms_scale(ss, 1.0f / static_cast<float>(row_len), eps);
   for (int c = threadIdx.x; c < row_len; c += kBlock) {
     // each thread re-reads exactly the elements it wrote, so sum_out == x is safe
     const float v = ADD ? sum_out[off + c] : x[off + c];

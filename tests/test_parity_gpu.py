@@ -544,6 +544,36 @@ def test_pq2_gather_rms_every_f16_scale(bh, oracle, synth, dev):
     assert np.array_equal(np.isnan(gn), np.isnan(ref_n))
 
 
+@pytest.mark.parametrize("case", ["few_scales", "big_then_tiny", "ties", "unit_scale"])
+def test_pq2_gather_rms_closed_form_edge_rows(bh, oracle, synth, dev, case):
+    """Rows whose sequential sum of squares is easy to get wrong: one scale
+    repeated over many blocks (long runs across powers of two), a large scale
+    followed by tiny ones (the sum stops moving), power-of-two scales (sums
+    that land on rounding ties), and scale 1.0 (exact integer sums).  Both
+    outputs bit-exact against the reference's sequential loop."""
+    rows, ne0 = 96, 40 * 128
+    rng = np.random.default_rng({"few_scales": 1, "big_then_tiny": 2, "ties": 3, "unit_scale": 4}[case])
+    codes = rng.choice(np.array([0, 1, 2], np.uint8), size=(rows, ne0), p=[0.3, 0.4, 0.3])
+    if case == "few_scales":
+        pool = rng.integers(0x0400, 0x7400, size=(rows, 3)).astype(np.uint16)
+        scales = np.take_along_axis(pool, rng.integers(0, 3, size=(rows, 40)), 1)
+    elif case == "big_then_tiny":
+        scales = rng.integers(1, 0x1000, size=(rows, 40)).astype(np.uint16)
+        scales[:, 0] = rng.integers(0x7000, 0x7400, size=rows)
+    elif case == "ties":
+        # scale 2^k: squares are powers of two, so sums land on ties often
+        scales = (rng.integers(5, 25, size=(rows, 40)) << 10).astype(np.uint16)
+    else:
+        scales = np.full((rows, 40), 0x3c00, np.uint16)
+    table = synth.pack_pq2_rows(codes, scales)
+    ids = rng.permutation(rows).astype(np.uint32)
+    w = synth.Rng(19).normal(ne0, 1.0, 0.1)
+    e, n = bh.pq2_embed_gather(_t(table, dev), ne0, rows, _t(ids, dev), w=_t(w, dev), eps=1e-6)
+    ref_e, ref_n = oracle.embed_gather(table, ne0, rows, ids, w, 1e-6)
+    assert bits_equal(_h(e), ref_e)
+    assert bits_equal(_h(n), ref_n)
+
+
 @pytest.mark.parametrize("ne0", [128, 200, 256, 5120, 130])
 def test_pq2_gather_shapes(bh, oracle, synth, dev, ne0):
     table = synth.pq2_table(synth.Rng(ne0), 50, ne0)
