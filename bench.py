@@ -639,6 +639,8 @@ def main() -> int:
                  lambda: wl_attention(bh, synth, dev, stream, 1, 32767, True)),
                 ("attention batch 64 queries ctx=4096 f32",
                  lambda: wl_attention(bh, synth, dev, stream, 64, 4032, False)),
+                ("attention prefill 2048 queries from 0 f32",
+                 lambda: wl_attention(bh, synth, dev, stream, 2048, 0, False)),
                 ("attention decode ctx=32768 planar4",
                  lambda: wl_attention_planar(bh, synth, dev, stream, 1, 32767, 4)),
                 ("attention decode ctx=4096 planar4",
@@ -660,6 +662,17 @@ def main() -> int:
                 if re.search(args.only, name):
                     kernels.append(measure_mm(name, rows, ne0, n_tok, bh, synth, dev, stream,
                                               ksteps, args.warmup))
+            for k in kernels:
+                if k["kernel"].startswith("attention prefill 2048"):
+                    # causal prefill: scores and P.V each 2 flops per (query, head,
+                    # visible position, dim); query i sees i + 1 positions
+                    n, heads, hd = 2048, 24, 256
+                    flops = 2 * 2 * heads * hd * (n * (n + 1) // 2)
+                    tf = flops / (k["ms"] * 1e-3) / 1e12
+                    k.update({"useful_flops": flops, "TFLOPs": round(tf, 2),
+                              "frac_mfma_f16": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                              "note": "f32 operands as f16 hi + lo: three MFMA products per "
+                                      "useful one, so a third of the f16 peak is its ceiling"})
 
     cpu = None
     if args.cpu_seconds > 0:

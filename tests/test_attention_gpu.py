@@ -192,3 +192,33 @@ def test_attention_multi_query_matrix_cores(bh, oracle, synth, dev, n_q, pos0, f
     err = rel_err(got, ref)
     _say("  rel", err)
     assert err <= TOL
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_attention_prefill_2048_from_position_0(bh, oracle, synth, dev, f16):
+    """The prefill shape behind config 4b's scores: 2048 causal queries from
+    position 0 on the model's heads (src/forward.rs:273-375 run for a whole
+    window, as GDev::prefill_batch does).  The whole batch runs in one call;
+    sampled query rows (the first, chunk and tile edges, the last) are
+    checked against the oracle's per-token loop at their own positions, and
+    query 0 -- which sees position 0 alone, so its softmax is exactly 1 --
+    must return v_0 of its kv head (to the f16 hi + lo products' 2^-21)."""
+    n_head, n_kv, hd = MODEL
+    n = 2048
+    _say("attention prefill 2048", "f16" if f16 else "f32")
+    q, kc, vc = _case(synth, n, 0, n_head, n_kv, hd, 911 + int(f16))
+    if f16:
+        kc = kc.astype(np.float16).view(np.uint16)
+        vc = vc.astype(np.float16).view(np.uint16)
+    got = _run(bh, dev, q, 0, kc, vc, n_kv)
+    assert np.all(np.isfinite(got))
+    v0 = (vc[0].view(np.float16).astype(np.float32) if f16 else vc[0]).reshape(n_kv, hd)
+    grp = n_head // n_kv
+    for h in range(n_head):
+        assert rel_err(got[0, h], v0[h // grp]) <= 1e-6
+    worst = 0.0
+    for i in (1, 2, 63, 64, 127, 511, 1000, 1023, 1024, 1535, 2046, 2047):
+        ref = oracle.attention(q[i:i + 1], i, kc[:i + 1], vc[:i + 1], n_kv)
+        worst = max(worst, rel_err(got[i:i + 1], ref))
+    _say("  rel (sampled rows)", worst)
+    assert worst <= TOL
