@@ -631,6 +631,7 @@ def main() -> int:
                 ("pq2_gather_rms T=8192", lambda: wl_gather_rms(bh, synth, dev, stream)),
                 ("gdn_step decode T=1", lambda: wl_gdn_step(bh, synth, dev, stream, 1)),
                 ("gdn_step T=256", lambda: wl_gdn_step(bh, synth, dev, stream, 256)),
+                ("gdn_step T=2048", lambda: wl_gdn_step(bh, synth, dev, stream, 2048)),
                 ("attention decode ctx=4096 f32",
                  lambda: wl_attention(bh, synth, dev, stream, 1, 4095, False)),
                 ("attention decode ctx=32768 f32",

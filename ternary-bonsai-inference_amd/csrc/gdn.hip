@@ -40,7 +40,27 @@ struct GdnStepArgs {
   size_t n_tok;
   int h_k, h_v, s;
   float scale;
+  int xcd_map;  // 1: place the blocks of one q/k head on one XCD (see row_tile)
 };
+
+// The row tile (of `bph` per v-head) a block works on.  Workgroups go to the
+// chip's 8 XCDs round robin (block b to XCD b % 8), and every block of the
+// v-heads that share a q/k head reads that head's q and k rows; with
+// xcd_map the blocks are renumbered so all of them land on one XCD and its
+// L2 serves the re-reads (otherwise each XCD would fetch them from HBM):
+// XCD x takes the q/k heads x, x + 8, ..., each with its rep * bph blocks.
+// Used when h_k % 8 == 0 and h_v % h_k == 0 (the model's 16 / 48 heads);
+// it changes which block does what, never the results.
+__device__ __forceinline__ int row_tile(const GdnStepArgs &a, int bph) {
+  const int p = static_cast<int>(blockIdx.x);
+  if (!a.xcd_map) return p;
+  const int g = (a.h_v / a.h_k) * bph;  // blocks per q/k head
+  const int x = p % 8, sl = p / 8;
+  const int kh = (sl / g) * 8 + x;
+  const int local = sl % g;
+  const int h = kh + (local / bph) * a.h_k;
+  return h * bph + local % bph;
+}
 
 // Sum over the 16 lanes of a row group (lanes 16r .. 16r+15), every lane
 // receiving the same total: DPP swaps within quads (xor 1, xor 2), then
@@ -106,7 +126,8 @@ __device__ __forceinline__ void store_state(float *mp, const float (&m)[kPerLane
 // Few tokens (decode): each lane loads its token inputs straight from
 // global memory, the next token's while the current one computes.
 __global__ __launch_bounds__(kBlock) void gdn_step128_direct_kernel(GdnStepArgs a) {
-  const int row = blockIdx.x * kRowsPerBlock + threadIdx.x / kLanesPerRow;  // h * 128 + j
+  const int row = row_tile(a, kFast / kRowsPerBlock) * kRowsPerBlock +
+                  threadIdx.x / kLanesPerRow;  // h * 128 + j
   const int sub = threadIdx.x % kLanesPerRow;
   const int h = row / kFast, j = row % kFast;
   const int kh = h % a.h_k;
@@ -275,7 +296,7 @@ template <int L>
 __global__ __launch_bounds__(kBlock) void gdn_step128_kernel(GdnStepArgs a) {
   using S = StagedShape<L>;
   __shared__ ChunkLds<S::kRows> lds;
-  const int row0 = blockIdx.x * S::kRows;  // h * 128 + j0
+  const int row0 = row_tile(a, kFast / S::kRows) * S::kRows;  // h * 128 + j0
   const int rl = threadIdx.x / L;
   const int sub = threadIdx.x % L;
   const int h = row0 / kFast, j0 = row0 % kFast;
@@ -427,7 +448,8 @@ extern "C" int bh_gdn_step(const float *q, const float *k, const float *v, const
     return fail(BH_ERR_ARG, "gdn_step: null pointer");
   GdnStepArgs a{q, k, v, gate, beta, state, attn, n_tok, static_cast<int>(h_k),
                 static_cast<int>(h_v), static_cast<int>(s),
-                1.0f / sqrtf(static_cast<float>(s))};  // src/gdn.rs:31, f32 on the host
+                1.0f / sqrtf(static_cast<float>(s)),  // src/gdn.rs:31, f32 on the host
+                (h_k % 8 == 0 && h_v % h_k == 0) ? 1 : 0};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool fast =
       s == static_cast<size_t>(kFast) && aligned16(q) && aligned16(k) && aligned16(state);
