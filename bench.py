@@ -528,14 +528,20 @@ def cpu_baselines_other(bh, synth, oracle, seconds: float):
                           lambda lo, hi: oracle.softmax_rows(xb[lo:hi], 2048), 2048, 2048 * 8, 1,
                           seconds, "oracle softmax_rows on one head's 2048 causal rows"))
     # config 5: gather + first RMSNorm (src/forward.rs:691, 701-702)
-    tab = synth.pq2_table(synth.Rng(5), 16384, 5120)
-    ids = (synth.Rng(6).u64(1024) % np.uint64(16384)).astype(np.uint32)
+    # the full 248320-row table (338 MB, built on the device and copied to
+    # host memory), so the CPU gathers rows that are not cache-resident,
+    # as the GPU does
+    import torch
+    tab = synth.torch_pq2_table(248320, 5120, torch.device("cuda:0")).cpu().numpy()
+    ids = (synth.Rng(6).u64(1024) % np.uint64(248320)).astype(np.uint32)
     w5 = synth.Rng(7).normal(5120, 1.0, 0.1)
     per5 = 1360 + 4 + 2 * 5120 * 4
     out.append(_cpu_entry("config 5 pq2_gather_rms [8192 ids, 248320x5120]",
-                          lambda lo, hi: oracle.embed_gather(tab, 5120, 16384, ids[lo:hi], w5,
+                          lambda lo, hi: oracle.embed_gather(tab, 5120, 248320, ids[lo:hi], w5,
                                                              1e-6), 1024, per5, 1, seconds,
-                          "oracle embed_gather + rms on 1024 ids from a 16384-row table"))
+                          "oracle embed_gather + rms on 1024 uniform ids from the full "
+                          "248320-row table (338 MB in host memory)"))
+    del tab
     return out
 
 

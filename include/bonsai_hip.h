@@ -65,6 +65,17 @@ const char *bh_last_error(void);
 /* Library identification string (version, target architecture). */
 const char *bh_version(void);
 
+/* Scratch housekeeping (no counterpart in the reference, whose kernels run
+ * on the host).  A scratch buffer that grows keeps the buffer it replaces
+ * until the process ends (a captured graph may still hold its address);
+ * bh_scratch_retired_bytes reports how many bytes those retired buffers hold
+ * on all devices, and bh_scratch_release synchronizes each device that has
+ * any and frees them -- for callers that know no captured graph still uses
+ * an old buffer (e.g. after a one-off very large call).  Not to be called
+ * while other threads run library calls. */
+size_t bh_scratch_retired_bytes(void);
+int bh_scratch_release(void);
+
 /* ---------------------------------------------------------------------------
  * Normalisation (src/kernels.rs:58-145)
  * ------------------------------------------------------------------------- */
@@ -228,7 +239,11 @@ int bh_kv_store_planar(const float *k, const float *v, size_t n_tok, size_t n_kv
  * V quantized: the (p_j |v_j|)-weighted centroid sum turned back by the
  * inverse rotation; V in f32 (vq = vn = NULL): p . v_f32.  q, out
  * [n_q][n_head][hd]; n_head / n_kv in {1, 2, 3, 4, 6, 8}.  Uses library
- * scratch (like bh_attention). */
+ * scratch (like bh_attention).  A position whose probability is 0 adds
+ * nothing, as the reference skips it (src/forward.rs:335) -- except on the
+ * matrix-core path (many queries per kv head), where a quantized V row with
+ * an infinite norm |v_j| gives NaN outputs for the rows that do not see it
+ * (0 x inf inside the tile product); finite norms are unaffected. */
 int bh_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *kq,
                         const float *kn, const uint8_t *vq, const float *vn, const float *v_f32,
                         unsigned bits, size_t n_head, size_t n_kv, size_t hd, float *out,

@@ -1,7 +1,17 @@
-// build.rs -- compile the HIP kernels for gfx950 and link them
+// build.rs -- compile the HIP kernels for gfx950 and link them.
+//
+// These are lines to add to the reference's existing build script: call
+// build_hip() from its fn main() (this file has no main of its own).
+// Layout it expects, relative to the crate root (where build.rs lives):
+//   hip/csrc/     the csrc/ directory of this repository
+//   include/      the include/ directory of this repository
+// csrc/common.hpp includes "../../include/bonsai_hip.h", which from
+// hip/csrc/ resolves to include/ at the crate root.
 fn build_hip() {
     let out = std::path::PathBuf::from(std::env::var("OUT_DIR").unwrap());
     let src = "hip/csrc"; // the csrc/ directory of this repository, vendored
+    assert!(std::path::Path::new("include/bonsai_hip.h").exists(),
+            "vendor this repository's include/ at the crate root (hip/csrc includes ../../include)");
     let mut objs = Vec::new();
     for f in std::fs::read_dir(src).unwrap() {
         let p = f.unwrap().path();

@@ -93,6 +93,8 @@ class QkNormRopeArgs(ctypes.Structure):
 _SIGNATURES = {
     "bh_last_error": (ctypes.c_char_p, []),
     "bh_version": (ctypes.c_char_p, []),
+    "bh_scratch_retired_bytes": (ctypes.c_size_t, []),
+    "bh_scratch_release": (_c_int, []),
     "bh_pq2_row_bytes": (_c_size, [_c_size]),
     "bh_rms_norm": (_c_int, [_vp, _vp, _c_size, _c_float, _vp, _vp]),
     "bh_rms_norm_rows": (_c_int, [_vp, _c_size, _vp, _c_size, _c_size, _c_float, _vp, _vp]),

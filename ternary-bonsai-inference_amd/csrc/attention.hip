@@ -789,8 +789,10 @@ __global__ __launch_bounds__(kBlock) void attn_planar_kernel(PlanarArgs a, Plana
     for (int pass = 0; pass < kPasses; ++pass) {
       const float e = hm == -INFINITY ? 0.0f : expf(sc[pass] - hm);
       ps += e;
-      // the P.V weight: p_j, or (p_j |v_j|) for a quantized V (src/forward.rs:344)
-      if (sub < REP) s_e[w][4 * pass + grp4][sub] = VQ ? e * cur.vn[pass] : e;
+      // the P.V weight: p_j, or (p_j |v_j|) for a quantized V (src/forward.rs:344);
+      // p_j == 0 adds nothing even for an infinite |v_j| (the reference skips
+      // such positions, src/forward.rs:335)
+      if (sub < REP) s_e[w][4 * pass + grp4][sub] = VQ ? (e != 0.0f ? e * cur.vn[pass] : 0.0f) : e;
     }
     run_l = run_l * corr_mine + rows4_sum(ps);
     float corr[REP];  // head r's correction, from lane r

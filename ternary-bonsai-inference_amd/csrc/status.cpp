@@ -5,6 +5,7 @@
 // thread-local string readable through bh_last_error().
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdint>
 #include <mutex>
@@ -28,7 +29,12 @@ std::vector<Scratch> g_scratch;  // indexed by device ordinal * kScratchSlots + 
 // captured while one was current still holds its address, and replaying that
 // graph must find the memory alive.  Growth is at least twofold, so the
 // retired buffers of a slot add up to less than its current one.
-std::vector<void *> g_retired;
+struct Retired {
+  void *ptr;
+  size_t bytes;
+  int dev;
+};
+std::vector<Retired> g_retired;
 }  // namespace
 
 int fail(int code, const std::string &msg) {
@@ -76,7 +82,7 @@ void *device_scratch(size_t bytes, int slot, hipStream_t stream) {
   void *p = nullptr;
   if (check_hip(hipMalloc(&p, want), "scratch hipMalloc") != BH_OK) return nullptr;
   // queued work and captured graphs may still use the old buffer: keep it
-  if (s.ptr != nullptr) g_retired.push_back(s.ptr);
+  if (s.ptr != nullptr) g_retired.push_back(Retired{s.ptr, s.bytes, dev});
   s.ptr = p;
   s.bytes = want;
   return p;
@@ -106,6 +112,39 @@ size_t device_cu_count() {
 }  // namespace bh
 
 extern "C" const char *bh_last_error(void) { return bh::g_last_error.c_str(); }
+
+extern "C" size_t bh_scratch_retired_bytes(void) {
+  std::lock_guard<std::mutex> lock(bh::g_scratch_mu);
+  size_t n = 0;
+  for (const auto &r : bh::g_retired) n += r.bytes;
+  return n;
+}
+
+extern "C" int bh_scratch_release(void) {
+  std::lock_guard<std::mutex> lock(bh::g_scratch_mu);
+  if (bh::g_retired.empty()) return bh::ok();
+  int cur = 0;
+  if (int e = bh::check_hip(hipGetDevice(&cur), "hipGetDevice")) return e;
+  int status = BH_OK;
+  std::vector<bh::Retired> keep;
+  std::vector<int> synced;
+  for (const auto &r : bh::g_retired) {
+    bool ok = true;
+    if (std::find(synced.begin(), synced.end(), r.dev) == synced.end()) {
+      ok = bh::check_hip(hipSetDevice(r.dev), "hipSetDevice") == BH_OK &&
+           bh::check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize") == BH_OK;
+      if (ok) synced.push_back(r.dev);
+    } else {
+      ok = bh::check_hip(hipSetDevice(r.dev), "hipSetDevice") == BH_OK;
+    }
+    if (ok && bh::check_hip(hipFree(r.ptr), "scratch hipFree") == BH_OK) continue;
+    status = BH_ERR_HIP;
+    keep.push_back(r);
+  }
+  bh::g_retired.swap(keep);
+  (void)hipSetDevice(cur);
+  return status == BH_OK ? bh::ok() : status;
+}
 
 extern "C" const char *bh_version(void) {
   return "bonsai-hip 0.1.0 (gfx950)";

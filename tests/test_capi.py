@@ -13,7 +13,7 @@ import pytest
 def test_library_exports_every_header_symbol(bh):
     lib = bh.lib()
     names = bh.header_symbols()
-    assert len(names) == 39
+    assert len(names) == 41
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     # and the Python binding declares a signature for each of them

@@ -136,6 +136,29 @@ def test_graph_softmax_survives_scratch_growth(bh, oracle, synth, dev):
             torch.cuda.synchronize()
 
 
+def test_scratch_release_frees_retired_buffers(bh, oracle, synth, dev):
+    """Growing a scratch slot retires the old buffer; bh_scratch_release
+    (for callers that know no captured graph still uses it) frees every
+    retired buffer after synchronizing, and later calls work as before."""
+    import torch
+    from conftest import rel_err
+    lib = bh.lib()
+    before = lib.bh_scratch_retired_bytes()
+    # a wide softmax needing more partials than any earlier call: the slot grows
+    row = 1 << 22
+    big = torch.randn((400, row // 4), device=dev, generator=torch.Generator(dev).manual_seed(4))
+    bh.softmax_rows(big.reshape(100, row), row, 1.0)
+    torch.cuda.synchronize()
+    grown = lib.bh_scratch_retired_bytes()
+    assert grown >= before
+    assert lib.bh_scratch_release() == bh.BH_OK, bh.last_error()
+    assert lib.bh_scratch_retired_bytes() == 0
+    del big
+    xs = synth.Rng(41).normal(3 * 248320, 0.0, 3.0).reshape(3, 248320)
+    got = bh.softmax_rows(_t(xs, dev), 248320, 1.0).cpu().numpy()
+    assert rel_err(got, oracle.softmax_rows(xs, 248320, 1.0)) < 2e-5
+
+
 @pytest.mark.parametrize("n_q,pos0,f16", [(1, 4095, False), (3, 63, False), (1, 4095, True),
                                           (2, 700, True)])
 def test_graph_attention_decode(bh, synth, dev, n_q, pos0, f16):

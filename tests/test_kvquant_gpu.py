@@ -153,3 +153,25 @@ def test_planar_argument_errors(bh):
                                   None) == bh.BH_ERR_ARG
     assert lib.bh_attention_planar(None, 1, 0, None, None, None, None, None, 4, 24, 5, 256, None,
                                    None) == bh.BH_ERR_SHAPE
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_attention_planar_skips_zero_probability_inf_norm(bh, oracle, synth, dev, bits):
+    """One query over two positions: position 0's key points along q (score
+    ~ +2000), position 1's against it (~ -2000), so p_1 underflows to 0, and
+    position 1's V row overflows to an infinite norm.  The reference skips
+    p == 0 (src/forward.rs:335), so the output is finite: 1 x |v_0|-weighted
+    centroids of v_0; the decode kernel must not form 0 x inf."""
+    n_head, n_kv = 4, 1
+    r = synth.Rng(77 + bits)
+    q = (r.normal(n_head * HD).reshape(1, n_head, HD) * np.float32(2.0)).astype(np.float32)
+    qd = q[0, 0] / np.linalg.norm(q[0, 0])
+    k = np.stack([qd * 1e3, -qd * 1e3]).astype(np.float32)
+    v = np.stack([r.normal(HD), r.normal(HD) * np.float32(1e30)]).astype(np.float32)
+    kq, kn, vq, vn, vf = _store(bh, dev, k, v, n_kv, bits, 2, True)
+    assert np.isinf(vn.cpu().numpy()[1, 0])
+    got = bh.attention_planar(_t(q, dev), 1, kq, kn, n_kv, bits, vq, vn, vf).cpu().numpy()
+    rkq, rkn, rvq, rvn, rvf = oracle.kv_store_planar(k, v, n_kv, HD, bits, 2, 0, True)
+    ref = oracle.attention_planar(q, 1, rkq, rkn, rvq, rvn, rvf, n_kv, bits, True)
+    assert np.all(np.isfinite(ref[0, 0])) and np.all(np.isfinite(got[0, 0]))
+    assert rel_err(got[0, 0], ref[0, 0]) <= TOL

@@ -56,3 +56,57 @@ def test_noalloc_rejects_inputs_beyond_its_scratch(bh, dev):
     assert st == bh.BH_ERR_SHAPE
     assert "above the fixed 1048576" in bh.last_error()
     torch.cuda.synchronize()
+
+
+_CAPTURE_SCRIPT = r'''
+import ctypes, sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+from conftest import load_bonsai
+bh = load_bonsai()
+lib = bh.lib()
+dev = torch.device("cuda:0")
+rows, row_len, inv_t = 16, 248320, 1 / 0.7
+x = torch.randn((rows, row_len), device=dev) * 3
+want = torch.empty_like(x)
+got = torch.full_like(x, float("nan"))
+s = torch.cuda.Stream(device=dev)
+def call(fn, out, stream):
+    return fn(ctypes.c_void_p(x.data_ptr()), x.numel(), row_len, ctypes.c_float(inv_t),
+              ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+lib.bh_softmax_rows_noalloc.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                        ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    # the process's first no-allocation call: its scratch lookup happens here
+    assert call(lib.bh_softmax_rows_noalloc, got, s) == 0, bh.last_error()
+torch.cuda.synchronize()
+assert call(lib.bh_softmax_rows, want, torch.cuda.current_stream()) == 0, bh.last_error()
+torch.cuda.synchronize()
+w = want.cpu().numpy().view(np.uint32)
+for rep in range(3):
+    got.fill_(float("nan"))
+    x.mul_(1.0)  # eager work between replays
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), w), f"replay {rep}"
+print("capture ok")
+'''
+
+
+def test_noalloc_first_call_inside_graph_capture(dev):
+    """The first wide-row no-allocation call of a process made inside a HIP
+    graph capture (so the per-device scratch address is looked up during the
+    capture); three replays, with eager work between them, each match
+    bh_softmax_rows bit for bit.  Runs in a fresh process so no earlier call
+    has done the lookup."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    here = Path(__file__).resolve().parent
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT, str(here)], capture_output=True,
+                         text=True, timeout=300)
+    print(res.stdout[-2000:], res.stderr[-2000:])
+    assert res.returncode == 0 and "capture ok" in res.stdout
