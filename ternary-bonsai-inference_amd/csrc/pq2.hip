@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kFusedThreads) void pq2_gather_rms_kernel(GatherArg
                               pq2_weight((code >> 4) & 3u, sc, finite), pq2_weight((code >> 6) & 3u, sc, finite));
               t = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
             }
-            reinterpret_cast<float4 *>(a.out)[(row0 + r) * n4 + f] = v;
+            store_stream(reinterpret_cast<float4 *>(a.out) + (row0 + r) * n4 + f, v);
           }
           dst[q * kRingStride + r] = t;
         }
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(kFusedThreads) void pq2_gather_rms_kernel(GatherArg
       const float rs = row_scale[r];
       o = make_float4((v.x * rs) * wv.x, (v.y * rs) * wv.y, (v.z * rs) * wv.z, (v.w * rs) * wv.w);
     }
-    on[i] = o;
+    store_stream(on + i, o);
   }
 }
 
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
   } else if (f == 0 && a.bad_id != nullptr) {
     *a.bad_id = id;
   }
-  reinterpret_cast<float4 *>(a.out)[idx] = o;
+  store_stream(reinterpret_cast<float4 *>(a.out) + idx, o);
 }
 
 // Any ne0 / alignment: byte reads straight from the table.
