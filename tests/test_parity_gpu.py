@@ -52,6 +52,7 @@ def test_rms_norm_known_answer(bh, dev):
 
 @pytest.mark.parametrize("rows,row_len", [
     (512, 5120),        # config 1 (block-per-row, 256 lanes x 5 float4)
+    (2050, 5120),       # wave-per-row range, ragged last block of four rows
     (2048 * 24, 256),   # per-head q norm (one wave per row)
     (4096, 128),        # ssm_norm heads (half-wave rows)
     (33, 4),            # tiny rows, 64 rows per wave
@@ -95,7 +96,7 @@ def test_rms_norm_single_vector(bh, oracle, synth, dev):
     assert rel_err(_h(out), oracle.rms_norm(x, w, 1e-6)) <= TOL
 
 
-@pytest.mark.parametrize("rows,row_len", [(2048, 5120), (3, 36)])
+@pytest.mark.parametrize("rows,row_len", [(2048, 5120), (3071, 5120), (3, 36)])
 def test_add_rms_norm_rows(bh, oracle, synth, dev, rows, row_len):
     _say("add_rms_norm_rows", rows, row_len)
     r = synth.Rng(11)
