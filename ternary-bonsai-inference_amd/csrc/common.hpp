@@ -53,7 +53,8 @@ inline int pow2ceil(size_t v) {
 constexpr int kScratchSoftmax = 0;  // split-row softmax partials
 constexpr int kScratchMatmul = 1;   // PQ2_0 product: f16 x fragments, token scales
 constexpr int kScratchAttention = 2;  // attention: chunk partials or probabilities
-constexpr int kScratchSlots = 3;
+constexpr int kScratchGather = 3;     // gather + RMSNorm: the row scales
+constexpr int kScratchSlots = 4;
 void *device_scratch(size_t bytes, int slot, hipStream_t stream);
 // Current size of this device's buffer for `slot` (0 before the first use).
 size_t scratch_bytes(int slot);

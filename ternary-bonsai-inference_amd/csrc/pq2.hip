@@ -27,7 +27,11 @@
 // order, one row per lane -- the same additions in the same order as the
 // CPU, so the norm output is bit-identical too.  The chain (5120 dependent
 // adds, ~21 us) runs under the embedding stores; the norm rows are then
-// decoded a second time from LDS and stored.
+// decoded a second time from LDS and stored.  Batches of at least 16 rows per
+// CU take two launches instead, with flat writers: the row scales come from
+// runs of identical squares evaluated in closed form (seqsum.hpp), computed
+// by the first blocks of the launch that writes the embedding rows, and a
+// second launch writes the norm rows.
 //
 // Bit-exactness: the f16 scale is widened with integer arithmetic (exact for
 // all patterns, see half_bits_to_f32_bits) and the weight is one multiply of
@@ -37,6 +41,7 @@
 #include <string>
 
 #include "common.hpp"
+#include "seqsum.hpp"
 
 namespace bh {
 namespace {
@@ -215,6 +220,195 @@ __device__ __forceinline__ float4 decode4_global(const uint8_t *rowb, int f) {
                      pq2_weight((c >> 6) & 3u, scale, finite));
 }
 
+// ---------------------------------------------------------------------------
+// Gather + RMSNorm in two launches with flat writers.
+// ---------------------------------------------------------------------------
+// Launch 1 (pq2_scale_embed_kernel): its first blocks compute every row's
+// 1 / sqrt(ss / n + eps)
+// with ss the reference's sequential f32 sum of squares, bit for bit, without
+// decoding the row: on a block of ternary codes (0, 1, 2) every square is d*d
+// or +0, and +0 leaves the sum unchanged, so the block adds d*d as many times
+// as it has codes other than 1 -- a run that repeat_add_f32 evaluates in
+// closed form.  A block holding code 3 (square 4*d*d) or a non-finite scale
+// is added weight by weight instead.  One lane walks one row, so the walk is
+// a chain of ~55 dependent steps (one per block plus one per binade the sum
+// crosses, ~20 us); the launch's other blocks write the embedding rows from a
+// flat grid meanwhile.  Launch 2 (pq2_norm_write_kernel) writes the norm rows
+// from a flat grid.  Both writers keep the streaming-store shape: no block
+// stores a region longer than 4 KB.
+constexpr int kScaleRows = 16;  // rows per scale block: one per lane of its walk
+constexpr int kEmbedV = 4;      // float4 per lane of the embedding writer blocks
+
+// Sum-of-squares summary of one 128-weight block of a staged row: the run
+// value d*d (f32 bits) and the run length, or the fallback flag.
+struct BlockRun {
+  uint32_t xbits;
+  uint32_t n;  // bit 31: add this block weight by weight
+};
+
+// Scale block `sblk` of launch 1: rows sblk*kScaleRows .. (+kScaleRows).
+__device__ __forceinline__ void row_scale_block(const GatherArgs &a, float *row_scale,
+                                                unsigned sblk, BlockRun *runs) {
+  const int nblk = a.row_bytes / kPq2Block;
+  const int tid = threadIdx.x;
+  const size_t row0 = static_cast<size_t>(sblk) * kScaleRows;
+  const int nr = (a.n_ids - static_cast<int>(row0)) < kScaleRows ? a.n_ids - static_cast<int>(row0)
+                                                                 : kScaleRows;
+  // one lane per (row, block), straight from the table: count the codes
+  // other than 1 among the block's valid weights, flag code 3 and
+  // non-finite scales.  The block's 34 bytes start on an even byte: eight
+  // aligned words and one halfword cover them without reading past it.
+  // A lane takes up to kScalePairs pairs per round and issues all their
+  // loads (ids, then table words) before it uses any: under the writers'
+  // HBM traffic a load round trip is long, and the walk waits for this.
+  constexpr int kScalePairs = 4;
+  const int total = nr * nblk;
+  for (int base = 0; base < total; base += 256 * kScalePairs) {
+    uint32_t idp[kScalePairs];
+#pragma unroll
+    for (int p = 0; p < kScalePairs; ++p) {
+      const int i = base + p * 256 + tid;
+      idp[p] = i < total ? a.ids[row0 + i / nblk] : a.n_rows;
+    }
+    uint32_t dw[kScalePairs][8];
+    uint32_t h16[kScalePairs];
+#pragma unroll
+    for (int p = 0; p < kScalePairs; ++p) {
+      const int i = base + p * 256 + tid;
+      const int b = i - (i / nblk) * nblk;
+      const bool even = (b & 1) == 0;  // block start 4-aligned (rows are 16-aligned)
+      h16[p] = 0u;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) dw[p][k] = 0u;
+      if (idp[p] < a.n_rows) {
+        const uint8_t *blk = a.table + static_cast<size_t>(idp[p]) * a.row_bytes + b * kPq2Block;
+        const uint32_t *w32 = reinterpret_cast<const uint32_t *>(blk + (even ? 0 : 2));
+        h16[p] = *reinterpret_cast<const uint16_t *>(blk + (even ? 32 : 0));
+#pragma unroll
+        for (int k = 0; k < 8; ++k) dw[p][k] = w32[k];
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kScalePairs; ++p) {
+      const int i = base + p * 256 + tid;
+      if (idp[p] >= a.n_rows) continue;  // past the pairs, or a bad id (no scale)
+      const int b = i - (i / nblk) * nblk;
+      const bool even = (b & 1) == 0;
+      const uint32_t h = even ? (dw[p][0] & 0xffffu) : h16[p];
+      const int valid = (a.ne0 - b * 128) < 128 ? a.ne0 - b * 128 : 128;
+      uint32_t ones = 0, threes = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {  // 16 codes per 32-bit word
+        const uint32_t w =
+            even ? ((dw[p][k] >> 16) | ((k < 7 ? dw[p][k < 7 ? k + 1 : 0] : h16[p]) << 16)) : dw[p][k];
+        const int lo = valid - 16 * k;
+        const uint32_t mask = lo >= 16 ? 0x55555555u : (lo <= 0 ? 0u : 0x55555555u & ((1u << (2 * lo)) - 1u));
+        const uint32_t t = w ^ 0x55555555u;  // code 1 -> 00
+        ones += __popc(~(t | (t >> 1)) & mask);
+        threes |= w & (w >> 1) & mask;
+      }
+      const bool finite = (h & 0x7c00u) != 0x7c00u;
+      const float d = __uint_as_float(half_bits_to_f32_bits(h));
+      BlockRun br;
+      br.xbits = __float_as_uint(d * d);
+      br.n = static_cast<uint32_t>(valid) - ones;
+      if (threes != 0u || !finite) br.n |= 0x80000000u;
+      runs[i] = br;
+    }
+  }
+  __syncthreads();
+  if (tid >= nr) return;
+  const uint32_t id = a.ids[row0 + tid];
+  if (id >= a.n_rows) return;
+  // the walk is the launch's latency-critical path: its wave goes first
+  // when it shares a SIMD with the writer waves
+  __builtin_amdgcn_s_setprio(3);
+  const BlockRun *rr = runs + tid * nblk;
+  // Each lane walks its own row's blocks; one repeat_add_step_f32 per loop
+  // trip, and a lane whose block is done moves to its next one in the same
+  // trip, so the wave's trips are the most any of its rows needs rather
+  // than the sum of per-block maxima.
+  float ss = 0.0f;
+  int b = 0;
+  BlockRun cur = rr[0];
+  BlockRun next = rr[nblk > 1 ? 1 : 0];  // an index select: both from LDS
+  while (b < nblk) {
+    uint32_t left = cur.n;
+    if (left & 0x80000000u) {
+      // weight by weight, as src/kernels.rs:65-68 (code 3 or a non-finite scale)
+      const uint8_t *blk = a.table + static_cast<size_t>(id) * a.row_bytes + b * kPq2Block;
+      const uint32_t h = *reinterpret_cast<const uint16_t *>(blk);
+      const float sc = __uint_as_float(half_bits_to_f32_bits(h));
+      const bool finite = (h & 0x7c00u) != 0x7c00u;
+      const int valid = (a.ne0 - b * 128) < 128 ? a.ne0 - b * 128 : 128;
+      for (int j = 0; j < valid; ++j) {
+        const uint32_t code = (static_cast<uint32_t>(blk[2 + (j >> 2)]) >> ((j & 3) * 2)) & 3u;
+        const float v = pq2_weight(code, sc, finite);
+        ss += v * v;  // no contraction: built with -ffp-contract=off
+      }
+      left = 0u;
+    } else if (left != 0u && cur.xbits != 0u) {
+      left = repeat_add_step_f32(ss, __uint_as_float(cur.xbits), left);
+    } else {
+      left = 0u;  // d = 0 or only code 1: the squares are all +0
+    }
+    cur.n = left;
+    if (left == 0u) {
+      ++b;
+      cur = next;
+      if (b + 1 < nblk) next = rr[b + 1];
+    }
+  }
+  // src/kernels.rs:69-70: mean = ss / n; scale = 1 / sqrt(mean + eps)
+  row_scale[row0 + tid] = 1.0f / sqrtf(ss / static_cast<float>(a.ne0) + a.eps);
+}
+
+// Launch 1: blocks [0, n_scale) compute the row scales (dispatched first, so
+// their walks run under the stores), the rest write the embedding rows, one
+// float4 per lane over the flat [n_ids][ne0/4] range.
+__global__ __launch_bounds__(256) void pq2_scale_embed_kernel(GatherArgs a, float *row_scale,
+                                                              unsigned n_scale) {
+  extern __shared__ BlockRun runs[];  // [kScaleRows][nblk]
+  if (blockIdx.x < n_scale) {
+    row_scale_block(a, row_scale, blockIdx.x, runs);
+    return;
+  }
+  // kEmbedV float4 per lane, grid-stride (each block's stores stay 4 KB
+  // runs): every lane's id and table loads are in flight before its first
+  // store -- the first touch of each gathered row is a long round trip
+  const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
+  const uint32_t total = static_cast<uint32_t>(a.n_ids) * n4;
+  const uint32_t stride = (gridDim.x - n_scale) * 256u;
+  const uint32_t idx0 = (blockIdx.x - n_scale) * 256u + threadIdx.x;
+  uint32_t id[kEmbedV];
+#pragma unroll
+  for (int v = 0; v < kEmbedV; ++v) {
+    const uint32_t idx = idx0 + v * stride;
+    id[v] = idx < total ? a.ids[idx / n4] : 0u;
+  }
+  float4 val[kEmbedV];
+#pragma unroll
+  for (int v = 0; v < kEmbedV; ++v) {
+    const uint32_t idx = idx0 + v * stride;
+    const uint32_t f = idx % n4;
+    val[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (idx < total && id[v] < a.n_rows)
+      val[v] = decode4_global(a.table + static_cast<size_t>(id[v]) * a.row_bytes, f);
+  }
+#pragma unroll
+  for (int v = 0; v < kEmbedV; ++v) {
+    const uint32_t idx = idx0 + v * stride;
+    if (idx < total) {
+      if (id[v] >= a.n_rows && idx % n4 == 0 && a.bad_id != nullptr) *a.bad_id = id[v];
+      store_stream(reinterpret_cast<float4 *>(a.out) + idx, val[v]);
+    }
+  }
+}
+
+size_t scale_smem_bytes(size_t row_bytes) {
+  return kScaleRows * (row_bytes / kPq2Block) * sizeof(BlockRun);
+}
+
 // Plain gather: one float4 of output per lane over the flat [n_ids][ne0/4]
 // range (fits 32 bits: checked by the host).
 __global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
@@ -231,6 +425,26 @@ __global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
     *a.bad_id = id;
   }
   store_stream(reinterpret_cast<float4 *>(a.out) + idx, o);
+}
+
+// Launch 2: the norm rows (v * scale) * w (src/kernels.rs:71-73), one float4
+// per lane over the flat [n_ids][ne0/4] range, with the row scales of
+// launch 1 (bad ids: zeros, as the embedding rows).
+__global__ __launch_bounds__(256) void pq2_norm_write_kernel(GatherArgs a, const float *row_scale) {
+  const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  if (idx >= static_cast<uint32_t>(a.n_ids) * n4) return;
+  const uint32_t t = idx / n4;
+  const uint32_t f = idx - t * n4;
+  const uint32_t id = a.ids[t];
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (id < a.n_rows) {
+    const float rs = row_scale[t];
+    const float4 wv = reinterpret_cast<const float4 *>(a.w)[f];
+    const float4 v = decode4_global(a.table + static_cast<size_t>(id) * a.row_bytes, f);
+    o = make_float4((v.x * rs) * wv.x, (v.y * rs) * wv.y, (v.z * rs) * wv.z, (v.w * rs) * wv.w);
+  }
+  store_stream(reinterpret_cast<float4 *>(a.out_norm) + idx, o);
 }
 
 // Any ne0 / alignment: byte reads straight from the table.
@@ -288,7 +502,7 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
   const uint32_t nr = static_cast<uint32_t>(n_rows);
   // writers: one float4 per lane (16-byte stores, halfword table loads); the
   // fused kernel stages rows with 16-byte loads
-  const bool rows_ok = (ne0 % 4 == 0) && n_ids * (ne0 / 4) < 0xffffff00u && aligned16(table) &&
+  const bool rows_ok = (ne0 % 4 == 0) && n_ids * (ne0 / 4) < 0xfffff000u && aligned16(table) &&
                        aligned16(out) && (!norm || (aligned16(out_norm) && aligned16(w)));
   const unsigned wgrid = static_cast<unsigned>((n_ids * (ne0 / 4) + 255) / 256);
   GatherArgs ga{};
@@ -307,6 +521,28 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
     BH_LAUNCH(pq2_rows_write_kernel, wgrid, 256, 0, st, ga);
     return ok();
   }
+  const size_t cus = device_cu_count();
+  if (rows_ok && norm && row_bytes % 16 == 0 && n_ids >= 16 * cus &&
+      scale_smem_bytes(row_bytes) <= kMaxSeqSmem) {
+    // Long batches: row scales + embedding rows, then the norm rows (two
+    // flat writers).  The scale walk (~20 us of dependent steps) hides under
+    // the embedding stores only when there are enough of them: measured at
+    // T=8192 65.9-67.1 us against 70.6-72.5 for the one-launch kernel below,
+    // at T=2048 31.5 against 29.8 (so shorter batches stay on that kernel).
+    float *scales = static_cast<float *>(device_scratch(n_ids * sizeof(float), kScratchGather, st));
+    if (scales == nullptr) return BH_ERR_HIP;
+    const size_t smem = scale_smem_bytes(row_bytes);
+    if (int e = check_hip(hipFuncSetAttribute(reinterpret_cast<const void *>(pq2_scale_embed_kernel),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              static_cast<int>(smem)),
+                          "hipFuncSetAttribute"))
+      return e;
+    const unsigned n_scale = static_cast<unsigned>((n_ids + kScaleRows - 1) / kScaleRows);
+    const unsigned egrid = static_cast<unsigned>((n_ids * (ne0 / 4) + 256 * kEmbedV - 1) / (256 * kEmbedV));
+    BH_LAUNCH(pq2_scale_embed_kernel, n_scale + egrid, 256, smem, st, ga, scales, n_scale);
+    BH_LAUNCH(pq2_norm_write_kernel, wgrid, 256, 0, st, ga, scales);
+    return ok();
+  }
   if (rows_ok && norm && row_bytes % 16 == 0 && fused_smem_bytes(row_bytes, 16, 128) <= kMaxSeqSmem) {
     // 16 rows per block while that still gives every CU a block; fewer rows
     // per block (more blocks) for short batches: the chain's latency is the
@@ -316,7 +552,6 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
     // 35.1 / 85, 4 x 256 38.6 / 69.  Longer chunks (fewer barriers on the
     // chain's path): 8 rows, chunks of 64 / 128 float4 33.3 / 32.7 at
     // T=2048; 16 rows, 64: 70.2 at T=8192 (128: 80.5).
-    const size_t cus = device_cu_count();
     const int rows = n_ids >= 16 * cus ? 16 : (n_ids >= 8 * cus ? 8 : 4);
     auto launch = [&](auto kern, int r, int threads, int chunk_q) -> int {
       const size_t smem = fused_smem_bytes(row_bytes, r, chunk_q);

@@ -518,7 +518,18 @@ def test_pq2_gather_every_f16_scale(bh, oracle, synth, dev):
     assert bits_equal(got, ref)
 
 
-def test_pq2_gather_rms_every_f16_scale(bh, oracle, synth, dev):
+# Batches of at least 16 rows per CU (4096 on MI355X) take the two-launch
+# path (closed-form row scales + flat writers), shorter ones the one-launch
+# kernel; LONG tiles a test's ids up to that size so both paths see its rows.
+LONG = 4096
+
+
+def _tiled(ids, tile):
+    return np.tile(ids, -(-LONG // ids.size)) if tile else ids
+
+
+@pytest.mark.parametrize("tile", [False, True])
+def test_pq2_gather_rms_every_f16_scale(bh, oracle, synth, dev, tile):
     """The fused norm over rows holding every f16 scale pattern and every
     code (code 3 included): the closed-form sum of squares must equal the
     reference's sequential f32 sum, so every row with finite scales is
@@ -533,20 +544,21 @@ def test_pq2_gather_rms_every_f16_scale(bh, oracle, synth, dev):
     codes = (rng.u64(rows * ne0) % np.uint64(4)).astype(np.uint8).reshape(rows, ne0)
     codes[9] = 3
     table = synth.pack_pq2_rows(codes, scales)
-    ids = np.arange(rows, dtype=np.uint32)[::-1].copy()
+    ids = _tiled(np.arange(rows, dtype=np.uint32)[::-1].copy(), tile)
     w = synth.Rng(18).normal(ne0, 1.0, 0.1)
     e, n = bh.pq2_embed_gather(_t(table, dev), ne0, rows, _t(ids, dev), w=_t(w, dev), eps=1e-6)
     ref_e, ref_n = oracle.embed_gather(table, ne0, rows, ids, w, 1e-6)
     ge, gn = _h(e), _h(n)
     assert bits_equal(ge, ref_e)
     finite = np.all((scales[ids] & 0x7c00) != 0x7c00, axis=1)
-    assert finite.sum() >= rows - 8
+    assert finite.sum() >= ids.size * (rows - 8) // rows
     assert bits_equal(gn[finite], ref_n[finite])
     assert np.array_equal(np.isnan(gn), np.isnan(ref_n))
 
 
+@pytest.mark.parametrize("tile", [False, True])
 @pytest.mark.parametrize("case", ["few_scales", "big_then_tiny", "ties", "unit_scale"])
-def test_pq2_gather_rms_closed_form_edge_rows(bh, oracle, synth, dev, case):
+def test_pq2_gather_rms_closed_form_edge_rows(bh, oracle, synth, dev, case, tile):
     """Rows whose sequential sum of squares is easy to get wrong: one scale
     repeated over many blocks (long runs across powers of two), a large scale
     followed by tiny ones (the sum stops moving), power-of-two scales (sums
@@ -567,7 +579,7 @@ def test_pq2_gather_rms_closed_form_edge_rows(bh, oracle, synth, dev, case):
     else:
         scales = np.full((rows, 40), 0x3c00, np.uint16)
     table = synth.pack_pq2_rows(codes, scales)
-    ids = rng.permutation(rows).astype(np.uint32)
+    ids = _tiled(rng.permutation(rows).astype(np.uint32), tile)
     w = synth.Rng(19).normal(ne0, 1.0, 0.1)
     e, n = bh.pq2_embed_gather(_t(table, dev), ne0, rows, _t(ids, dev), w=_t(w, dev), eps=1e-6)
     ref_e, ref_n = oracle.embed_gather(table, ne0, rows, ids, w, 1e-6)
@@ -586,20 +598,41 @@ def test_pq2_gather_shapes(bh, oracle, synth, dev, ne0):
     assert bits_equal(_h(nrm), ref_n)   # sequential sum of squares on every path
 
 
-def test_pq2_gather_rms_bad_ids_and_ragged_tail(bh, oracle, synth, dev):
+@pytest.mark.parametrize("ne0", [1000, 1024, 5120])
+def test_pq2_gather_rms_long_batch_shapes(bh, oracle, synth, dev, ne0):
+    """Long batches (two-launch path) with a partial last 128-block
+    (ne0=1000: 104 valid weights in block 7), an 8-block row and the model
+    row; random codes 0..3, so code-3 blocks take the weight-by-weight sum
+    next to closed-form blocks in the same row."""
+    rows = 300
+    rng = np.random.default_rng(ne0)
+    nblk = -(-ne0 // 128)
+    codes = rng.choice(np.array([0, 1, 2, 3], np.uint8), size=(rows, ne0), p=[0.3, 0.4, 0.28, 0.02])
+    scales = rng.integers(0x0400, 0x5000, size=(rows, nblk)).astype(np.uint16)
+    table = synth.pack_pq2_rows(codes, scales)
+    ids = rng.integers(0, rows, size=LONG + 5).astype(np.uint32)
+    w = synth.Rng(20).normal(ne0, 1.0, 0.1)
+    e, n = bh.pq2_embed_gather(_t(table, dev), ne0, rows, _t(ids, dev), w=_t(w, dev), eps=1e-6)
+    ref_e, ref_n = oracle.embed_gather(table, ne0, rows, ids, w, 1e-6)
+    assert bits_equal(_h(e), ref_e)
+    assert bits_equal(_h(n), ref_n)
+
+
+@pytest.mark.parametrize("tile", [False, True])
+def test_pq2_gather_rms_bad_ids_and_ragged_tail(bh, oracle, synth, dev, tile):
     """Bad ids inside a 16-row block give zero rows in both outputs; the other
     rows of the block stay bit-exact; T not a multiple of 16."""
     import torch
     table = synth.pq2_table(synth.Rng(12), 40, 5120)
     ids = (synth.Rng(13).u64(37) % np.uint64(40)).astype(np.uint32)
     ids[[3, 20, 36]] = [40, 1000, 4294967295]
+    ids = _tiled(ids, tile)
     w = synth.Rng(14).normal(5120, 1.0, 0.1)
     bad = torch.full((1,), -1, dtype=torch.int32, device=dev)
     emb, nrm = bh.pq2_embed_gather(_t(table, dev), 5120, 40, _t(ids, dev), w=_t(w, dev),
                                    bad_id=bad)
     e, n = _h(emb), _h(nrm)
-    good = np.ones(37, bool)
-    good[[3, 20, 36]] = False
+    good = ids < 40
     assert np.all(e[~good] == 0) and np.all(n[~good] == 0)
     ref_e, ref_n = oracle.embed_gather(table, 5120, 40, ids[good], w, 1e-6)
     assert bits_equal(e[good], ref_e) and bits_equal(n[good], ref_n)
