@@ -127,6 +127,7 @@ def test_graph_softmax_survives_scratch_growth(bh, oracle, synth, dev):
             # 100 rows of 2^22: 1024 chunks per row -> 102400 partials x 12 B
             row = 1 << 22
             big = torch.randn((100, row), device=dev, generator=torch.Generator(dev).manual_seed(3))
+            torch.cuda.synchronize()  # big comes from the default stream; the call runs on s
             bout = bh.softmax_rows(big, row, 1.0, stream=s)
             torch.cuda.synchronize()
             for r in (0, 99):
