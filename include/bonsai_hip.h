@@ -29,8 +29,9 @@
  *
  * Threading: every device entry point is re-entrant per stream, except
  * bh_softmax_rows on rows too wide for one workgroup, bh_attention,
- * bh_attention_planar, and the
- * PQ2_0 products (bh_pq2_matvec_range, bh_pq2_matmul_n) with more than 4
+ * bh_attention_planar, bh_pq2_embed_gather_rms on batches of at least 16
+ * ids per compute unit (4096 on MI355X; it keeps the row scales there), and
+ * the PQ2_0 products (bh_pq2_matvec_range, bh_pq2_matmul_n) with more than 4
  * tokens or on shapes outside the integer path, which use per-device
  * scratch buffers: each must not run concurrently with itself on one device.
  *
@@ -353,6 +354,9 @@ int bh_pq2_embed_gather(const uint8_t *table, size_t ne0, size_t n_rows,
 /* Embedding gather fused with the first RMSNorm (src/forward.rs:691, 701-702):
  * out_embed[i] = decode_pq2_0_row(row ids[i])      (bit-exact, the residual)
  * out_norm[i]  = rms_norm(out_embed[i], w, eps)    (blk.0.attn_norm)
+ * Both outputs bit-exact: the row's sum of squares is the reference's
+ * sequential f32 sum.  Batches of at least 16 ids per compute unit keep
+ * their row scales in library scratch (n_ids * 4 bytes; see Threading).
  * BH_ERR_SHAPE when w_len != ne0. */
 int bh_pq2_embed_gather_rms(const uint8_t *table, size_t ne0, size_t n_rows,
                             const uint32_t *ids, size_t n_ids, const float *w,
