@@ -328,6 +328,26 @@ def test_softmax_nan_and_inf_entries(bh, oracle, synth, dev):
         assert rel_err(got, ref) <= TOL_SOFTMAX
 
 
+def test_softmax_wide_nan_inf_rows(bh, oracle, synth, dev):
+    """Vocabulary-wide rows (split path, 61 chunk states per row): an all-NaN
+    row, one NaN in the last chunk, one +inf in a middle chunk, a row whose
+    first three quarters are masked (-inf), and a row masked but for one
+    value."""
+    row_len = 248320
+    x = synth.Rng(77).normal(6 * row_len, 0.0, 3.0)
+    x[0:row_len] = np.nan
+    x[row_len + 240000] = np.nan
+    x[2 * row_len + 100000] = np.inf
+    x[3 * row_len: 3 * row_len + 3 * 65536] = -np.inf
+    x[4 * row_len: 5 * row_len] = -np.inf
+    x[4 * row_len + 70000] = 1.5
+    got = _h(bh.softmax_rows(_t(x, dev), row_len, 1.25))
+    ref = oracle.softmax_rows(x, row_len, 1.25)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert rel_err(got, ref) <= TOL_SOFTMAX
+    assert got[4 * row_len + 70000] == 1.0 and np.count_nonzero(got[4 * row_len: 5 * row_len]) == 1
+
+
 def test_softmax_split_repeated_mixed_shapes(bh, oracle, synth, dev):
     """The wide-row path keeps per-chunk partial states in the library's
     scratch, reused by every call: repeated calls with changing shapes (whose
