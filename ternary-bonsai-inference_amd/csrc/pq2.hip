@@ -237,7 +237,14 @@ __device__ __forceinline__ float4 decode4_global(const uint8_t *rowb, int f) {
 // from a flat grid.  Both writers keep the streaming-store shape: no block
 // stores a region longer than 4 KB.
 constexpr int kScaleRows = 16;  // rows per scale block: one per lane of its walk
-constexpr int kEmbedV = 4;      // float4 per lane of the embedding writer blocks
+
+// Logical block of physical block p when a grid of 8 * per blocks is
+// numbered XCD-contiguously: the hardware hands block p to XCD p % 8, and
+// that XCD takes logical blocks [(p % 8) * per, (p % 8 + 1) * per) in order.
+// (Only the speed depends on that dispatch order, never the results.)
+__device__ __forceinline__ unsigned xcd_block(unsigned p, unsigned per) {
+  return (p & 7u) * per + (p >> 3);
+}
 
 // Sum-of-squares summary of one 128-weight block of a staged row: the run
 // value d*d (f32 bits) and the run length, or the fallback flag.
@@ -367,42 +374,34 @@ __device__ __forceinline__ void row_scale_block(const GatherArgs &a, float *row_
 // their walks run under the stores), the rest write the embedding rows, one
 // float4 per lane over the flat [n_ids][ne0/4] range.
 __global__ __launch_bounds__(256) void pq2_scale_embed_kernel(GatherArgs a, float *row_scale,
-                                                              unsigned n_scale) {
+                                                              unsigned n_scale, unsigned s_per,
+                                                              unsigned e_per) {
   extern __shared__ BlockRun runs[];  // [kScaleRows][nblk]
   if (blockIdx.x < n_scale) {
-    row_scale_block(a, row_scale, blockIdx.x, runs);
+    // scale blocks in the same XCD-contiguous order as the writers, so a
+    // row's summary pass runs on the XCD that writes it
+    const unsigned sblk = xcd_block(blockIdx.x, s_per);
+    if (sblk * kScaleRows < static_cast<unsigned>(a.n_ids)) row_scale_block(a, row_scale, sblk, runs);
     return;
   }
-  // kEmbedV float4 per lane, grid-stride (each block's stores stay 4 KB
-  // runs): every lane's id and table loads are in flight before its first
-  // store -- the first touch of each gathered row is a long round trip
+  // one float4 per lane; the writer blocks are numbered XCD-contiguously:
+  // the blocks one XCD runs (every 8th) write one contiguous range of rows,
+  // so each gathered row is fetched into one XCD's L2 (and its address
+  // translations warmed there) instead of the five XCDs its 5 blocks would
+  // otherwise spread over
   const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
-  const uint32_t total = static_cast<uint32_t>(a.n_ids) * n4;
-  const uint32_t stride = (gridDim.x - n_scale) * 256u;
-  const uint32_t idx0 = (blockIdx.x - n_scale) * 256u + threadIdx.x;
-  uint32_t id[kEmbedV];
-#pragma unroll
-  for (int v = 0; v < kEmbedV; ++v) {
-    const uint32_t idx = idx0 + v * stride;
-    id[v] = idx < total ? a.ids[idx / n4] : 0u;
+  const uint32_t idx = xcd_block(blockIdx.x - n_scale, e_per) * 256u + threadIdx.x;
+  if (idx >= static_cast<uint32_t>(a.n_ids) * n4) return;
+  const uint32_t t = idx / n4;
+  const uint32_t f = idx - t * n4;
+  const uint32_t id = a.ids[t];
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (id < a.n_rows) {
+    v = decode4_global(a.table + static_cast<size_t>(id) * a.row_bytes, f);
+  } else if (f == 0 && a.bad_id != nullptr) {
+    *a.bad_id = id;
   }
-  float4 val[kEmbedV];
-#pragma unroll
-  for (int v = 0; v < kEmbedV; ++v) {
-    const uint32_t idx = idx0 + v * stride;
-    const uint32_t f = idx % n4;
-    val[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (idx < total && id[v] < a.n_rows)
-      val[v] = decode4_global(a.table + static_cast<size_t>(id[v]) * a.row_bytes, f);
-  }
-#pragma unroll
-  for (int v = 0; v < kEmbedV; ++v) {
-    const uint32_t idx = idx0 + v * stride;
-    if (idx < total) {
-      if (id[v] >= a.n_rows && idx % n4 == 0 && a.bad_id != nullptr) *a.bad_id = id[v];
-      store_stream(reinterpret_cast<float4 *>(a.out) + idx, val[v]);
-    }
-  }
+  store_stream(reinterpret_cast<float4 *>(a.out) + idx, v);
 }
 
 size_t scale_smem_bytes(size_t row_bytes) {
@@ -430,9 +429,10 @@ __global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
 // Launch 2: the norm rows (v * scale) * w (src/kernels.rs:71-73), one float4
 // per lane over the flat [n_ids][ne0/4] range, with the row scales of
 // launch 1 (bad ids: zeros, as the embedding rows).
-__global__ __launch_bounds__(256) void pq2_norm_write_kernel(GatherArgs a, const float *row_scale) {
+__global__ __launch_bounds__(256) void pq2_norm_write_kernel(GatherArgs a, const float *row_scale,
+                                                             unsigned per) {
   const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
-  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t idx = xcd_block(blockIdx.x, per) * 256u + threadIdx.x;  // as launch 1
   if (idx >= static_cast<uint32_t>(a.n_ids) * n4) return;
   const uint32_t t = idx / n4;
   const uint32_t f = idx - t * n4;
@@ -537,10 +537,12 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
                                               static_cast<int>(smem)),
                           "hipFuncSetAttribute"))
       return e;
-    const unsigned n_scale = static_cast<unsigned>((n_ids + kScaleRows - 1) / kScaleRows);
-    const unsigned egrid = static_cast<unsigned>((n_ids * (ne0 / 4) + 256 * kEmbedV - 1) / (256 * kEmbedV));
-    BH_LAUNCH(pq2_scale_embed_kernel, n_scale + egrid, 256, smem, st, ga, scales, n_scale);
-    BH_LAUNCH(pq2_norm_write_kernel, wgrid, 256, 0, st, ga, scales);
+    const unsigned scale_blocks = static_cast<unsigned>((n_ids + kScaleRows - 1) / kScaleRows);
+    const unsigned s_per = (scale_blocks + 7) / 8;
+    const unsigned e_per = (wgrid + 7) / 8;
+    BH_LAUNCH(pq2_scale_embed_kernel, 8 * s_per + 8 * e_per, 256, smem, st, ga, scales, 8 * s_per,
+              s_per, e_per);
+    BH_LAUNCH(pq2_norm_write_kernel, 8 * e_per, 256, 0, st, ga, scales, e_per);
     return ok();
   }
   if (rows_ok && norm && row_bytes % 16 == 0 && fused_smem_bytes(row_bytes, 16, 128) <= kMaxSeqSmem) {
