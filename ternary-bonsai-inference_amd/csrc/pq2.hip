@@ -410,9 +410,10 @@ size_t scale_smem_bytes(size_t row_bytes) {
 
 // Plain gather: one float4 of output per lane over the flat [n_ids][ne0/4]
 // range (fits 32 bits: checked by the host).
-__global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a) {
+__global__ __launch_bounds__(256) void pq2_rows_write_kernel(GatherArgs a, unsigned per) {
   const uint32_t n4 = static_cast<uint32_t>(a.ne0) >> 2;
-  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  // XCD-contiguous block order: a row's blocks share one XCD's L2
+  const uint32_t idx = xcd_block(blockIdx.x, per) * 256u + threadIdx.x;
   if (idx >= static_cast<uint32_t>(a.n_ids) * n4) return;
   const uint32_t t = idx / n4;
   const uint32_t f = idx - t * n4;
@@ -518,7 +519,8 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
   ga.n_rows = nr;
   ga.eps = eps;
   if (rows_ok && !norm) {
-    BH_LAUNCH(pq2_rows_write_kernel, wgrid, 256, 0, st, ga);
+    const unsigned per = (wgrid + 7) / 8;
+    BH_LAUNCH(pq2_rows_write_kernel, 8 * per, 256, 0, st, ga, per);
     return ok();
   }
   const size_t cus = device_cu_count();
