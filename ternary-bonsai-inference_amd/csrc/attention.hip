@@ -1003,7 +1003,13 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
     const int full = n_groups / 8 * 8;         // groups placed 8 at a time
     const int x = b % 8, jb = b / 8;
     int q;
-    if (jb < (full / 8) * tiles_r) {
+    if (a.n_chunks == 1) {
+      // one chunk (every position in one block, e.g. a causal prefill): the
+      // row tiles longest-first, kv heads interleaved, so the tiles that see
+      // the most positions start in the first round instead of the last
+      t = tiles_r - 1 - b / a.n_kv;
+      q = b % a.n_kv;
+    } else if (jb < (full / 8) * tiles_r) {
       q = (jb / tiles_r) * 8 + x;
       t = jb % tiles_r;
     } else {  // the last n_groups % 8 groups, in plain order
