@@ -940,6 +940,9 @@ struct MqArgs {
   // planar-quantized caches: kc holds the packed K rows, vc the packed V rows
   // (or V's f32 rows), kn / vn the norms; unused otherwise
   const float *kn, *vn;
+  // one chunk: the rows are final, written here as acc / l (the merge of a
+  // single chunk, bit for bit) instead of as partials; nullptr otherwise
+  float *out;
 };
 
 // 2^e as a float for e <= 127; 0 below the normal range
@@ -1032,7 +1035,13 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
   const size_t end = beg + a.chunk < lim_blk ? beg + a.chunk : lim_blk;
   const size_t part = (static_cast<size_t>(qi) * a.n_head + head) * a.n_chunks + c;
   if (beg >= end) {  // no position of this chunk is visible to the tile
-    if (valid) {
+    if (valid && a.out != nullptr) {
+      // (not reached: a one-chunk tile sees position 0) the merge's 0 / 0
+      f32x4 *dst = reinterpret_cast<f32x4 *>(a.out + (static_cast<size_t>(qi) * a.n_head + head) * kHd);
+      const float nan = __builtin_nanf("");
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) dst[4 * dt + grp] = f32x4{nan, nan, nan, nan};
+    } else if (valid) {
       if (grp == 0) {
         a.pm[part] = -INFINITY;
         a.pl[part] = 0.0f;
@@ -1364,14 +1373,21 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
     __syncthreads();  // the staged tile is consumed
   }
   if (valid) {
-    if (grp == 0) {
-      a.pm[part] = run_m;
-      a.pl[part] = run_l;
-    }
     const float u = F16 ? 1.0f / 16384.0f : pow2f(vs_cur - 14);
-    f32x4 *acc = reinterpret_cast<f32x4 *>(a.pacc + part * kHd);
+    if (a.out != nullptr) {
+      // the merge of one chunk: weight e^0 = 1, so (acc * 1) / (l * 1)
+      f32x4 *dst = reinterpret_cast<f32x4 *>(a.out + (static_cast<size_t>(qi) * a.n_head + head) * kHd);
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) acc[4 * dt + grp] = o[dt] * u;
+      for (int dt = 0; dt < 16; ++dt) dst[4 * dt + grp] = (o[dt] * u) / run_l;
+    } else {
+      if (grp == 0) {
+        a.pm[part] = run_m;
+        a.pl[part] = run_l;
+      }
+      f32x4 *acc = reinterpret_cast<f32x4 *>(a.pacc + part * kHd);
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt) acc[4 * dt + grp] = o[dt] * u;
+    }
   }
 }
 
@@ -1872,7 +1888,8 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
     if (scratch == nullptr) return BH_ERR_HIP;
     MqArgs m{q, k_cache, v_cache, scratch, scratch + rows, scratch + 2 * rows, pos0, kv_stride,
              chunk, static_cast<int>(n_head), static_cast<int>(n_q), static_cast<int>(rep),
-             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale, nullptr, nullptr};
+             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale, nullptr, nullptr,
+             n_chunks == 1 ? out : nullptr};
     // 1-D grid of (chunk, kv head, row tile) in XCD-aware order (the kernel
     // decodes it)
     const size_t nb = n_chunks * n_kv * tiles_r;
@@ -1882,8 +1899,9 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
       BH_LAUNCH(attn_mq_kernel<true>, grid, kMqThreads, 0, st, m);
     else
       BH_LAUNCH(attn_mq_kernel<false>, grid, kMqThreads, 0, st, m);
-    BH_LAUNCH(attn_merge_rows_kernel, static_cast<unsigned>(n_q * n_head), 256, 0, st, m.pm, m.pl,
-              m.pacc, static_cast<int>(n_chunks), out);
+    if (n_chunks > 1)
+      BH_LAUNCH(attn_merge_rows_kernel, static_cast<unsigned>(n_q * n_head), 256, 0, st, m.pm, m.pl,
+                m.pacc, static_cast<int>(n_chunks), out);
     return ok();
   }
   if (fast) {
@@ -2011,7 +2029,7 @@ extern "C" int bh_attention_planar(const float *q, size_t n_q, size_t pos0, cons
     MqArgs m{q, kq, vq != nullptr ? static_cast<const void *>(vq) : static_cast<const void *>(v_f32),
              scratch, scratch + rows, scratch + 2 * rows, pos0, n_kv * kHd, chunk,
              static_cast<int>(n_head), static_cast<int>(n_q), static_cast<int>(rep),
-             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale, kn, vn};
+             static_cast<int>(n_chunks), static_cast<int>(n_kv), scale, kn, vn, nullptr};
     const size_t nb = n_chunks * n_kv * tiles_r;
     if (nb > 0x7fffffffu) return fail(BH_ERR_SHAPE, "attention_planar: too many blocks");
     const int e = vq != nullptr ? launch_mq_planar<true>(static_cast<int>(bits), m, dim3(static_cast<unsigned>(nb)), tb, st)
