@@ -558,6 +558,59 @@ def load_traffic():
         return {}
 
 
+def measure_traffic_live(timeout_s: float = 90.0, budget_s: float = 240.0):
+    """The headline kernel's HBM bytes per call measured now: two rocprofv3
+    --pmc child runs of this bench (FETCH_SIZE, then WRITE_SIZE, headline
+    only), each scaled by what the same counter reads for a 256 MiB device
+    copy (two more child runs).  Returns (bytes, note) or (None, reason)."""
+    import csv
+    import glob
+    import shutil
+    import statistics
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None, "rocprofv3 not found"
+    env = dict(os.environ, TMPDIR="/tmp")
+    me = [sys.executable, str(Path(__file__).resolve())]
+    child = ["--headline-only", "--steps", "10", "--warmup", "2", "--cpu-seconds", "0",
+             "--traffic", "committed"]
+    runs = {"fetch": ("FETCH_SIZE", me + child),
+            "write": ("WRITE_SIZE", me + child),
+            "cfetch": ("FETCH_SIZE", me + ["--calibrate-copy", "256", "--steps", "5"]),
+            "cwrite": ("WRITE_SIZE", me + ["--calibrate-copy", "256", "--steps", "5"])}
+    vals = {}
+    t0 = time.time()
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        for key, (counter, cmd) in runs.items():
+            if time.time() - t0 > budget_s:
+                return None, "counter runs over their time budget"
+            d = os.path.join(tmp, key)
+            try:
+                subprocess.run([prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", key,
+                                "--"] + cmd, env=env, cwd="/tmp", capture_output=True,
+                               timeout=timeout_s, check=True)
+                f = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)[0]
+                rows = [r for r in csv.DictReader(open(f)) if r["Counter_Name"].startswith(counter)]
+                if key.startswith("c"):
+                    sel = [float(r["Counter_Value"]) for r in rows if "elementwise" in r["Kernel_Name"]
+                           and int(r.get("Grid_Size") or r.get("Grid_Size_X") or 0) > 1000000]
+                else:
+                    sel = [float(r["Counter_Value"]) for r in rows
+                           if "qk_norm_rope_kernel" in r["Kernel_Name"]]
+                vals[key] = statistics.median(sel)
+            except (OSError, subprocess.SubprocessError, IndexError, ValueError,
+                    statistics.StatisticsError) as e:
+                return None, f"live counter run {key} failed: {type(e).__name__}"
+    copy = 256 * 2**20
+    fbytes = vals["fetch"] * copy / vals["cfetch"]
+    wbytes = vals["write"] * copy / vals["cwrite"]
+    return int(fbytes + wbytes), ("live: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this bench's "
+                                  "headline in this run, scaled by a 256 MiB copy "
+                                  f"(fetch {fbytes / 1e6:.1f} MB, write {wbytes / 1e6:.1f} MB)")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -571,7 +624,15 @@ def main() -> int:
                     help="length of the CPU-baseline sample (0 disables)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
+    ap.add_argument("--traffic", choices=("live", "committed"), default="live",
+                    help="live (default): measure the headline's HBM traffic in this run with "
+                         "four short rocprofv3 counter child runs (falls back to the committed "
+                         "figure if they fail); committed: read profiles/traffic_all_configs.json")
     args = ap.parse_args()
+    # no nested counter runs when this process itself runs under rocprofv3
+    profiled = any(k.startswith("ROCPROF") for k in os.environ)
+    live = args.traffic == "live" and not args.calibrate_copy and args.gpus == 1 and not profiled
+    live_traffic = measure_traffic_live() if live else (None, "")
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(every kernel is row-independent: multi-GPU runs would shard rows with no "
@@ -693,6 +754,14 @@ def main() -> int:
     for k in kernels:
         if k["kernel"] in traffic:
             k["traffic"] = traffic[k["kernel"]]
+    traffic_source = ("profiles/traffic_all_configs.json: rocprofv3 --pmc FETCH_SIZE / "
+                      "WRITE_SIZE runs of this bench, copy-calibrated (commands inside)")
+    if live_traffic[0] is not None:
+        traffic["qk_norm_rope"] = live_traffic[0]
+        head["traffic"] = live_traffic[0]
+        traffic_source = live_traffic[1]
+    elif live:
+        traffic_source += f" (live measurement not used: {live_traffic[1]})"
     ms = head["ms"]
     line = {
         "metric": "achieved HBM GB/s (% of 8 TB/s) per fused kernel; rows/s at T=2048",
@@ -714,7 +783,7 @@ def main() -> int:
         "rows_per_s": head["rows_per_s"],
         "roofline": {"bound": "hbm", "achieved": head["GBps"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["GBps"] / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("qk_norm_rope")},
+                     "traffic": traffic.get("qk_norm_rope"), "traffic_source": traffic_source},
         "cpu_baseline": cpu,
         "kernels": kernels,
     }
