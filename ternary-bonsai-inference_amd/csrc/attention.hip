@@ -940,8 +940,9 @@ struct MqArgs {
   // planar-quantized caches: kc holds the packed K rows, vc the packed V rows
   // (or V's f32 rows), kn / vn the norms; unused otherwise
   const float *kn, *vn;
-  // one chunk: the rows are final, written here as acc / l (the merge of a
-  // single chunk, bit for bit) instead of as partials; nullptr otherwise
+  // one chunk: the rows are final, written here as acc / l (what the merge
+  // of a single chunk computes; only an exact zero's sign can differ)
+  // instead of as partials; nullptr otherwise
   float *out;
 };
 
@@ -1376,6 +1377,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
     const float u = F16 ? 1.0f / 16384.0f : pow2f(vs_cur - 14);
     if (a.out != nullptr) {
       // the merge of one chunk: weight e^0 = 1, so (acc * 1) / (l * 1)
+      // (the merge's 0 + acc turns an exact -0 into +0; nothing else differs)
       f32x4 *dst = reinterpret_cast<f32x4 *>(a.out + (static_cast<size_t>(qi) * a.n_head + head) * kHd);
 #pragma unroll
       for (int dt = 0; dt < 16; ++dt) dst[4 * dt + grp] = (o[dt] * u) / run_l;
