@@ -234,6 +234,18 @@ __device__ __forceinline__ float exp_hw(float x) {
   return x == -INFINITY ? 0.0f : r * __builtin_fmaf(err, kLn2, 1.0f);
 }
 
+// silu with the hardware exponential (exp_hw) and reciprocal: within a few
+// ulps of silu() -- for kernels whose outputs carry the 1e-5 tolerance, not
+// for the bit-exact unary entry point.  Infinite and NaN inputs give what
+// silu() gives (-inf: NaN; +inf: +inf).
+__device__ __forceinline__ float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + exp_hw(-x));
+}
+// sigmoid the same way (within a few ulps of sigmoid())
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + exp_hw(-x));
+}
+
 // gguf::half_to_f32 (src/gguf.rs:881-911) in integer arithmetic: exact for
 // every one of the 65536 patterns, NaN payloads kept (no quieting).
 __device__ __forceinline__ uint32_t half_bits_to_f32_bits(uint32_t h) {

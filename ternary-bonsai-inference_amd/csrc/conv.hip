@@ -99,7 +99,8 @@ __global__ __launch_bounds__(kBlock) void conv1d_silu4_kernel(ConvIn cv, float *
         acc.w += wv[3][j] * win[j].w;
       }
       store_stream(reinterpret_cast<float4 *>(out + (t0 + tt) * cv.ch) + i,
-                   make_float4(silu(acc.x), silu(acc.y), silu(acc.z), silu(acc.w)));
+                   make_float4(silu_fast(acc.x), silu_fast(acc.y), silu_fast(acc.z),
+                               silu_fast(acc.w)));
 #pragma unroll
       for (int j = 0; j < 3; ++j) win[j] = win[j + 1];
     }

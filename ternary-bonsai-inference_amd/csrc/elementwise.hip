@@ -137,8 +137,19 @@ __global__ __launch_bounds__(kBlock) void gdn_gate_prep_kernel(GdnParams a, size
   if (i < total) small_gates(a, i, static_cast<int>(i % a.n_v_head));
 }
 
+// The fused prep kernels' activations: the hardware exponential and
+// reciprocal (silu_fast / sigmoid_fast, a few ulps from the reference's
+// expf-based forms; these outputs carry the 1e-5 tolerance).  Measured on
+// the standalone conv: 65.5 -> 62.5 us.
 __device__ __forceinline__ float4 silu4(float4 v) {
-  return make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
+  return make_float4(silu_fast(v.x), silu_fast(v.y), silu_fast(v.z), silu_fast(v.w));
+}
+// src/forward.rs:549-551 / :379-382: y * silu(z) or y * sigmoid(z)
+__device__ __forceinline__ float4 gate4(float4 z, float4 y, bool sig) {
+  return sig ? make_float4(y.x * sigmoid_fast(z.x), y.y * sigmoid_fast(z.y), y.z * sigmoid_fast(z.z),
+                           y.w * sigmoid_fast(z.w))
+             : make_float4(y.x * silu_fast(z.x), y.y * silu_fast(z.y), y.z * silu_fast(z.z),
+                           y.w * silu_fast(z.w));
 }
 
 // kU = 2 float4 per lane (measured on [4096 tokens, 6144]: 92 us vs 100 us
@@ -200,7 +211,7 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_fused_kernel(GdnParams a, int
       const int i = ((part - bc) * kU + u) * kBlock + tid;
       if (i < n4) {
         store_stream(reinterpret_cast<float4 *>(a.gated_out) + t * n4 + i,
-                   a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(z[u], y[u]) : unary_op4<BH_SILU_MUL>(z[u], y[u]));
+                     gate4(z[u], y[u], a.sigmoid_gate != 0));
       }
     }
   }
@@ -353,8 +364,7 @@ __global__ __launch_bounds__(kBlock) void gdn_prep_conv_kernel(GdnParams a, int 
       const int i = (gb * kU + u) * kBlock + tid;
       if (i < n4)
         store_stream(reinterpret_cast<float4 *>(a.gated_out) + t * n4 + i,
-                     a.sigmoid_gate ? unary_op4<BH_SIGMOID_MUL>(z[u], y[u])
-                                    : unary_op4<BH_SILU_MUL>(z[u], y[u]));
+                     gate4(z[u], y[u], a.sigmoid_gate != 0));
     }
   }
 }
