@@ -529,8 +529,8 @@ int gather_impl(const uint8_t *table, size_t ne0, size_t n_rows, const uint32_t 
     // Long batches: row scales + embedding rows, then the norm rows (two
     // flat writers).  The scale walk (~20 us of dependent steps) hides under
     // the embedding stores only when there are enough of them: measured at
-    // T=8192 65.9-67.1 us against 70.6-72.5 for the one-launch kernel below,
-    // at T=2048 31.5 against 29.8 (so shorter batches stay on that kernel).
+    // T=8192 55.5-64 us against 69-72 for the one-launch kernel below, at
+    // T=2048 32.0 against 30.0 (so shorter batches stay on that kernel).
     float *scales = static_cast<float *>(device_scratch(n_ids * sizeof(float), kScratchGather, st));
     if (scales == nullptr) return BH_ERR_HIP;
     const size_t smem = scale_smem_bytes(row_bytes);
