@@ -54,7 +54,8 @@ constexpr int kScratchSoftmax = 0;  // split-row softmax partials
 constexpr int kScratchMatmul = 1;   // PQ2_0 product: f16 x fragments, token scales
 constexpr int kScratchAttention = 2;  // attention: chunk partials or probabilities
 constexpr int kScratchGather = 3;     // gather + RMSNorm: the row scales
-constexpr int kScratchSlots = 4;
+constexpr int kScratchGdn = 4;        // gated delta-net chunks: prepared matrices
+constexpr int kScratchSlots = 5;
 void *device_scratch(size_t bytes, int slot, hipStream_t stream);
 // Current size of this device's buffer for `slot` (0 before the first use).
 size_t scratch_bytes(int slot);

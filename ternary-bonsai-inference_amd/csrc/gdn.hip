@@ -431,6 +431,418 @@ __global__ __launch_bounds__(kBlock) void gdn_step_generic_kernel(GdnStepArgs a)
   }
 }
 
+// ---- chunked path (matrix cores) -----------------------------------------
+//
+// Long batches (prefill) take the recurrence 64 tokens at a time in its
+// closed form per chunk.  For one v-head, a row m of the state (m_0 at the
+// chunk start), the chunk's tokens t = 0..63 with decays a_t = expf(gate_t),
+// A_t = a_0 ... a_t and D_ts = A_t / A_s (s <= t), unrolling the per-token
+// steps gives
+//   x_t     = a_t m_(t-1).k_t = A_t (m_0.k_t) + sum_(s<t) D_ts (k_s.k_t) delta_s
+//   delta_t = beta_t (v_t - x_t)
+// so the chunk's deltas solve the unit lower triangular system
+//   (I + L) delta = beta (v - A (K m_0)),   L_ts = beta_t D_ts (k_t.k_s), s < t,
+// whose matrix depends on the head's gates, betas and keys only -- not on
+// the state, so it is inverted once per (chunk, v-head) for all 128 rows.
+// With T' = (I + L)^-1 diag(beta) and P_ts = D_ts (q_t.k_s) (s <= t):
+//   delta = T' (v - A (K m_0))
+//   attn  = (A (Q m_0) + P delta) / sqrt(s)
+//   m_64  = A_63 m_0 + sum_s (A_63 / A_s) delta_s k_s.
+// The same algebra the per-token steps perform, rounded differently (the
+// products summed in other orders); measured within ~2e-6 of the per-token
+// f32 recurrence (relative to the tensor's largest magnitude) on keys from
+// independent to nearly identical, betas up to 1 and decays from none to
+// underflow.
+//
+// gdn_chunk_prep_kernel (one workgroup per (chunk, q/k head), all chunks in
+// parallel) forms K K^T and Q K^T on v_mfma_f32_16x16x4_f32, then, one wave
+// per v-head of that q/k head, the decays (prefix sums of the gates in f64,
+// so a large early gate costs no precision in later differences), L, its
+// inverse (16 x 16 diagonal blocks by forward substitution, a lane per
+// column, the other blocks by f32 MFMA products), T' and P, stored in
+// the order the walk's MFMA A operands read them.  gdn_chunk_walk_kernel
+// (one workgroup per (v-head, 16 state rows)) keeps its rows' state in
+// registers as MFMA operands and walks the chunks in order: K m_0 and Q m_0
+// (wave w: tokens 16w..16w+15), delta through T' (LDS exchange of the
+// right-hand sides), the outputs through P, and the new state (wave w: 32
+// of the 128 columns), all on f32 MFMA.
+constexpr int kCk = 64;                         // tokens per chunk
+constexpr int kCkFrag = kCk * kCk;              // floats of a 64 x 64 matrix
+constexpr int kCkPer = 2 * kCkFrag + 2 * kCk;   // per (chunk, v-head): T', P, A, e
+constexpr int kCkPitch = 132;                   // prep: staged K / Q rows (floats)
+constexpr int kCkBuf = 65;                      // prep: pitch of the 64 x 64 matrices in LDS
+constexpr int kCkKPitch = 144;                  // walk: staged K rows
+constexpr int kCkMPitch = 132;                  // walk: staged state rows
+constexpr size_t kChunkMin = 64;                // batches from which the chunked path runs
+constexpr float kGateFloor = -200.0f;           // expf below this is 0 in f32
+static_assert(kCk * kCkBuf <= 2 * kCk * kCkPitch, "L fits the staging area");
+
+typedef float f32x4m __attribute__((ext_vector_type(4)));
+
+struct GdnChunkArgs {
+  const float *q, *k, *v, *gate, *beta;
+  float *state, *attn;
+  float *scr;  // [n_chunks][h_v][kCkPer]
+  size_t n_tok;
+  int h_k, h_v, n_chunks;
+  float scale;
+  int xcd_map;
+  int prep_per;  // prep workgroups per (chunk, q/k head): 1, or one per v-head
+};
+
+__device__ __forceinline__ f32x4m mfma_f32(float a, float b, f32x4m c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// T' and P are stored in MFMA A-fragment order: element (r, c) of row tile
+// wt = r / 16 belongs to lane l = r % 16 + 16 (c % 4) at step ks = c / 4 and
+// sits at ((wt * 64 + l) * 16 + ks), so each lane of the walk reads its 16
+// values of a tile as four 16-byte loads.
+
+// Block (bi, bj), bi >= bj, of the inverse in a per-wave 64 x 64 buffer:
+// diagonal blocks in place, T_ij (i > j) in the upper block (j, i), which L
+// leaves free.
+__device__ __forceinline__ float *tblock(float *buf, int bi, int bj) {
+  return bi == bj ? buf + 16 * bi * (kCkBuf + 1) : buf + 16 * bj * kCkBuf + 16 * bi;
+}
+
+// Tiles k = w + 4 u (u < N) of the lower triangle of K K^T and Q K^T (tile
+// k: row tile ti, column tile nt <= ti), accumulated over the 128 dims and
+// written to LDS at pitch kCkBuf.  N is a template parameter so the
+// accumulators stay in registers across the loop (no per-step branches).
+template <int N>
+__device__ __forceinline__ void prep_qk_tiles(const float *sK, const float *sQ, float *sKK,
+                                              float *sQK, int w, int lr, int lg) {
+  f32x4m accK[N], accQ[N];
+  int ra[N], rb[N], ti[N], nt[N];
+#pragma unroll
+  for (int u = 0; u < N; ++u) {
+    const int k = w + 4 * u;
+    ti[u] = k < 1 ? 0 : (k < 3 ? 1 : (k < 6 ? 2 : 3));
+    nt[u] = k - ti[u] * (ti[u] + 1) / 2;
+    ra[u] = (16 * ti[u] + lr) * kCkPitch + lg;
+    rb[u] = (16 * nt[u] + lr) * kCkPitch + lg;
+    accK[u] = accQ[u] = f32x4m{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll 8
+  for (int ks = 0; ks < kFast / 4; ++ks) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+      const float b = sK[rb[u] + 4 * ks];
+      accK[u] = mfma_f32(sK[ra[u] + 4 * ks], b, accK[u]);
+      accQ[u] = mfma_f32(sQ[ra[u] + 4 * ks], b, accQ[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < N; ++u)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      sKK[(16 * ti[u] + 4 * lg + rr) * kCkBuf + 16 * nt[u] + lr] = accK[u][rr];
+      sQK[(16 * ti[u] + 4 * lg + rr) * kCkBuf + 16 * nt[u] + lr] = accQ[u][rr];
+    }
+}
+
+// Workgroup (chunk c, q/k head kh, part): with `per` = 1 it prepares every
+// v-head of kh (K K^T and Q K^T formed once for all of them); with per > 1
+// (short batches, to fill the chip) part n prepares v-head kh + n h_k only.
+// The four waves share each v-head: wave w forms rows 16 w .. 16 w + 15 of P
+// and L (lane (lr, lg): row 16 w + lr, columns 16 lg .. 16 lg + 15),
+// inverts diagonal block w, takes pair w of each distance of the
+// off-diagonal blocks and stores row tile w of T'.  Its LDS (K, Q, K K^T,
+// Q K^T) allows one workgroup per CU, so registers are scheduled for one
+// wave per SIMD.
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+gdn_chunk_prep_kernel(GdnChunkArgs a) {
+  __shared__ __attribute__((aligned(16))) float sStage[2 * kCk * kCkPitch];  // K, Q; then L and the inverse
+  __shared__ float sKK[kCk * kCkBuf];  // pitch 65: lane t reading row t hits bank t + s
+  __shared__ float sQK[kCk * kCkBuf];
+  __shared__ double sG[kCk];
+  __shared__ float sB[kCk];
+  __shared__ float sS[4][16 * 17];  // per-wave block products in transit
+  const int per = a.prep_per;
+  const int bid = static_cast<int>(blockIdx.x);
+  const int c = bid / (a.h_k * per), kh = (bid / per) % a.h_k, part = bid % per;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar branches)
+  const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+  const size_t t0 = static_cast<size_t>(c) * kCk;
+  float *sK = sStage, *sQ = sStage + kCk * kCkPitch;
+  // stage the chunk's k and q rows of this head (zeros past the batch)
+#pragma unroll
+  for (int i = 0; i < kCk * 32 / kBlock; ++i) {
+    const int e = i * kBlock + threadIdx.x, t = e >> 5, c4 = e & 31;
+    f32x4m kv = {0.0f, 0.0f, 0.0f, 0.0f}, qv = kv;
+    if (t0 + t < a.n_tok) {
+      const size_t off = ((t0 + t) * a.h_k + kh) * kFast + 4 * c4;
+      kv = *reinterpret_cast<const f32x4m *>(a.k + off);
+      qv = *reinterpret_cast<const f32x4m *>(a.q + off);
+    }
+    *reinterpret_cast<f32x4m *>(sK + t * kCkPitch + 4 * c4) = kv;
+    *reinterpret_cast<f32x4m *>(sQ + t * kCkPitch + 4 * c4) = qv;
+  }
+  __syncthreads();
+  // K K^T and Q K^T on the 10 tiles with s <= t: tiles k = w, w + 4, w + 8
+  // (of those below 10) to wave w
+  if (w < 2)
+    prep_qk_tiles<3>(sK, sQ, sKK, sQK, w, lr, lg);
+  else
+    prep_qk_tiles<2>(sK, sQ, sKK, sQK, w, lr, lg);
+  __syncthreads();
+  float *buf = sStage;  // 64 x 64 at pitch kCkBuf: L, then the inverse
+  const int n_vh = (a.h_v - kh + a.h_k - 1) / a.h_k;  // v-heads h = kh + n h_k
+  const int t = 16 * w + lr;                            // this lane's row of P and L
+  for (int n = part; n < n_vh; n += per) {              // the same count in every wave
+    const int hv = kh + n * a.h_k;
+    float *out = a.scr + (static_cast<size_t>(c) * a.h_v + hv) * kCkPer;
+    if (w == 0) {
+      // decays: A_t = expf(G_t), e_t = expf(G_63 - G_t), G the prefix sums
+      // of the gates (f64) -- lane l = token l
+      float g = 0.0f, b = 0.0f;
+      if (t0 + l < a.n_tok) {
+        g = a.gate[(t0 + l) * a.h_v + hv];
+        b = a.beta[(t0 + l) * a.h_v + hv];
+      }
+      g = g < kGateFloor ? kGateFloor : g;  // -inf too (NaN stays NaN)
+      double G = static_cast<double>(g);
+#pragma unroll
+      for (int d = 1; d < kCk; d <<= 1) {
+        const double o = __shfl_up(G, d, kCk);
+        if (l >= d) G += o;
+      }
+      const double Glast = __shfl(G, kCk - 1, kCk);
+      sG[l] = G;
+      sB[l] = b;
+      out[2 * kCkFrag + l] = expf(static_cast<float>(G));
+      out[2 * kCkFrag + kCk + l] = expf(static_cast<float>(Glast - G));
+    }
+    __syncthreads();
+    // P and L on this lane's 16 entries (D_ts = expf(G_t - G_s), s <= t);
+    // P goes out in A-fragment order: entries 16 lg + m + 4 j (j = 0..3) are
+    // the consecutive steps 4 lg + j of lane t % 16 + 16 m
+    {
+      const double Gt = sG[t];
+      const float bt = sB[t];
+      float pv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int s = 16 * lg + i;
+        const float arg = static_cast<float>(Gt - sG[s]);
+        const float d = s <= t ? exp_hw(arg < 0.0f ? arg : 0.0f) : 0.0f;
+        pv[i] = s <= t ? d * sQK[t * kCkBuf + s] : 0.0f;
+        buf[t * kCkBuf + s] = s < t ? bt * d * sKK[t * kCkBuf + s] : 0.0f;
+      }
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<f32x4m *>(out + kCkFrag + (w * 64 + lr + 16 * m) * 16 + 4 * lg) =
+            f32x4m{pv[m], pv[m + 4], pv[m + 8], pv[m + 12]};
+    }
+    __syncthreads();
+    // (I + L)^-1 blockwise (16 x 16 blocks).  Diagonal block w: lane lr of
+    // lane group 0 takes column lr by forward substitution (when row r is
+    // final its multiple goes into every later row), then overwrites L_ww.
+    float x[16];
+    float *dg = buf + 16 * w * (kCkBuf + 1);
+    if (lg == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[r] = r == lr ? 1.0f : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 15; ++r)
+#pragma unroll
+        for (int r2 = r + 1; r2 < 16; ++r2) x[r2] = fmaf(-dg[r2 * kCkBuf + r], x[r], x[r2]);
+    }
+    __syncthreads();
+    if (lg == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dg[r * kCkBuf + lr] = x[r];
+    }
+    __syncthreads();
+    // Off-diagonal blocks, one distance at a time, pair (w + dist, w) on
+    // wave w:  T_ij = -T_ii (sum_(j <= m < i) L_im T_mj)  (f32 MFMA); T_ij
+    // (i > j) is kept in the upper block (j, i), which L leaves free.
+    for (int dist = 1; dist < 4; ++dist) {
+      const int bi = w + dist, bj = w;
+      if (bi < 4) {
+        f32x4m S = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int m = bj; m < bi; ++m) {
+          const float *la = buf + (16 * bi + lr) * kCkBuf + 16 * m + lg;  // L_(bi, m), A operand
+          const float *tt = tblock(buf, m, bj) + lg * kCkBuf + lr;       // T_(m, bj), B operand
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) S = mfma_f32(la[4 * ks], tt[4 * ks * kCkBuf], S);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) sS[w][(4 * lg + rr) * 17 + lr] = S[rr];
+      }
+      __syncthreads();
+      if (bi < 4) {
+        f32x4m tij = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float *ta = tblock(buf, bi, bi) + lr * kCkBuf + lg;  // T_ii, A operand
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) tij = mfma_f32(ta[4 * ks], sS[w][(4 * ks + lg) * 17 + lr], tij);
+        float *dst = tblock(buf, bi, bj);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) dst[(4 * lg + rr) * kCkBuf + lr] = -tij[rr];
+      }
+      __syncthreads();
+    }
+    // T' = (I + L)^-1 diag(beta), row tile w in A-fragment order: lane l =
+    // r % 16 + 16 (c % 4) holds steps ks = c / 4 of row r = 16 w + l % 16
+    {
+      f32x4m *d = reinterpret_cast<f32x4m *>(out + (w * 64 + l) * 16);
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        f32x4m v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int col = 4 * (4 * i4 + e) + lg;
+          v[e] = (col >> 4) <= w ? tblock(buf, w, col >> 4)[lr * kCkBuf + (col & 15)] * sB[col]
+                                 : 0.0f;
+        }
+        d[i4] = v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Workgroup p -> (v-head, 16-row slab).  With xcd_map the 8 slabs of every
+// v-head of one q/k head land on one XCD (workgroup p runs on XCD p % 8), so
+// that XCD's L2 serves their re-reads of the head's k and q rows and of the
+// prepared matrices.  Only placement changes, never results.
+__device__ __forceinline__ int walk_tile(const GdnChunkArgs &a) {
+  const int p = static_cast<int>(blockIdx.x);
+  constexpr int bph = kFast / 16;
+  if (!a.xcd_map) return p;
+  const int g = (a.h_v / a.h_k) * bph;
+  const int x = p % 8, sl = p / 8;
+  const int kh = (sl / g) * 8 + x;
+  const int local = sl % g;
+  return (kh + (local / bph) * a.h_k) * bph + local % bph;
+}
+
+// The token rows of chunk c (k and q at A-operand row 16 w + lr, v at the
+// D rows 16 w + 4 lg + rr of state row j); zeros past the batch.
+__device__ __forceinline__ void walk_load_tokens(const GdnChunkArgs &a, int c, int h, int kh, int j,
+                                                 int w, int lr, int lg, f32x4m (&kr)[8],
+                                                 f32x4m (&qr)[8], float (&vr)[4]) {
+  const size_t t0 = static_cast<size_t>(c) * kCk;
+  const size_t tok = t0 + 16 * w + lr;
+  if (tok < a.n_tok) {
+    const size_t off = (tok * a.h_k + kh) * kFast + 4 * lg;
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+      kr[ib] = *reinterpret_cast<const f32x4m *>(a.k + off + 16 * ib);
+      qr[ib] = *reinterpret_cast<const f32x4m *>(a.q + off + 16 * ib);
+    }
+  } else {
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) kr[ib] = qr[ib] = f32x4m{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const size_t tt = t0 + 16 * w + 4 * lg + rr;
+    vr[rr] = tt < a.n_tok ? a.v[(tt * a.h_v + h) * kFast + j] : 0.0f;
+  }
+}
+
+// The chunk's rows are loaded while the previous chunk runs (issued after
+// its K m_0 / Q m_0 products, when those registers are free), and the
+// prepared matrices at the top of the chunk, ahead of the products that
+// precede their use: each chunk then waits on at most one memory round trip.
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+gdn_chunk_walk_kernel(GdnChunkArgs a) {
+  __shared__ __attribute__((aligned(16))) float sK[kCk * kCkKPitch];
+  __shared__ __attribute__((aligned(16))) float sR[kCk * 16];
+  __shared__ __attribute__((aligned(16))) float sD[kCk * 16];
+  __shared__ __attribute__((aligned(16))) float sM[16 * kCkMPitch];
+  __shared__ float sE[kCk];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (scalar branches)
+  const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
+  const int tile = walk_tile(a);
+  const int h = tile / (kFast / 16), kh = h % a.h_k;
+  const int j = (tile % (kFast / 16)) * 16 + lr;  // the state row of this lane's columns
+  float *mrow = a.state + (static_cast<size_t>(h) * kFast + j) * kFast;
+  // M[ib][r] = m_0[j][16 ib + 4 lg + r]: the B operand of step (ib, r) of
+  // K m_0^T and the D fragment of column tile ib of the new state
+  f32x4m M[8];
+#pragma unroll
+  for (int ib = 0; ib < 8; ++ib) M[ib] = *reinterpret_cast<const f32x4m *>(mrow + 16 * ib + 4 * lg);
+  f32x4m kr[8], qr[8];
+  float vr[4];
+  walk_load_tokens(a, 0, h, kh, j, w, lr, lg, kr, qr, vr);
+  for (int c = 0; c < a.n_chunks; ++c) {
+    const size_t t0 = static_cast<size_t>(c) * kCk;
+    const float *scr = a.scr + (static_cast<size_t>(c) * a.h_v + h) * kCkPer;
+    const f32x4m *tf = reinterpret_cast<const f32x4m *>(scr + (w * 64 + l) * 16);
+    const f32x4m *pf = reinterpret_cast<const f32x4m *>(scr + kCkFrag + (w * 64 + l) * 16);
+    f32x4m tfr[4], pfr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      tfr[i] = tf[i];
+      pfr[i] = pf[i];
+    }
+    const f32x4m At = *reinterpret_cast<const f32x4m *>(scr + 2 * kCkFrag + 16 * w + 4 * lg);
+    const float alast = scr[2 * kCkFrag + kCk - 1];
+    if (w == 0) sE[l] = scr[2 * kCkFrag + kCk + l];
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib)
+      *reinterpret_cast<f32x4m *>(sK + (16 * w + lr) * kCkKPitch + 16 * ib + 4 * lg) = kr[ib];
+    // K m_0^T and Q m_0^T, two accumulators each (independent MFMA chains)
+    f32x4m X0 = {0.0f, 0.0f, 0.0f, 0.0f}, X1 = X0, Y0 = X0, Y1 = X0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ib += 2)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        X0 = mfma_f32(kr[ib][r], M[ib][r], X0);
+        Y0 = mfma_f32(qr[ib][r], M[ib][r], Y0);
+        X1 = mfma_f32(kr[ib + 1][r], M[ib + 1][r], X1);
+        Y1 = mfma_f32(qr[ib + 1][r], M[ib + 1][r], Y1);
+      }
+    const f32x4m X = X0 + X1, Y = Y0 + Y1;
+    // right-hand sides v - A (K m_0): tokens 16 w + 4 lg + rr, row j
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sR[(16 * w + 4 * lg + rr) * 16 + lr] = vr[rr] - At[rr] * X[rr];
+    if (c + 1 < a.n_chunks) walk_load_tokens(a, c + 1, h, kh, j, w, lr, lg, kr, qr, vr);
+    __syncthreads();
+    // delta rows of tile w = T' (lower triangular: steps below 4 (w + 1))
+    f32x4m D = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks)
+      if (ks < 4 * (w + 1)) D = mfma_f32(tfr[ks >> 2][ks & 3], sR[(4 * ks + lg) * 16 + lr], D);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sD[(16 * w + 4 * lg + rr) * 16 + lr] = D[rr];
+    __syncthreads();
+    // outputs A (Q m_0) + P delta
+    f32x4m O = At * Y;
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks)
+      if (ks < 4 * (w + 1)) O = mfma_f32(pfr[ks >> 2][ks & 3], sD[(4 * ks + lg) * 16 + lr], O);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const size_t tt = t0 + 16 * w + 4 * lg + rr;
+      if (tt < a.n_tok) a.attn[(tt * a.h_v + h) * kFast + j] = O[rr] * a.scale;
+    }
+    // new state, column tiles 2w and 2w + 1: A_63 m_0 + (e K)^T delta
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+      if ((ib >> 1) == w) {
+        f32x4m acc = alast * M[ib];
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {
+          const int s = 4 * ks + lg;
+          acc = mfma_f32(sE[s] * sK[s * kCkKPitch + 16 * ib + lr], sD[s * 16 + lr], acc);
+        }
+        *reinterpret_cast<f32x4m *>(sM + lr * kCkMPitch + 16 * ib + 4 * lg) = acc;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib)
+      M[ib] = *reinterpret_cast<const f32x4m *>(sM + lr * kCkMPitch + 16 * ib + 4 * lg);
+  }
+#pragma unroll
+  for (int ib = 0; ib < 8; ++ib)
+    if ((ib >> 1) == w) *reinterpret_cast<f32x4m *>(mrow + 16 * ib + 4 * lg) = M[ib];
+}
+
 }  // namespace
 }  // namespace bh
 
@@ -453,7 +865,23 @@ extern "C" int bh_gdn_step(const float *q, const float *k, const float *v, const
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool fast =
       s == static_cast<size_t>(kFast) && aligned16(q) && aligned16(k) && aligned16(state);
-  if (fast) {
+  if (fast && n_tok >= kChunkMin && aligned16(v) && aligned16(attn)) {
+    const size_t n_chunks = (n_tok + kCk - 1) / kCk;
+    size_t bytes = 0;
+    if (n_chunks > 0x7fffffffu || !mul_size(n_chunks, h_v, kCkPer * sizeof(float), &bytes))
+      return fail(BH_ERR_SHAPE, "gdn_step: batch too long");
+    float *scr = static_cast<float *>(device_scratch(bytes, kScratchGdn, st));
+    if (scr == nullptr) return BH_ERR_HIP;
+    // one prep workgroup per (chunk, v-head) while (chunk, q/k head) would
+    // leave most CUs idle; each fills a CU (its LDS)
+    const size_t rep = (h_v + h_k - 1) / h_k;
+    const int per = n_chunks * h_k >= 2 * device_cu_count() ? 1 : static_cast<int>(rep);
+    GdnChunkArgs ca{q, k, v, gate, beta, state, attn, scr, n_tok, static_cast<int>(h_k),
+                    static_cast<int>(h_v), static_cast<int>(n_chunks), a.scale, a.xcd_map, per};
+    BH_LAUNCH(gdn_chunk_prep_kernel, static_cast<unsigned>(n_chunks * h_k * per), kBlock, 0, st,
+              ca);
+    BH_LAUNCH(gdn_chunk_walk_kernel, static_cast<unsigned>(h_v * (kFast / 16)), kBlock, 0, st, ca);
+  } else if (fast) {
     const unsigned grid = static_cast<unsigned>(h_v * s / kRowsPerBlock);
     if (n_tok <= kDirectMax)
       BH_LAUNCH(gdn_step128_direct_kernel, grid, kBlock, 0, st, a);

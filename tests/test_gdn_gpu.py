@@ -134,3 +134,74 @@ def test_gdn_step_graph_replay_advances_state(bh, oracle, synth, dev):
         assert rel_err(attn.cpu().numpy(), ref_attn) <= TOL, rep
         assert rel_err(dst.cpu().numpy(), cur) <= TOL, rep
 
+
+
+@pytest.mark.parametrize("n_tok,h_k,h_v", [
+    (64, 16, 48),    # one whole chunk of the chunked (matrix-core) path
+    (65, 16, 48),    # a chunk and one token
+    (200, 16, 48),   # a ragged last chunk
+    (2048, 16, 48),  # the prefill length of the metric: 32 chunks
+    (130, 2, 6),     # q/k heads not a multiple of 8 (no XCD placement)
+    (70, 3, 4),      # v-heads not a multiple of the q/k heads
+])
+def test_gdn_step_chunked(bh, oracle, synth, dev, n_tok, h_k, h_v):
+    _say("gdn_step chunked", n_tok, h_k, h_v)
+    case = gdn_case(synth, n_tok, h_k, h_v, 128, 300 + n_tok + h_v)
+    ref_attn, ref_st = oracle.gdn_step(*case)
+    attn, st = _run(bh, dev, case)
+    errs = rel_err(attn, ref_attn), rel_err(st, ref_st)
+    _say("  rel", errs)
+    assert max(errs) <= TOL
+
+
+def test_gdn_step_chunked_hard_inputs(bh, oracle, synth, dev):
+    """The chunked path where its triangular solve and decays are stressed:
+    keys of a head nearly identical, betas near 1, no decay on some heads, a
+    -inf gate (the state is cleared) and gates whose decay underflows."""
+    n_tok, h_k, h_v, s = 160, 16, 48, 128
+    q, k, v, gate, beta, st = gdn_case(synth, n_tok, h_k, h_v, s, 96)
+    r = synth.Rng(97)
+    base = r.normal(h_k * s).reshape(1, h_k, s)
+    k = base + np.float32(0.05) * r.normal(n_tok * h_k * s).reshape(n_tok, h_k, s)
+    k = (k / np.linalg.norm(k, axis=-1, keepdims=True)).astype(np.float32)
+    beta = (np.float32(0.99) + np.float32(0.01) * beta).astype(np.float32)
+    gate = gate.copy()
+    gate[:, :16] = 0.0
+    gate[5, 16:32] = -np.inf
+    gate[70:, 32:40] = -150.0
+    ref_attn, ref_st = oracle.gdn_step(q, k, v, gate, beta, st)
+    attn, got = _run(bh, dev, (q, k, v, gate, beta, st))
+    errs = rel_err(attn, ref_attn), rel_err(got, ref_st)
+    _say("  rel", errs)
+    assert max(errs) <= TOL
+
+
+def test_gdn_step_chunked_graph_replay(bh, oracle, synth, dev):
+    """The chunked path (prepared matrices in library scratch) captured in a
+    HIP graph after one eager call: each replay advances the state like an
+    eager call."""
+    import torch
+    n_tok, h_k, h_v, s = 128, 16, 48, 128
+    q, k, v, gate, beta, st = gdn_case(synth, n_tok, h_k, h_v, s, 98)
+    d = [_t(a, dev) for a in (q, k, v, gate, beta)]
+    dst = _t(st, dev)
+    attn = torch.empty_like(d[2])
+    strm = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(strm):
+        bh.gdn_step(*d, dst, attn=attn, stream=strm)  # sizes the scratch outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=strm):
+        bh.gdn_step(*d, dst, attn=attn, stream=strm)
+    torch.cuda.synchronize()
+    dst.copy_(_t(st, dev))
+    cur = st
+    for rep in range(3):
+        torch.cuda.synchronize()
+        with torch.cuda.stream(strm):
+            g.replay()
+        torch.cuda.synchronize()
+        ref_attn, cur = oracle.gdn_step(q, k, v, gate, beta, cur)
+        assert rel_err(attn.cpu().numpy(), ref_attn) <= TOL, rep
+        assert rel_err(dst.cpu().numpy(), cur) <= TOL, rep
