@@ -33,7 +33,7 @@
  * ids per compute unit (4096 on MI355X; it keeps the row scales there), and
  * the PQ2_0 products (bh_pq2_matvec_range, bh_pq2_matmul_n) with more than 4
  * tokens or on shapes outside the integer path, and bh_gdn_step on batches
- * of 64 or more tokens at s = 128, which use per-device scratch buffers:
+ * of 128 or more tokens at s = 128, which use per-device scratch buffers:
  * each must not run concurrently with itself on one device.
  *
  * Scratch and HIP graphs: a scratch buffer grows (allocates) the first time
@@ -258,7 +258,7 @@ int bh_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *
  * beta[t][h]; M[j] += k * delta[j]; attn[t][h][j] = (M[j].q) / sqrtf(s).
  * q, k: [n_tok][h_k][s]; v, attn: [n_tok][h_v][s]; gate, beta: [n_tok][h_v];
  * state: [h_v][s][s], updated in place.  n_tok = 0 is a no-op.  With s = 128
- * and 64 or more tokens the batch runs in 64-token chunks on matrix cores
+ * and 128 or more tokens the batch runs in 64-token chunks on matrix cores
  * and uses library scratch (about 33 KB per chunk and v-head); fewer tokens
  * use none. */
 int bh_gdn_step(const float *q, const float *k, const float *v, const float *gate,

@@ -3,8 +3,9 @@ oracle's restatement of src/gdn.rs:17-77 applied token by token.
 
 Bar: max|gpu-ref| / max(|ref|, |gpu|) <= 1e-5 for attn and for the advanced
 state.  The device sums each 128-long dot as 8 in-lane products and a fixed
-16-lane tree where the reference adds in index order, so the two differ by
-rounding only.
+16-lane tree where the reference adds in index order, and batches of 128 or
+more tokens take the recurrence's closed form per 64-token chunk (a
+triangular solve and matrix products), so the two differ by rounding only.
 """
 from __future__ import annotations
 
@@ -137,12 +138,12 @@ def test_gdn_step_graph_replay_advances_state(bh, oracle, synth, dev):
 
 
 @pytest.mark.parametrize("n_tok,h_k,h_v", [
-    (64, 16, 48),    # one whole chunk of the chunked (matrix-core) path
-    (65, 16, 48),    # a chunk and one token
+    (128, 16, 48),   # the shortest batch of the chunked (matrix-core) path: 2 chunks
+    (129, 16, 48),   # two chunks and one token
     (200, 16, 48),   # a ragged last chunk
     (2048, 16, 48),  # the prefill length of the metric: 32 chunks
     (130, 2, 6),     # q/k heads not a multiple of 8 (no XCD placement)
-    (70, 3, 4),      # v-heads not a multiple of the q/k heads
+    (150, 3, 4),     # v-heads not a multiple of the q/k heads
 ])
 def test_gdn_step_chunked(bh, oracle, synth, dev, n_tok, h_k, h_v):
     _say("gdn_step chunked", n_tok, h_k, h_v)
