@@ -478,7 +478,7 @@ constexpr int kCkMPitch = 132;                  // walk: staged state rows
 // 100 against 139)
 constexpr size_t kChunkMin = 128;
 constexpr float kGateFloor = -200.0f;           // expf below this is 0 in f32
-static_assert(kCk * kCkBuf <= 2 * kCk * kCkPitch, "L fits the staging area");
+static_assert(3 * kCk * kCkBuf <= 2 * kCk * kCkPitch, "K K^T, Q K^T and L fit the staging area");
 
 typedef float f32x4m __attribute__((ext_vector_type(4)));
 
@@ -511,8 +511,9 @@ __device__ __forceinline__ float *tblock(float *buf, int bi, int bj) {
 
 // Tiles k = w + 4 u (u < N) of the lower triangle of K K^T and Q K^T (tile
 // k: row tile ti, column tile nt <= ti), accumulated over the 128 dims and
-// written to LDS at pitch kCkBuf.  N is a template parameter so the
-// accumulators stay in registers across the loop (no per-step branches).
+// written to LDS at pitch kCkBuf once every wave has read the staged rows
+// (one block barrier).  N is a template parameter so the accumulators stay
+// in registers across the loop (no per-step branches).
 template <int N>
 __device__ __forceinline__ void prep_qk_tiles(const float *sK, const float *sQ, float *sKK,
                                               float *sQK, int w, int lr, int lg) {
@@ -536,6 +537,7 @@ __device__ __forceinline__ void prep_qk_tiles(const float *sK, const float *sQ, 
       accQ[u] = mfma_f32(sQ[ra[u] + 4 * ks], b, accQ[u]);
     }
   }
+  __syncthreads();  // sKK and sQK overlay the staged K and Q
 #pragma unroll
   for (int u = 0; u < N; ++u)
 #pragma unroll
@@ -552,13 +554,13 @@ __device__ __forceinline__ void prep_qk_tiles(const float *sK, const float *sQ, 
 // and L (lane (lr, lg): row 16 w + lr, columns 16 lg .. 16 lg + 15),
 // inverts diagonal block w, takes pair w of each distance of the
 // off-diagonal blocks and stores row tile w of T'.  Its LDS (K, Q, K K^T,
-// Q K^T) allows one workgroup per CU, so registers are scheduled for one
-// wave per SIMD.
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, 1))) void
+// Q K^T, L, all in the 67 KB that first holds the staged K and Q) lets two
+// workgroups share a CU.
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 gdn_chunk_prep_kernel(GdnChunkArgs a) {
-  __shared__ __attribute__((aligned(16))) float sStage[2 * kCk * kCkPitch];  // K, Q; then L and the inverse
-  __shared__ float sKK[kCk * kCkBuf];  // pitch 65: lane t reading row t hits bank t + s
-  __shared__ float sQK[kCk * kCkBuf];
+  // K, Q (pitch kCkPitch); then K K^T, Q K^T and L / the inverse (pitch 65:
+  // lane t reading row t hits bank t + s)
+  __shared__ __attribute__((aligned(16))) float sStage[2 * kCk * kCkPitch];
   __shared__ double sG[kCk];
   __shared__ float sB[kCk];
   __shared__ float sS[4][16 * 17];  // per-wave block products in transit
@@ -569,6 +571,7 @@ gdn_chunk_prep_kernel(GdnChunkArgs a) {
   const int l = threadIdx.x & 63, lr = l & 15, lg = l >> 4;
   const size_t t0 = static_cast<size_t>(c) * kCk;
   float *sK = sStage, *sQ = sStage + kCk * kCkPitch;
+  float *sKK = sStage, *sQK = sStage + kCk * kCkBuf;
   // stage the chunk's k and q rows of this head (zeros past the batch)
 #pragma unroll
   for (int i = 0; i < kCk * 32 / kBlock; ++i) {
@@ -590,7 +593,7 @@ gdn_chunk_prep_kernel(GdnChunkArgs a) {
   else
     prep_qk_tiles<2>(sK, sQ, sKK, sQK, w, lr, lg);
   __syncthreads();
-  float *buf = sStage;  // 64 x 64 at pitch kCkBuf: L, then the inverse
+  float *buf = sStage + 2 * kCk * kCkBuf;  // 64 x 64 at pitch kCkBuf: L, then the inverse
   const int n_vh = (a.h_v - kh + a.h_k - 1) / a.h_k;  // v-heads h = kh + n h_k
   const int t = 16 * w + lr;                            // this lane's row of P and L
   for (int n = part; n < n_vh; n += per) {              // the same count in every wave
