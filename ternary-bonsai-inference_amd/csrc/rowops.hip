@@ -644,16 +644,14 @@ int rms_rows_impl(const float *x, const float *r, const float *w, float *sum_out
   // 5120-wide rows, 2048..4095 of them: one wave per row (20 float4 per lane,
   // four rows per 256-lane block) measured 8-10% faster than the 640-lane
   // block-per-row form (T=2048: 15.1 vs 16.6 us, T=3072: 22.1 vs 24.1 us);
-  // below and above that range the block form is as fast or faster.
-  if (vec && row_len == 5120 && rows >= 2048 && rows < 4096) {
+  // below and above that range the block form is as fast or faster.  The
+  // residual-add form stays on the block form: with two inputs per lane it
+  // needs more than the 128 registers per lane the kernel's 1024-lane bound
+  // allows, and spilled.
+  if (vec && !add && row_len == 5120 && rows >= 2048 && rows < 4096) {
     const unsigned grid = static_cast<unsigned>((rows + 3) / 4);
-    if (add) {
-      BH_LAUNCH((rms_rows_kernel<64, 20, true>), grid, 256, 0, st, x, r, w, sum_out, out, rows,
-                5120, eps);
-    } else {
-      BH_LAUNCH((rms_rows_kernel<64, 20, false>), grid, 256, 0, st, x, r, w, sum_out, out, rows,
-                5120, eps);
-    }
+    BH_LAUNCH((rms_rows_kernel<64, 20, false>), grid, 256, 0, st, x, r, w, sum_out, out, rows,
+              5120, eps);
     return ok();
   }
   if (vec) {
