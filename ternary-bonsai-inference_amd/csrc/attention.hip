@@ -929,6 +929,7 @@ constexpr int kMqTile = 32;     // positions per tile
 constexpr int kKStride = 264;   // halves per staged K row (256 + 8: no bank conflicts)
 constexpr int kVStride = 40;    // halves per staged V^T row (32 + 8)
 constexpr int kMqMinRows = 48;  // q rows per kv head from which this path is taken
+constexpr size_t kMqPreTiles = 8;  // row tiles per kv head from which an f32 cache is pre-split
 
 struct MqArgs {
   const float *q;
@@ -944,6 +945,13 @@ struct MqArgs {
   // of a single chunk computes; only an exact zero's sign can differ)
   // instead of as partials; nullptr otherwise
   float *out;
+  // f32 cache pre-split by attn_kv_split_kernel (PRE): K as f16 hi / lo
+  // halves in the cache's layout with its per-position factors 2^-b; V per
+  // (32-position tile, kv head) as [dim][32 halves in vcol order], hi then
+  // lo, with the tile's shift; unused otherwise
+  const uint16_t *kh, *kl, *vh;
+  const float *ks;
+  const int *vsh;
 };
 
 // 2^e as a float for e <= 127; 0 below the normal range
@@ -982,11 +990,12 @@ __device__ __forceinline__ int vcol(int p) { return p < 16 ? 8 * (p >> 2) + (p &
 // q is rotated as it is split, each score takes K's row norm with the
 // position's scale (src/forward.rs:307), and the sums stay in rotated space
 // for attn_merge_rows_rot_kernel to turn back.  The rest is the f32 path.
-template <bool F16, int PB, bool VQ>
+template <bool F16, int PB, bool VQ, bool PRE = false>
 __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, const float *gc,
                                         const float *gs) {
   constexpr bool PL = PB > 0;
   static_assert(!(PL && F16), "planar caches take the f32 staging");
+  static_assert(!(PRE && (PL || F16)), "the pre-split form is for the f32 cache");
   __shared__ __attribute__((aligned(16))) _Float16 sKh[kMqTile * kKStride];
   __shared__ __attribute__((aligned(16))) _Float16 sKl[F16 ? 8 : kMqTile * kKStride];
   __shared__ __attribute__((aligned(16))) _Float16 sVh[kHd * kVStride];
@@ -1142,12 +1151,33 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
   constexpr bool kVTwo = PL && 8 % PB != 0;
   uint32_t kw[kKWords];
   float knr = 0.0f;
+  // pre-split f32 cache: K row sp's 16 hi then 16 lo halves, its factor, the
+  // V halves of the lane's positions and dims, the tile's V shift
+  // (ext_vector_type arrays: HIP's uint4 struct arrays carried across the
+  // tile loop are kept in scratch memory)
+  u32x4v kph[PRE ? 4 : 1];
+  u32x4v vpq[PRE ? 4 : 1];  // 16-byte pieces tid, tid + 512 of the tile's V hi, then of its lo
+  float ksr = 0.0f;
+  int vsr = 0, cur_vst = 0;
   uint32_t vlo[PL && VQ ? 4 : 1][PL && VQ ? 4 : 1], vhi[kVTwo && VQ ? 4 : 1][kVTwo && VQ ? 4 : 1];
   float vnr[PL && VQ ? 4 : 1];
   auto fetch = [&](size_t t0) {
     const int nt = static_cast<int>(end - t0 < kMqTile ? end - t0 : kMqTile);
     const size_t krow = (t0 + (sp < nt ? sp : nt - 1)) * a.kv_stride + head_off + 16 * kpart;
     const VElt *vcp = static_cast<const VElt *>(a.vc);
+    if constexpr (PRE) {
+      kph[0] = *reinterpret_cast<const u32x4v *>(a.kh + krow);
+      kph[1] = *reinterpret_cast<const u32x4v *>(a.kh + krow + 8);
+      kph[2] = *reinterpret_cast<const u32x4v *>(a.kl + krow);
+      kph[3] = *reinterpret_cast<const u32x4v *>(a.kl + krow + 8);
+      ksr = a.ks[(t0 + (sp < nt ? sp : nt - 1)) * a.n_kv + g];
+      const size_t vt = ((t0 / kMqTile) * a.n_kv + g) * (2 * kHd * kMqTile);
+      const u32x4v *vsrc = reinterpret_cast<const u32x4v *>(a.vh + vt);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vpq[r] = vsrc[tid + kMqThreads * r];
+      vsr = a.vsh[(t0 / kMqTile) * a.n_kv + g];
+      return;
+    }
     if constexpr (PL) {
       const size_t prow = (t0 + (sp < nt ? sp : nt - 1)) * a.n_kv + g;
       const uint8_t *src = static_cast<const uint8_t *>(a.kc) + prow * kPlen + 2 * PB * kpart;
@@ -1199,7 +1229,24 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
   for (size_t t0 = beg; t0 < end; t0 += kMqTile) {
     const int nt = static_cast<int>(end - t0 < kMqTile ? end - t0 : kMqTile);
     const int vc0 = vcol(4 * vpg);  // the 4 columns of this lane's positions
-    if constexpr (F16) {
+    if constexpr (PRE) {
+      u32x4v *kd = reinterpret_cast<u32x4v *>(sKh + sp * kKStride + 16 * kpart);
+      kd[0] = kph[0];
+      kd[1] = kph[1];
+      u32x4v *kld = reinterpret_cast<u32x4v *>(sKl + sp * kKStride + 16 * kpart);
+      kld[0] = kph[2];
+      kld[1] = kph[3];
+      if (kpart == 0) sKs[sp] = ksr;
+      // piece u of an array: dim u / 4, columns 8 (u % 4) .. +7
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int u = (tid + kMqThreads * r) & (4 * kHd - 1);
+        _Float16 *dst = (r < 2 ? sVh : sVl) + (u >> 2) * kVStride + 8 * (u & 3);
+        *reinterpret_cast<u32x4v *>(dst) = vpq[r];
+      }
+      cur_vst = vsr;  // the prefetch below overwrites vsr
+      __syncthreads();
+    } else if constexpr (F16) {
       const uint4 k0 = kr[0], k1 = kr[1];
       uint4 *kd = reinterpret_cast<uint4 *>(sKh + sp * kKStride + 16 * kpart);
       kd[0] = k0;
@@ -1288,7 +1335,11 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
     }
     if (t0 + kMqTile < end) fetch(t0 + kMqTile);  // the next tile, in flight during this one
     int vs = vs_cur;
-    if constexpr (!F16) {
+    float pfac = 1.0f;  // PRE: the tile's V is in units of 2^vst, the block's of 2^vs
+    if constexpr (PRE) {
+      vs = cur_vst > vs_cur ? cur_vst : vs_cur;
+      pfac = pow2f(cur_vst - vs);
+    } else if constexpr (!F16) {
       const int vst = v_shift(__uint_as_float(sVmax[parity]));
       vs = vst > vs_cur ? vst : vs_cur;
       // the other slot was last read before the previous tile's final
@@ -1343,7 +1394,7 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
       const float p = exp_hw(none ? -INFINITY : sc[k] - m_new);
       psum += p;
       _Float16 h, lo;
-      split_hl(p * 16384.0f, h, lo);
+      split_hl(p * (PRE ? 16384.0f * pfac : 16384.0f), h, lo);
       ph[k] = h;
       pl[k] = lo;
     }
@@ -1396,6 +1447,102 @@ __device__ __forceinline__ void mq_body(const MqArgs &a, const float *cent, cons
 template <bool F16>
 __global__ __launch_bounds__(kMqThreads) void attn_mq_kernel(MqArgs a) {
   mq_body<F16, 0, false>(a, nullptr, nullptr, nullptr);
+}
+
+// The f32 path over a pre-split cache (see attn_kv_split_kernel).
+__global__ __launch_bounds__(kMqThreads) void attn_mq_pre_kernel(MqArgs a) {
+  mq_body<false, 0, false, true>(a, nullptr, nullptr, nullptr);
+}
+
+// Splits the f32 cache once for a multi-query call whose blocks would each
+// split the same K / V tiles again: block (tile, g) takes positions 32 tile
+// .. 32 tile + 31 of kv head g.  Each K row is scaled so its largest |k| lies
+// in [2^13, 2^14) (factor 2^-b kept per position) and each 32-position V
+// tile by its own shift vst (its largest |v| into [2^13, 2^14)); both are
+// split into f16 hi = f16(x') and lo = f16(x' - hi), stored in the caches'
+// layout (V per tile in the order the block stages it: [dim][32 halves at
+// columns vcol(p)], hi rows then lo rows).  These are the scales and splits
+// the f32 staging of mq_body forms
+// per tile (the block then multiplies P by 2^(vst - vs) for its running V
+// unit vs instead of rescaling V).
+__global__ __launch_bounds__(256) void attn_kv_split_kernel(const float *kc, const float *vc,
+                                                            size_t n_pos, size_t kv_stride, int n_kv,
+                                                            uint16_t *kh, uint16_t *kl, float *ks,
+                                                            uint16_t *vt, int *vsh) {
+  __shared__ float sm[4];
+  const int tile = static_cast<int>(blockIdx.x) / n_kv, g = static_cast<int>(blockIdx.x) % n_kv;
+  const size_t p0 = static_cast<size_t>(tile) * kMqTile, head_off = static_cast<size_t>(g) * kHd;
+  const int tid = threadIdx.x, sp = tid >> 4, kpart = tid & 15;
+#pragma unroll
+  for (int pass = 0; pass < kMqTile / 16; ++pass) {
+    const size_t p = p0 + 16 * pass + sp;
+    const bool ok = p < n_pos;
+    const size_t off = p * kv_stride + head_off + 16 * kpart;
+    f32x4 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      x[k] = ok ? *reinterpret_cast<const f32x4 *>(kc + off + 4 * k) : f32x4{0.f, 0.f, 0.f, 0.f};
+    float km = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      km = fmaxf(km, fmaxf(fmaxf(fabsf(x[k].x), fabsf(x[k].y)), fmaxf(fabsf(x[k].z), fabsf(x[k].w))));
+    km = lane_group_reduce<16>(km, FMaxOp{});
+    const int kb = split_shift(km);
+    const float kf = ldexpf(1.0f, kb);
+    if (ok) {
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        half8 hv, lv;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const f32x4 y = x[2 * k2 + k];
+          _Float16 h, lo;
+          split_hl(y.x * kf, h, lo); hv[4 * k + 0] = h; lv[4 * k + 0] = lo;
+          split_hl(y.y * kf, h, lo); hv[4 * k + 1] = h; lv[4 * k + 1] = lo;
+          split_hl(y.z * kf, h, lo); hv[4 * k + 2] = h; lv[4 * k + 2] = lo;
+          split_hl(y.w * kf, h, lo); hv[4 * k + 3] = h; lv[4 * k + 3] = lo;
+        }
+        *reinterpret_cast<half8 *>(kh + off + 8 * k2) = hv;
+        *reinterpret_cast<half8 *>(kl + off + 8 * k2) = lv;
+      }
+      if (kpart == 0) ks[p * n_kv + g] = ldexpf(1.0f, -kb);
+    }
+  }
+  // V: dim tid of the tile's positions (past the cache's end, copies of
+  // its last row: finite values the kernel masks)
+  float v[kMqTile];
+  float vm = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kMqTile; ++i) {
+    const size_t p = p0 + i < n_pos ? p0 + i : n_pos - 1;
+    v[i] = vc[p * kv_stride + head_off + tid];
+    vm = fmaxf(vm, fabsf(v[i]));
+  }
+  vm = wave_max(vm);
+  if ((tid & 63) == 0) sm[tid >> 6] = vm;
+  __syncthreads();
+  vm = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
+  const int vst = v_shift(vm);
+  if (tid == 0) vsh[tile * n_kv + g] = vst;
+  const float vf = ldexpf(1.0f, -vst);
+  // the row of dim tid in the staged order (position p at column vcol(p)),
+  // hi then lo, 64 contiguous bytes each
+  half8 hrow[4], lrow[4];
+#pragma unroll
+  for (int i = 0; i < kMqTile; ++i) {
+    _Float16 h, lo;
+    split_hl(v[i] * vf, h, lo);
+    const int col = vcol(i);
+    hrow[col >> 3][col & 7] = h;
+    lrow[col >> 3][col & 7] = lo;
+  }
+  half8 *dh = reinterpret_cast<half8 *>(vt + ((static_cast<size_t>(tile) * n_kv + g) * 2 * kHd + tid) * kMqTile);
+  half8 *dl = reinterpret_cast<half8 *>(vt + ((static_cast<size_t>(tile) * n_kv + g) * 2 * kHd + kHd + tid) * kMqTile);
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) {
+    dh[c4] = hrow[c4];
+    dl[c4] = lrow[c4];
+  }
 }
 
 template <int PB, bool VQ>
@@ -1897,7 +2044,33 @@ extern "C" int bh_attention(const float *q, size_t n_q, size_t pos0, const void 
     const size_t nb = n_chunks * n_kv * tiles_r;
     if (nb > 0x7fffffffu) return fail(BH_ERR_SHAPE, "attention: too many blocks");
     const dim3 grid(static_cast<unsigned>(nb));
-    if (f16)
+    // an f32 cache read by many row tiles per kv head (a prefill) is split
+    // into f16 hi / lo once instead of in every block
+    const bool pre = !f16 && tiles_r >= kMqPreTiles;
+    if (pre) {
+      const size_t n_tiles = (n_max + kMqTile - 1) / kMqTile;
+      const size_t halves = n_max * kv_stride;  // per array
+      const size_t kh_b = (halves * 2 + 255) / 256 * 256;
+      const size_t ks_b = (n_max * n_kv * 4 + 255) / 256 * 256;
+      const size_t vt_b = n_tiles * n_kv * 2 * kHd * kMqTile * 2;  // whole tiles (rows past the end padded)
+      const size_t total = 2 * kh_b + vt_b + ks_b + n_tiles * n_kv * 4;
+      uint8_t *base = static_cast<uint8_t *>(device_scratch(total, kScratchKvSplit, st));
+      if (base == nullptr) return BH_ERR_HIP;
+      uint16_t *kh = reinterpret_cast<uint16_t *>(base);
+      uint16_t *kl = reinterpret_cast<uint16_t *>(base + kh_b);
+      uint16_t *vt = reinterpret_cast<uint16_t *>(base + 2 * kh_b);
+      float *ks = reinterpret_cast<float *>(base + 2 * kh_b + vt_b);
+      int *vsh = reinterpret_cast<int *>(base + 2 * kh_b + vt_b + ks_b);
+      BH_LAUNCH(attn_kv_split_kernel, static_cast<unsigned>(n_tiles * n_kv), 256, 0, st,
+                static_cast<const float *>(k_cache), static_cast<const float *>(v_cache), n_max,
+                kv_stride, static_cast<int>(n_kv), kh, kl, ks, vt, vsh);
+      m.kh = kh;
+      m.kl = kl;
+      m.vh = vt;
+      m.ks = ks;
+      m.vsh = vsh;
+      BH_LAUNCH(attn_mq_pre_kernel, grid, kMqThreads, 0, st, m);
+    } else if (f16)
       BH_LAUNCH(attn_mq_kernel<true>, grid, kMqThreads, 0, st, m);
     else
       BH_LAUNCH(attn_mq_kernel<false>, grid, kMqThreads, 0, st, m);

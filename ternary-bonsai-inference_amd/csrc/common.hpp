@@ -55,7 +55,8 @@ constexpr int kScratchMatmul = 1;   // PQ2_0 product: f16 x fragments, token sca
 constexpr int kScratchAttention = 2;  // attention: chunk partials or probabilities
 constexpr int kScratchGather = 3;     // gather + RMSNorm: the row scales
 constexpr int kScratchGdn = 4;        // gated delta-net chunks: prepared matrices
-constexpr int kScratchSlots = 5;
+constexpr int kScratchKvSplit = 5;    // attention: f32 cache split into f16 hi / lo
+constexpr int kScratchSlots = 6;
 void *device_scratch(size_t bytes, int slot, hipStream_t stream);
 // Current size of this device's buffer for `slot` (0 before the first use).
 size_t scratch_bytes(int slot);

@@ -174,6 +174,10 @@ def test_store_then_attend_token_loop(bh, oracle, synth, dev):
     (16, 500, False, 24, 4, 3e6, 1e-3),    # large v (scaled-down tiles), small q
     (16, 500, False, 24, 4, 1e-6, 10.0),   # tiny v, peaked attention (logits ~ N(0, 10^2))
     (33, 2000, True, 12, 4, 1.0, 0.05),    # f16 cache, near-flat attention
+    # 8+ row tiles per kv head: the f32 cache is split into f16 hi / lo once
+    (200, 37, False, 24, 4, 1.0, 2.0),     # ragged row and position tiles
+    (176, 500, False, 24, 4, 3e6, 1e-3),   # large v, small q
+    (176, 500, False, 24, 4, 1e-6, 10.0),  # tiny v, peaked attention
 ])
 def test_attention_multi_query_matrix_cores(bh, oracle, synth, dev, n_q, pos0, f16, n_head, n_kv,
                                             vscale, qscale):
@@ -222,3 +226,22 @@ def test_attention_prefill_2048_from_position_0(bh, oracle, synth, dev, f16):
         worst = max(worst, rel_err(got[i:i + 1], ref))
     _say("  rel (sampled rows)", worst)
     assert worst <= TOL
+
+
+def test_attention_presplit_tile_scales(bh, oracle, synth, dev):
+    """The pre-split f32 path (8+ row tiles per kv head) with V tiles whose
+    magnitudes differ by up to 2^48 along the positions: each 32-position
+    tile keeps its own power-of-two unit, and a block whose running unit
+    has grown scales the tile's probabilities down instead.  <= 1e-5
+    against the oracle's per-token loop."""
+    n_head, n_kv, hd = MODEL
+    n_q, pos0 = 192, 300
+    q, kc, vc = _case(synth, n_q, pos0, n_head, n_kv, hd, 977)
+    n = pos0 + n_q
+    expo = np.round(24.0 * np.sin(np.arange(n) / 37.0)).astype(np.float32)
+    vc = (vc * np.exp2(expo)[:, None]).astype(np.float32)
+    ref = oracle.attention(q, pos0, kc, vc, n_kv)
+    got = _run(bh, dev, q, pos0, kc, vc, n_kv)
+    err = rel_err(got, ref)
+    _say("  rel", err)
+    assert err <= TOL
