@@ -23,6 +23,12 @@
 // the reference's up to rounding (sums in another order); a non-finite v at
 // a position whose probability underflows to 0 is not skipped here.
 //
+// Many queries per kv head (prefill, verification; hd = 256): the
+// matrix-core path (mq_body: f16 hi / lo products with power-of-two
+// scaling, one block per (position chunk, 128-row tile, kv head)); over an
+// f32 cache read by 8 or more row tiles per kv head the cache is first
+// split into f16 hi / lo once (attn_kv_split_kernel) instead of per block.
+//
 // Generic path (any hd and grouping, any alignment): one block per (query,
 // head) computes the scores, the reference's softmax (f32 max, expf, f64
 // sum, inv = 1 / (f32)sum, p = e * inv) into scratch; a second launch forms

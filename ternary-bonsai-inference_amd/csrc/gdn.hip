@@ -19,6 +19,9 @@
 // The reference sums the 128 products of a dot in index order; the tree
 // order and the regrouping differ by rounding only (outputs and state within
 // 1e-5 of the reference's scale).
+// Batches of kChunkMin tokens or more take the recurrence's closed form per
+// 64-token chunk on f32 matrix cores instead (gdn_chunk_prep_kernel, then
+// gdn_chunk_walk_kernel; the algebra is written out above them).
 #include <hip/hip_runtime.h>
 
 #include <string>
