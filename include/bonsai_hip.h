@@ -260,7 +260,10 @@ int bh_attention_planar(const float *q, size_t n_q, size_t pos0, const uint8_t *
  * state: [h_v][s][s], updated in place.  n_tok = 0 is a no-op.  With s = 128
  * and 128 or more tokens the batch runs in 64-token chunks on matrix cores
  * and uses library scratch (about 33 KB per chunk and v-head); fewer tokens
- * use none. */
+ * use none.  In that chunked form a non-finite q, k or v at token t also
+ * makes the outputs of the chunk's earlier tokens non-finite (the chunk's
+ * products include it with weight 0, and 0 x inf is NaN), where the
+ * per-token reference leaves them finite; finite inputs are unaffected. */
 int bh_gdn_step(const float *q, const float *k, const float *v, const float *gate,
                 const float *beta, float *state, float *attn, size_t n_tok, size_t h_k,
                 size_t h_v, size_t s, bh_stream stream);
