@@ -457,13 +457,14 @@ __global__ __launch_bounds__(kBlock) void gdn_step_generic_kernel(GdnStepArgs a)
 // independent to nearly identical, betas up to 1 and decays from none to
 // underflow.
 //
-// gdn_chunk_prep_kernel (one workgroup per (chunk, q/k head), all chunks in
-// parallel) forms K K^T and Q K^T on v_mfma_f32_16x16x4_f32, then, one wave
-// per v-head of that q/k head, the decays (prefix sums of the gates in f64,
-// so a large early gate costs no precision in later differences), L, its
-// inverse (16 x 16 diagonal blocks by forward substitution, a lane per
-// column, the other blocks by f32 MFMA products), T' and P, stored in
-// the order the walk's MFMA A operands read them.  gdn_chunk_walk_kernel
+// gdn_chunk_prep_kernel (all chunks in parallel; a workgroup per (chunk,
+// q/k head), or per (chunk, v-head) for short batches) forms K K^T and
+// Q K^T on v_mfma_f32_16x16x4_f32, then for each v-head, its four waves
+// sharing the work: the decays (prefix sums of the gates in f64, so a large
+// early gate costs no precision in later differences), P and L, the inverse
+// (16 x 16 diagonal blocks by forward substitution, a lane per column; the
+// other blocks by f32 MFMA products) and T', stored in the order the walk's
+// MFMA A operands read them.  gdn_chunk_walk_kernel
 // (one workgroup per (v-head, 16 state rows)) keeps its rows' state in
 // registers as MFMA operands and walks the chunks in order: K m_0 and Q m_0
 // (wave w: tokens 16w..16w+15), delta through T' (LDS exchange of the
@@ -505,7 +506,7 @@ __device__ __forceinline__ f32x4m mfma_f32(float a, float b, f32x4m c) {
 // sits at ((wt * 64 + l) * 16 + ks), so each lane of the walk reads its 16
 // values of a tile as four 16-byte loads.
 
-// Block (bi, bj), bi >= bj, of the inverse in a per-wave 64 x 64 buffer:
+// Block (bi, bj), bi >= bj, of the inverse in the 64 x 64 buffer of L:
 // diagonal blocks in place, T_ij (i > j) in the upper block (j, i), which L
 // leaves free.
 __device__ __forceinline__ float *tblock(float *buf, int bi, int bj) {
@@ -515,7 +516,8 @@ __device__ __forceinline__ float *tblock(float *buf, int bi, int bj) {
 // Tiles k = w + 4 u (u < N) of the lower triangle of K K^T and Q K^T (tile
 // k: row tile ti, column tile nt <= ti), accumulated over the 128 dims and
 // written to LDS at pitch kCkBuf once every wave has read the staged rows
-// (one block barrier).  N is a template parameter so the accumulators stay
+// (one block barrier: every wave runs exactly one instantiation, so each
+// arrives at it once).  N is a template parameter so the accumulators stay
 // in registers across the loop (no per-step branches).
 template <int N>
 __device__ __forceinline__ void prep_qk_tiles(const float *sK, const float *sQ, float *sKK,
